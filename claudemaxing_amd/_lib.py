@@ -1,0 +1,103 @@
+"""ctypes binding of the gfx950 kernel library (include/claudemaxing_amd.h).
+
+The library is loaded on first use, after torch (so it shares torch's HIP runtime and its
+streams). A missing or mismatched library raises ImportError; a non-zero return code of an
+entry point raises RuntimeError with the library's error string. There is no other code path:
+the kernels either run on the GPU or the call fails.
+"""
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
+ABI_VERSION = 1
+
+F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
+_DTYPE_CODES = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.uint8: U8,
+    torch.bool: U8,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+
+_P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/claudemaxing_amd.h
+SIGNATURES = {
+    "cm_abi_version": (_I, []),
+    "cm_error_string": (ctypes.c_char_p, [_I]),
+    "cm_nf4_dequant": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P]),
+    "cm_rmsnorm_fwd": (_I, [_P, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P, _I, _L, _I, _F, _P]),
+    "cm_rmsnorm_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _L, _I, _P]),
+    "cm_rmsnorm_bwd_partials": (_L, [_L]),
+    "cm_rope": (_I, [_P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _I, _P, _I, _P, _P, _I,
+                     _L, _L, _I, _I, _I, _I, _P]),
+    "cm_swiglu_fwd": (_I, [_P, _I, _P, _I, _P, _I, _L, _I, _P]),
+    "cm_swiglu_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _L, _I, _I, _I, _P]),
+    "cm_lora_pack": (_I, [_P, _I, _P, _P, _P, _L, _F, _P]),
+    "cm_lora_unpack": (_I, [_P, _P, _P, _P, _P, _I, _L, _F, _P]),
+    "cm_xent_rows": (_I, [_P, _I, _L, _P, _P, _P, _P, _L, _L, _I, _F, _P]),
+    "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L, _P]),
+    "cm_lmhead_ce_workspace_bytes": (_L, [_L, _L, _I, _L]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """The loaded library (ctypes.CDLL); ImportError if it is missing or its ABI differs."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build the gfx950 kernel library first "
+                "(python -m claudemaxing_amd.build_lib)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                raise ImportError(f"{LIB_PATH} does not export {name}")
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.cm_abi_version()
+        if version != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Call entry point `name`; raise RuntimeError with the library's message on failure."""
+    lib = load()
+    code = getattr(lib, name)(*args)
+    if code != 0:
+        msg = lib.cm_error_string(code).decode()
+        raise RuntimeError(f"{name} failed: {msg} (code {code})")
+
+
+def dtype_code(dtype):
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+def ptr(t):
+    """Device address of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream(device=None):
+    """Handle of torch's current stream on `device`, for the stream argument."""
+    return torch.cuda.current_stream(device).cuda_stream

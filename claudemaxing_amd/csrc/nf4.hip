@@ -1,0 +1,205 @@
+// NF4 dequantization with the nested absmax decoded in the same pass (gfx950).
+//
+// Reproduces solution/nf4.py:26-46 (nf4_dequant_kernel) bit for bit. Layout: byte i of the
+// packed weight holds element 2i in its high nibble and 2i+1 in its low nibble; element j
+// belongs to absmax block j / blocksize. With double quantization the block scale is
+// code2[absmax8[b]] * absmax2[b / blocksize2] + offset, an fp32 multiply followed by an fp32
+// add (nf4.py:37-38, compiled there with fp fusion off). Each output is the fp32 product
+// code[nibble] * scale rounded to nearest even in the output type.
+//
+// Work split: a lane handles 4-byte units (8 outputs, one 16-byte fp16 store), all 8 in one
+// absmax block because blocksize >= 32. A workgroup of 256 lanes handles UNITS consecutive
+// 1 KiB slices of the packed weight, so every load and store instruction of a wavefront covers
+// one contiguous span (256 B in, 1 KiB out for fp16). The 16-entry code table sits in LDS:
+// the 16 entries fall in 16 distinct banks, so the per-lane lookups never conflict.
+#include "common.h"
+
+namespace {
+
+// No contraction anywhere in this file's arithmetic: the scale is a multiply then an add.
+#pragma clang fp contract(off)
+
+constexpr int kThreads = 256;
+constexpr int kUnits = 4;  // 4-byte units per lane
+
+template <bool NESTED>
+__device__ __forceinline__ float block_scale(const void* absmax, const float* code2,
+                                             const float* absmax2, float offset, uint32_t blk,
+                                             int bs2_shift, uint32_t bs2) {
+  if constexpr (NESTED) {
+    const uint8_t q8 = static_cast<const uint8_t*>(absmax)[blk];
+    const uint32_t blk2 = bs2_shift >= 0 ? (blk >> bs2_shift) : (blk / bs2);
+    const float prod = code2[q8] * absmax2[blk2];
+    return prod + offset;
+  } else {
+    return static_cast<const float*>(absmax)[blk];
+  }
+}
+
+template <typename OutT>
+struct Pack8;
+
+template <>
+struct Pack8<_Float16> {
+  static __device__ __forceinline__ void store(_Float16* out, const float (&v)[8]) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(v[i]);
+    *reinterpret_cast<h8*>(out) = h;
+  }
+};
+
+template <>
+struct Pack8<cm::bf16_t> {
+  static __device__ __forceinline__ void store(cm::bf16_t* out, const float (&v)[8]) {
+    uint4 r;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<uint32_t>(cm::from_f32<cm::bf16_t>(v[2 * i]).bits) |
+             (static_cast<uint32_t>(cm::from_f32<cm::bf16_t>(v[2 * i + 1]).bits) << 16);
+    }
+    r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+    *reinterpret_cast<uint4*>(out) = r;
+  }
+};
+
+template <>
+struct Pack8<float> {
+  static __device__ __forceinline__ void store(float* out, const float (&v)[8]) {
+    float4 a = make_float4(v[0], v[1], v[2], v[3]);
+    float4 b = make_float4(v[4], v[5], v[6], v[7]);
+    reinterpret_cast<float4*>(out)[0] = a;
+    reinterpret_cast<float4*>(out)[1] = b;
+  }
+};
+
+// Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes.
+template <typename OutT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
+    const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
+    const float* __restrict__ code, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
+    OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
+  __shared__ float s_code[16];
+  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
+  const float offset = NESTED ? *offset_ptr : 0.0f;
+  __syncthreads();
+
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnits) + threadIdx.x;
+  uint32_t word[kUnits];
+#pragma unroll
+  for (int j = 0; j < kUnits; ++j) {
+    const int64_t u = base + j * kThreads;
+    word[j] = u < n_units ? __builtin_nontemporal_load(packed + u) : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kUnits; ++j) {
+    const int64_t u = base + j * kThreads;
+    if (u >= n_units) break;
+    // 8 elements of unit u start at element 8u; blocksize = 8 << unit_shift elements.
+    const uint32_t blk = static_cast<uint32_t>(u >> unit_shift);
+    const float s = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t byte = (word[j] >> (8 * k)) & 0xffu;
+      v[2 * k] = s_code[byte >> 4] * s;
+      v[2 * k + 1] = s_code[byte & 0xfu] * s;
+    }
+    Pack8<OutT>::store(out + 8 * u, v);
+  }
+}
+
+// Scalar path: one packed byte per lane, any alignment; bytes [first, n_bytes).
+template <typename OutT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_bytes(
+    const uint8_t* __restrict__ packed, const void* __restrict__ absmax,
+    const float* __restrict__ code, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
+    OutT* __restrict__ out, int64_t first, int64_t n_bytes, int byte_shift, int bs2_shift,
+    uint32_t bs2) {
+  const int64_t i = first + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n_bytes) return;
+  const float offset = NESTED ? *offset_ptr : 0.0f;
+  const uint32_t byte = packed[i];
+  const uint32_t blk = static_cast<uint32_t>(i >> byte_shift);  // blocksize/2 bytes per block
+  const float s = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+  out[2 * i] = cm::from_f32<OutT>(code[byte >> 4] * s);
+  out[2 * i + 1] = cm::from_f32<OutT>(code[byte & 0xfu] * s);
+}
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t{1} << s) < v) ++s;
+  return s;
+}
+
+template <typename OutT, bool NESTED>
+int launch(const uint8_t* packed, const void* absmax, const float* code, const float* code2,
+           const float* absmax2, const float* offset, void* out_v, int64_t n_bytes,
+           int blocksize, int blocksize2, hipStream_t stream) {
+  OutT* out = static_cast<OutT*>(out_v);
+  const int bs_shift = log2_exact(blocksize);
+  const int bs2_shift = log2_exact(blocksize2);
+  const bool vec = cm::aligned(packed, 4) && cm::aligned(out, 16);
+  int64_t done = 0;
+  if (vec) {
+    const int64_t n_units = n_bytes / 4;
+    if (n_units > 0) {
+      const int64_t per_block = int64_t{kThreads} * kUnits;
+      const int64_t blocks = (n_units + per_block - 1) / per_block;
+      if (blocks > 0x7fffffff) return static_cast<int>(hipErrorInvalidValue);
+      // unit u covers elements [8u, 8u+8): block index = 8u / blocksize = u >> (bs_shift - 3)
+      hipLaunchKernelGGL((nf4_dequant_vec<OutT, NESTED>), dim3(static_cast<uint32_t>(blocks)),
+                         dim3(kThreads), 0, stream, reinterpret_cast<const uint32_t*>(packed),
+                         absmax, code, code2, absmax2, offset, out, n_units, bs_shift - 3,
+                         bs2_shift, static_cast<uint32_t>(blocksize2));
+      int st = cm::launch_status();
+      if (st) return st;
+    }
+    done = n_units * 4;
+  }
+  const int64_t rest = n_bytes - done;
+  if (rest > 0) {
+    const int64_t blocks = (rest + kThreads - 1) / kThreads;
+    if (blocks > 0x7fffffff) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL((nf4_dequant_bytes<OutT, NESTED>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kThreads), 0, stream, packed, absmax, code, code2, absmax2, offset,
+                       out, done, n_bytes, bs_shift - 1, bs2_shift,
+                       static_cast<uint32_t>(blocksize2));
+    int st = cm::launch_status();
+    if (st) return st;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested,
+                              const float* code, const float* code2, const float* absmax2,
+                              const float* offset, void* out, int out_dtype, int64_t n_bytes,
+                              int blocksize, int blocksize2, void* stream) {
+  CM_CHECK_ARG(n_bytes >= 0);
+  if (n_bytes == 0) return 0;
+  CM_CHECK_ARG(packed && absmax && code && out);
+  CM_CHECK_ARG(blocksize >= 32 && log2_exact(blocksize) >= 0);
+  // absmax block indices are 32-bit: n_bytes * 2 / blocksize must fit
+  CM_CHECK_ARG(n_bytes / (blocksize / 2) < (int64_t{1} << 31));
+  if (nested) CM_CHECK_ARG(code2 && absmax2 && offset && blocksize2 >= 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define CM_NF4_CASE(T)                                                                        \
+  return nested ? launch<T, true>(packed, absmax, code, code2, absmax2, offset, out, n_bytes, \
+                                  blocksize, blocksize2, s)                                   \
+                : launch<T, false>(packed, absmax, code, code2, absmax2, offset, out,         \
+                                   n_bytes, blocksize, 1, s)
+  switch (out_dtype) {
+    case CM_F16: CM_NF4_CASE(_Float16);
+    case CM_F32: CM_NF4_CASE(float);
+    case CM_BF16: CM_NF4_CASE(cm::bf16_t);
+    default: return static_cast<int>(hipErrorInvalidValue);
+  }
+#undef CM_NF4_CASE
+}

@@ -1,0 +1,379 @@
+// RMSNorm of Qwen2, forward and backward (gfx950).
+//
+// Reproduces solution/rmsnorm.py:28-47 (qwen_rmsnorm_fwd_kernel) and 51-91
+// (qwen_rmsnorm_bwd_kernel):
+//   rstd = 1 / sqrt(sum(x^2) / n + eps)      fp32
+//   normed = round_x(x * rstd);  out = round_out(normed * w)
+//   backward: gn = round_x(dy * w) (not rounded on the saved-output path),
+//             dx = round_x((gn - normed * sum(gn * normed) / n) * rstd),
+//             dw partial += dy * round_x(normed)
+// with the SAVE_LOW variant (fp32 x, frozen fp32 w) that keeps only the fp16 copy of the output
+// and the fp16 normalised values of the tiny-|w| columns, from which backward rebuilds normed.
+//
+// One wavefront owns one row; the row's sums are 64-lane shuffle reductions (no LDS, no block
+// barrier). A lane holds NV vectors of VEC contiguous columns in registers (VEC = 8: one
+// 16-byte access per vector for fp16), so x is read from HBM once; for rows wider than
+// NV * 64 * VEC columns the lane loops and the second pass re-reads the row from cache
+// (NV = 0). Four rows per 256-lane workgroup.
+#include <type_traits>
+
+#include "vec.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / cm::kWave;
+constexpr int kMaxBwdBlocks = 512;
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_v(const T* p, float (&v)[VEC], int cnt) {
+  if constexpr (VEC == 8) {
+    cm::Vec8<T, true>::load(p, v, cnt);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] = i < cnt ? cm::to_f32(p[i]) : 0.0f;
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_v(T* p, const float (&v)[VEC], int cnt) {
+  if constexpr (VEC == 8) {
+    cm::Vec8<T, true>::store(p, v, cnt);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      if (i < cnt) p[i] = cm::from_f32<T>(v[i]);
+  }
+}
+
+// NV > 0: the lane's columns are cached in registers; NV == 0: loop over the row.
+template <typename XT, typename WT, typename OT, int VEC, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
+    const XT* __restrict__ x, int64_t x_stride, const WT* __restrict__ w, OT* __restrict__ out,
+    float* __restrict__ rstd, _Float16* __restrict__ low16, const int32_t* __restrict__ slot,
+    _Float16* __restrict__ small16, int n_small, int64_t n_rows, int n_cols, float eps) {
+  const int lane = threadIdx.x % cm::kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / cm::kWave;
+  if (row >= n_rows) return;
+  const XT* xr = x + row * x_stride;
+  OT* orow = out + row * static_cast<int64_t>(n_cols);
+  constexpr int kCache = NV > 0 ? NV : 1;
+  float xv[kCache][VEC];
+  float ss = 0.0f;
+  const int step = cm::kWave * VEC;
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = i * step + lane * VEC;
+      const int cnt = c < n_cols ? min(VEC, n_cols - c) : 0;
+      load_v<XT, VEC>(xr + c, xv[i], cnt);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) ss += xv[i][k] * xv[i][k];
+    }
+  } else {
+    for (int c = lane * VEC; c < n_cols; c += step) {
+      load_v<XT, VEC>(xr + c, xv[0], min(VEC, n_cols - c));
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) ss += xv[0][k] * xv[0][k];
+    }
+  }
+  ss = cm::wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+  const bool save_low = low16 != nullptr;
+  const int n_iter = NV > 0 ? NV : (n_cols + step - 1) / step;
+  for (int i = 0; i < n_iter; ++i) {
+    const int c = i * step + lane * VEC;
+    if (c >= n_cols) break;
+    const int cnt = min(VEC, n_cols - c);
+    float xi[VEC], wv[VEC], o[VEC], nv[VEC];
+    if constexpr (NV > 0) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) xi[k] = xv[i][k];
+    } else {
+      load_v<XT, VEC>(xr + c, xi, cnt);
+    }
+    load_v<WT, VEC>(w + c, wv, cnt);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      nv[k] = cm::round_to<XT>(xi[k] * r);  // rounded to the input dtype before the weight
+      o[k] = nv[k] * wv[k];
+    }
+    store_v<OT, VEC>(orow + c, o, cnt);
+    if (save_low) {
+      store_v<_Float16, VEC>(low16 + row * static_cast<int64_t>(n_cols) + c, o, cnt);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        if (k < cnt) {
+          const int sl = slot[c + k];
+          if (sl >= 0) small16[row * static_cast<int64_t>(n_small) + sl] =
+              static_cast<_Float16>(nv[k]);
+        }
+      }
+    }
+  }
+}
+
+// Persistent over rows: wave g handles rows g, g + n_waves, ... and (with dw_partial) writes its
+// partial dw row g, zeros if it had no row.
+template <typename DT, typename XT, typename WT, typename DXT, int VEC, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_kernel(
+    const DT* __restrict__ dy, const void* __restrict__ xs_v, const WT* __restrict__ w,
+    const float* __restrict__ rstd, DXT* __restrict__ dx, float* __restrict__ dw_partial,
+    const int32_t* __restrict__ slot, const _Float16* __restrict__ small16, int n_small,
+    int saved_output, int64_t n_rows, int n_cols) {
+  const int lane = threadIdx.x % cm::kWave;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / cm::kWave;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
+  const int step = cm::kWave * VEC;
+  constexpr int kCache = NV > 0 ? NV : 1;
+  const bool want_dw = dw_partial != nullptr;
+  // Saved-output rows hold fp16 copies of the output; otherwise the rows hold x (type XT).
+  const XT* xs = static_cast<const XT*>(xs_v);
+  const _Float16* lows = static_cast<const _Float16*>(xs_v);
+  float dwacc[kCache][VEC];
+#pragma unroll
+  for (int i = 0; i < kCache; ++i)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) dwacc[i][k] = 0.0f;
+
+  for (int64_t row = wave; row < n_rows; row += n_waves) {
+    const float r = rstd[row];
+    const DT* dyr = dy + row * static_cast<int64_t>(n_cols);
+    float nc[kCache][VEC], gc[kCache][VEC];
+    float dot = 0.0f;
+    const int n_iter = NV > 0 ? NV : (n_cols + step - 1) / step;
+    // pass 1: normed and grad_normed, their dot product
+    for (int i = 0; i < n_iter; ++i) {
+      const int c = i * step + lane * VEC;
+      const int cnt = c < n_cols ? min(VEC, n_cols - c) : 0;
+      if (NV == 0 && cnt == 0) break;
+      const int ci = NV > 0 ? i : 0;
+      float d[VEC], wv[VEC], xv[VEC], nv[VEC], gv[VEC];
+      load_v<DT, VEC>(dyr + c, d, cnt);
+      load_v<WT, VEC>(w + c, wv, cnt);
+      if (saved_output) {
+        load_v<_Float16, VEC>(lows + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const int sl = k < cnt ? slot[c + k] : -1;
+          nv[k] = sl >= 0 ? static_cast<float>(small16[row * static_cast<int64_t>(n_small) + sl])
+                          : (k < cnt ? xv[k] / wv[k] : 0.0f);
+          gv[k] = d[k] * wv[k];
+        }
+      } else {
+        load_v<XT, VEC>(xs + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          nv[k] = xv[k] * r;
+          gv[k] = cm::round_to<XT>(d[k] * wv[k]);
+          if (want_dw) dwacc[ci][k] += d[k] * cm::round_to<XT>(nv[k]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        dot += gv[k] * nv[k];
+        nc[ci][k] = nv[k];
+        gc[ci][k] = gv[k];
+      }
+      if constexpr (NV == 0) {
+        // no register cache: finish nothing here, pass 2 recomputes
+      }
+    }
+    dot = cm::wave_sum(dot);
+    const float mean_dot = dot / static_cast<float>(n_cols);
+    DXT* dxr = dx + row * static_cast<int64_t>(n_cols);
+    // pass 2: dx
+    for (int i = 0; i < n_iter; ++i) {
+      const int c = i * step + lane * VEC;
+      if (c >= n_cols) break;
+      const int cnt = min(VEC, n_cols - c);
+      float nv[VEC], gv[VEC], o[VEC];
+      if constexpr (NV > 0) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          nv[k] = nc[i][k];
+          gv[k] = gc[i][k];
+        }
+      } else {
+        float d[VEC], wv[VEC], xv[VEC];
+        load_v<DT, VEC>(dyr + c, d, cnt);
+        load_v<WT, VEC>(w + c, wv, cnt);
+        if (saved_output) {
+          load_v<_Float16, VEC>(lows + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) {
+            const int sl = k < cnt ? slot[c + k] : -1;
+            nv[k] = sl >= 0
+                        ? static_cast<float>(small16[row * static_cast<int64_t>(n_small) + sl])
+                        : (k < cnt ? xv[k] / wv[k] : 0.0f);
+            gv[k] = d[k] * wv[k];
+          }
+        } else {
+          load_v<XT, VEC>(xs + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) {
+            nv[k] = xv[k] * r;
+            gv[k] = cm::round_to<XT>(d[k] * wv[k]);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) o[k] = (gv[k] - nv[k] * mean_dot) * r;
+      store_v<DXT, VEC>(dxr + c, o, cnt);
+    }
+  }
+  if (want_dw) {
+    float* pr = dw_partial + wave * static_cast<int64_t>(n_cols);
+    if constexpr (NV > 0) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int c = i * step + lane * VEC;
+        if (c < n_cols) store_v<float, VEC>(pr + c, dwacc[i], min(VEC, n_cols - c));
+      }
+    } else {
+      // Looped rows keep no register cache: redo the sums column by column (rare, wide rows).
+      for (int c = lane * VEC; c < n_cols; c += step) {
+        const int cnt = min(VEC, n_cols - c);
+        float acc[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+        for (int64_t row = wave; row < n_rows; row += n_waves) {
+          const float r = rstd[row];
+          float d[VEC], xv[VEC];
+          load_v<DT, VEC>(dy + row * static_cast<int64_t>(n_cols) + c, d, cnt);
+          load_v<XT, VEC>(xs + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) acc[k] += d[k] * cm::round_to<XT>(xv[k] * r);
+        }
+        store_v<float, VEC>(pr + c, acc, cnt);
+      }
+    }
+  }
+}
+
+// torch.promote_types over the three float dtypes: equal types stay, anything else is fp32
+// (fp16 with bf16 promotes to fp32 as well).
+int promote(int a, int b) { return a == b ? a : CM_F32; }
+
+template <typename XT, typename WT>
+using Promoted = typename std::conditional<std::is_same<XT, WT>::value, XT, float>::type;
+
+int pick_nv(int n_cols, int vec) {
+  const int per = cm::kWave * vec;
+  const int nv = (n_cols + per - 1) / per;
+  (void)vec;
+  return nv <= 4 ? nv : 0;
+}
+
+int64_t bwd_blocks(int64_t n_rows, bool want_dw) {
+  const int64_t need = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  return want_dw ? (need < kMaxBwdBlocks ? need : kMaxBwdBlocks) : need;
+}
+
+#define CM_NV_SWITCH(nv, NV, ...)        \
+  switch (nv) {                          \
+    case 1: { constexpr int NV = 1; __VA_ARGS__; } break; \
+    case 2: { constexpr int NV = 2; __VA_ARGS__; } break; \
+    case 3: { constexpr int NV = 3; __VA_ARGS__; } break; \
+    case 4: { constexpr int NV = 4; __VA_ARGS__; } break; \
+    default: { constexpr int NV = 0; __VA_ARGS__; } break; \
+  }
+
+}  // namespace
+
+extern "C" int64_t cm_rmsnorm_bwd_partials(int64_t n_rows) {
+  return n_rows <= 0 ? 0 : bwd_blocks(n_rows, true) * kRowsPerBlock;
+}
+
+extern "C" int cm_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, const void* w,
+                              int w_dtype, void* out, int out_dtype, float* rstd, void* low16,
+                              const int32_t* slot, void* small16, int n_small, int64_t n_rows,
+                              int n_cols, float eps, void* stream) {
+  CM_CHECK_ARG(n_rows >= 0 && n_cols > 0 && x_row_stride >= n_cols);
+  if (n_rows == 0) return 0;
+  CM_CHECK_ARG(x && w && out && rstd);
+  CM_CHECK_ARG(!low16 || (slot && small16 && n_small >= 1));
+  const int64_t blocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  CM_CHECK_ARG(blocks <= 0x7fffffff);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool v8 = n_cols % 8 == 0 && x_row_stride % 8 == 0 && cm::aligned(x, 16) &&
+                  cm::aligned(w, 16) && cm::aligned(out, 16) && (!low16 || cm::aligned(low16, 16));
+  const int vec = v8 ? 8 : 1;
+  const int nv = pick_nv(n_cols, vec);
+  // The output dtype is torch.promote_types(x, w), as in the reference.
+  CM_CHECK_ARG(out_dtype == promote(x_dtype, w_dtype));
+  CM_FLOAT_SWITCH(x_dtype, XT, CM_FLOAT_SWITCH(w_dtype, WT, {
+    using OT = Promoted<XT, WT>;
+    if (v8) {
+      CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, WT, OT, 8, NV>),
+                                              dim3(blocks), dim3(kThreads), 0, s,
+                                              static_cast<const XT*>(x), x_row_stride,
+                                              static_cast<const WT*>(w), static_cast<OT*>(out),
+                                              rstd, static_cast<_Float16*>(low16), slot,
+                                              static_cast<_Float16*>(small16), n_small, n_rows,
+                                              n_cols, eps));
+    } else {
+      CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, WT, OT, 1, NV>),
+                                              dim3(blocks), dim3(kThreads), 0, s,
+                                              static_cast<const XT*>(x), x_row_stride,
+                                              static_cast<const WT*>(w), static_cast<OT*>(out),
+                                              rstd, static_cast<_Float16*>(low16), slot,
+                                              static_cast<_Float16*>(small16), n_small, n_rows,
+                                              n_cols, eps));
+    }
+  }));
+  return cm::launch_status();
+}
+
+extern "C" int cm_rmsnorm_bwd(const void* dy, int dy_dtype, const void* xs, int xs_dtype,
+                              const void* w, int w_dtype, const float* rstd, void* dx,
+                              int dx_dtype, float* dw_partial, const int32_t* slot,
+                              const void* small16, int n_small, int saved_output,
+                              int64_t n_rows, int n_cols, void* stream) {
+  CM_CHECK_ARG(n_rows >= 0 && n_cols > 0);
+  if (n_rows == 0) return 0;
+  CM_CHECK_ARG(dy && xs && w && rstd && dx);
+  if (saved_output) {
+    // xs holds the fp16 output copy; dx has the dtype of x (fp32 on this path); no dw.
+    CM_CHECK_ARG(xs_dtype == CM_F16 && slot && small16 && n_small >= 1 && !dw_partial);
+  }
+  const bool want_dw = dw_partial != nullptr;
+  const int64_t blocks = bwd_blocks(n_rows, want_dw);
+  CM_CHECK_ARG(blocks <= 0x7fffffff);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool v8 = n_cols % 8 == 0 && cm::aligned(dy, 16) && cm::aligned(xs, 16) &&
+                  cm::aligned(w, 16) && cm::aligned(dx, 16) &&
+                  (!dw_partial || cm::aligned(dw_partial, 16));
+  const int vec = v8 ? 8 : 1;
+  const int nv = pick_nv(n_cols, vec);
+  // The kernel's XT is the dtype of x (rounding target of gn/normed). On the saved-output path
+  // x is fp32 and xs holds fp16 copies, read through the _Float16 view inside the kernel.
+  const int x_dtype = saved_output ? dx_dtype : xs_dtype;
+  // dx has the dtype of x; dy the dtype of the forward output, promote(x, w).
+  CM_CHECK_ARG(dx_dtype == x_dtype && dy_dtype == promote(x_dtype, w_dtype));
+  CM_FLOAT_SWITCH(x_dtype, XT, CM_FLOAT_SWITCH(w_dtype, WT, {
+    using DT = Promoted<XT, WT>;
+    using DXT = XT;
+    {
+      if (v8) {
+        CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, XT, WT, DXT, 8, NV>),
+                                                dim3(blocks), dim3(kThreads), 0, s,
+                                                static_cast<const DT*>(dy), xs,
+                                                static_cast<const WT*>(w), rstd,
+                                                static_cast<DXT*>(dx), dw_partial, slot,
+                                                static_cast<const _Float16*>(small16), n_small,
+                                                saved_output, n_rows, n_cols));
+      } else {
+        CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, XT, WT, DXT, 1, NV>),
+                                                dim3(blocks), dim3(kThreads), 0, s,
+                                                static_cast<const DT*>(dy), xs,
+                                                static_cast<const WT*>(w), rstd,
+                                                static_cast<DXT*>(dx), dw_partial, slot,
+                                                static_cast<const _Float16*>(small16), n_small,
+                                                saved_output, n_rows, n_cols));
+      }
+    }
+  }));
+  return cm::launch_status();
+}

@@ -1,0 +1,186 @@
+/*
+ * claudemaxing_amd: C ABI of the MI355X (gfx950) QLoRA training-step kernel set.
+ *
+ * Every entry point
+ *   - takes plain device pointers, element counts and strides, never torch types;
+ *   - is stream-ordered on `stream` (a hipStream_t passed as void*, NULL = the null stream);
+ *   - never allocates, never synchronises the host, holds no mutable global state;
+ *   - returns 0 on success, or a hipError_t value (hipErrorInvalidValue = 1 for bad arguments;
+ *     launch failures are reported from hipGetLastError()). cm_error_string() names a code.
+ *
+ * Each declaration cites the reference (arturbaimuratov1-sys/claudemaxing, Triton) kernel and
+ * host function whose behaviour it reproduces.
+ */
+#ifndef CLAUDEMAXING_AMD_H
+#define CLAUDEMAXING_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CM_ABI_VERSION 1
+
+/* Element types of tensor arguments. */
+typedef enum {
+  CM_F32 = 0,
+  CM_F16 = 1,
+  CM_BF16 = 2,
+  CM_U8 = 3,
+  CM_I32 = 4,
+  CM_I64 = 5
+} cm_dtype;
+
+/* ABI version of the loaded library (CM_ABI_VERSION it was built with). */
+int cm_abi_version(void);
+
+/* Human-readable name of a return code of this library. Never NULL. */
+const char* cm_error_string(int code);
+
+/* ------------------------------------------------------------------------------------------ */
+/* NF4 dequantization with the nested (double-quantized) absmax decoded in the same pass.
+ * Replaces solution/nf4.py:26-46 (nf4_dequant_kernel) as launched by dequantize_nf4
+ * (solution/nf4.py:64-82).
+ *
+ * Byte i of `packed` holds elements 2i (high nibble) and 2i+1 (low nibble). Element j belongs to
+ * absmax block b = j / blocksize. With nested != 0 the block scale is
+ *   s = code2[absmax_u8[b]] * absmax2[b / blocksize2] + offset[0]   (fp32 multiply, then add;
+ *                                                                     never fused)
+ * otherwise s = absmax_f32[b]. Output j = round_to_nearest_even(code[nibble_j] * s) in out_dtype
+ * (CM_F16 or CM_F32, or CM_BF16). blocksize must be even and >= 32 (bitsandbytes' blocksizes),
+ * blocksize2 >= 1. Bit-exact with the reference for every input.
+ */
+int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested, const float* code,
+                   const float* code2, const float* absmax2, const float* offset, void* out,
+                   int out_dtype, int64_t n_bytes, int blocksize, int blocksize2, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* RMSNorm forward, one row per wavefront. Replaces solution/rmsnorm.py:28-47
+ * (qwen_rmsnorm_fwd_kernel) as launched by RMSNorm.forward (solution/rmsnorm.py:147-192).
+ *   rstd[r] = 1 / sqrt(sum_c x[r,c]^2 / n_cols + eps)            (fp32)
+ *   normed = round_x(x * rstd);  out = round_out(normed * w)
+ * x is row-major [n_rows, n_cols] with row stride x_row_stride (elements); out is contiguous.
+ * With low16 != NULL (the SAVE_LOW path: fp32 x, frozen fp32 w), also writes
+ *   low16[r,c] = fp16(normed * w) and small16[r * n_small + slot[c]] = fp16(normed) for slot[c] >= 0.
+ */
+int cm_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, const void* w, int w_dtype,
+                   void* out, int out_dtype, float* rstd, void* low16, const int32_t* slot,
+                   void* small16, int n_small, int64_t n_rows, int n_cols, float eps,
+                   void* stream);
+
+/* RMSNorm backward. Replaces solution/rmsnorm.py:51-91 (qwen_rmsnorm_bwd_kernel) as launched
+ * by RMSNorm.backward (solution/rmsnorm.py:194-217).
+ * saved_output == 0: `xs` holds x (x_dtype);  normed = x * rstd;  gn = round_x(dy * w).
+ * saved_output != 0: `xs` holds the fp16 copy of the output (low16 of the forward); normed is
+ *   small16[r, slot[c]] where slot[c] >= 0, else xs / w;  gn = dy * w (x is fp32: no rounding).
+ *   dx[r,c] = round_x((gn - normed * sum_c(gn * normed) / n_cols) * rstd)
+ * dw_partial (may be NULL) receives per-workgroup fp32 partial sums of dy * round_x(normed), one
+ * row of n_cols per workgroup; the number of rows written is cm_rmsnorm_bwd_partials(n_rows).
+ */
+int cm_rmsnorm_bwd(const void* dy, int dy_dtype, const void* xs, int xs_dtype, const void* w,
+                   int w_dtype, const float* rstd, void* dx, int dx_dtype, float* dw_partial,
+                   const int32_t* slot, const void* small16, int n_small, int saved_output,
+                   int64_t n_rows, int n_cols, void* stream);
+/* Number of partial dw rows cm_rmsnorm_bwd writes for n_rows rows. */
+int64_t cm_rmsnorm_bwd_partials(int64_t n_rows);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Rotary position embedding, forward or backward (transposed rotation), on up to two tensors
+ * (q and k) in one launch. Replaces solution/rope.py:17-43 (qwen_rope_kernel) as launched twice
+ * by RoPE.forward / RoPE.backward (solution/rope.py:60-76, _rotate 46-57).
+ * x_i is [B, H_i, T, D] with element strides (sb_i, sh_i, st_i, 1); cos/sin are [Bc, T, D] with
+ * strides (cs_b, cs_t, 1); cs_b = 0 broadcasts one row of positions over the batch.
+ * out_i is contiguous [B, H_i, T, D]. With h = D/2:
+ *   forward:  o[:h] = x1*c1 - x2*s1;  o[h:] = x2*c2 + x1*s2
+ *   backward: o[:h] = x1*c1 + x2*s2;  o[h:] = x2*c2 - x1*s1         (fp32 arithmetic)
+ * Pass x1 = NULL (H1 = 0) to rotate one tensor. D must be even and <= 512.
+ */
+int cm_rope(const void* x0, int x0_dtype, int64_t sb0, int64_t sh0, int64_t st0, int H0,
+            void* out0, int out0_dtype, const void* x1, int x1_dtype, int64_t sb1, int64_t sh1,
+            int64_t st1, int H1, void* out1, int out1_dtype, const void* cos, const void* sin,
+            int cs_dtype, int64_t cs_b, int64_t cs_t, int B, int T, int D, int backward,
+            void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* SwiGLU forward: out = round_out(round_g?(silu(g)) * u), silu(g) = g / (1 + 2^(-g*log2(e))).
+ * Replaces solution/swiglu_recompute.py:36-48 (silu_mul_fwd_persistent) as launched by
+ * SwiGLURecompute.forward (91-104) and MLPInputRecompute.forward (155-186).
+ * round_silu != 0 rounds silu to g_dtype before the product. All tensors contiguous, n elements.
+ */
+int cm_swiglu_fwd(const void* gate, int g_dtype, const void* up, int u_dtype, void* out,
+                  int out_dtype, int64_t n, int round_silu, void* stream);
+
+/* SwiGLU backward with silu recomputed from gate. Replaces solution/swiglu_recompute.py:51-79
+ * (silu_mul_bwd_recompute) as launched by SwiGLURecompute.backward (106-122) and
+ * MLPInputRecompute.backward (188-215).
+ *   sig = 1/(1 + 2^(-g*log2(e)));  d_up = round_u(dy * round_g?(g*sig));
+ *   d_gate = round_g(round_g?(dy * u) * sig * (1 + g*(1 - sig)))
+ * dgate may equal gate and dup may equal up (in place: every element is read before it is
+ * written). want_dgate / want_dup select the outputs written.
+ */
+int cm_swiglu_bwd(const void* dy, int dy_dtype, const void* gate, int g_dtype, const void* up,
+                  int u_dtype, void* dgate, void* dup, int64_t n, int want_dgate, int want_dup,
+                  int round_silu, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* LoRA dropout mask pack. Replaces solution/lora.py:30-42 (lora_dropout_pack_kernel) as
+ * launched by _pack (lora.py:60-66).
+ *   xd[i] = fp16(keep[i] ? x[i] * scale : 0);  bits[i/8] bit (i%8) = keep[i] != 0
+ * keep is a bool/uint8 array of n elements; n must be a multiple of 8. Bit-exact.
+ */
+int cm_lora_pack(const void* x, int x_dtype, const uint8_t* keep, void* xd16, uint8_t* bits,
+                 int64_t n, float scale, void* stream);
+
+/* LoRA dropout mask unpack. Replaces solution/lora.py:45-57 (lora_dropout_unpack_kernel) as
+ * launched by _unpack (lora.py:69-75).
+ *   keep = bits[i/8] >> (i%8) & 1;  xd[i] = fp16(keep ? x16[i]*scale : 0);
+ *   dx[i] = round_dx(keep ? g16[i]*scale : 0)
+ * n must be a multiple of 8. Bit-exact.
+ */
+int cm_lora_unpack(const void* x16, const uint8_t* bits, const void* g16, void* xd16, void* dx,
+                   int dx_dtype, int64_t n, float scale, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Cross-entropy statistics of full logits, one row per workgroup (the fallback when logits
+ * exist anyway). Replaces solution/lm_head_loss.py:54-96 (lm_head_xent_rows_kernel) as launched
+ * by _rows / head_metrics_from_logits (lm_head_loss.py:168-172, 285-297).
+ *   loss[r] = label ? lse - z[t] : 0;  entropy[r] = lse - sum(e^z z)/sum(e^z);
+ *   correct[r] = label && first_argmax == t.  With write_grad, the row is overwritten by
+ *   round((softmax - onehot) * grad_scale) (zero for unlabelled rows).
+ * logits [n_rows, n_cols] (f16/bf16/f32) with row stride `row_stride`; target int64 [n_rows]
+ * with -100 = ignored.
+ */
+int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64_t* target,
+                 float* loss, float* entropy, int32_t* correct, int64_t n_rows, int64_t n_cols,
+                 int write_grad, float grad_scale, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Fused LM head + cross-entropy with per-row loss, entropy, accuracy and the hidden-state
+ * gradient, without materialising logits. Replaces the chunk loop of _FusedHeadLoss.forward
+ * (solution/lm_head_loss.py:192-245: torch.mm + lm_head_vocab_chunk_kernel (108-160) + torch.mm
+ * per vocabulary chunk, label fix-up 230-236).
+ *   z[r,v] = fp16(sum_k hidden[r,k] * W[v,k])          (fp32 accumulation, rounded to fp16)
+ *   lse_r = log sum_v e^{z[r,v]};  loss[r] = label ? lse_r - z[r,t_r] : 0;
+ *   entropy[r] = lse_r - sum_v softmax(z)_v z_v;  correct[r] = label && first_argmax_v z == t_r
+ *   grad (if not NULL) [n_rows, H] fp32 = grad_scale * sum_v (softmax_v - [v == t_r]) W[v,:]
+ *     (zero rows for unlabelled targets)
+ * hidden fp16 [n_rows, H] (row stride ld_h), W fp16 [V, H] (row stride ld_w), target int64.
+ * The vocabulary is walked in chunks of chunk_cols columns (0 = the library's default); the
+ * result does not depend on the chunk size beyond fp32 rounding.
+ * workspace: device memory of cm_lmhead_ce_workspace_bytes(n_rows, V, H, chunk_cols) bytes,
+ * 256-B aligned.
+ */
+int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
+                 const int64_t* target, int64_t n_rows, int64_t vocab, int hidden_size,
+                 int64_t chunk_cols, float* loss, float* entropy, int32_t* correct, float* grad,
+                 float grad_scale, void* workspace, int64_t workspace_bytes, void* stream);
+/* Workspace bytes cm_lmhead_ce needs for these sizes (chunk_cols as passed to cm_lmhead_ce). */
+int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_size,
+                                     int64_t chunk_cols);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLAUDEMAXING_AMD_H */

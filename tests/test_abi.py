@@ -1,0 +1,92 @@
+"""The C-ABI library: loads, exports every symbol include/claudemaxing_amd.h declares, and
+rejects bad arguments on the host before touching the GPU (no GPU needed)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from claudemaxing_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "claudemaxing_amd.h"
+INVALID = 1  # hipErrorInvalidValue
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_symbols()
+    assert "cm_nf4_dequant" in names and "cm_lmhead_ce" in names and len(names) >= 14
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_signatures_match_the_header_arity():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        m = re.search(rf"\b{name}\s*\(([^)]*)\)", text)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(argtypes), (name, len(params), len(argtypes))
+
+
+def test_abi_version_and_error_strings(lib):
+    assert lib.cm_abi_version() == _lib.ABI_VERSION
+    assert lib.cm_error_string(0) == b"success"
+    assert lib.cm_error_string(INVALID) == b"invalid argument"
+    assert lib.cm_error_string(12345)  # never NULL
+
+
+def test_argument_checks_run_on_the_host(lib):
+    # Every call below fails its argument checks before any HIP call is made.
+    assert lib.cm_lora_pack(None, 0, None, None, None, 7, 1.0, None) == INVALID  # n % 8
+    assert lib.cm_lora_unpack(None, None, None, None, None, 0, -8, 1.0, None) == INVALID
+    assert lib.cm_nf4_dequant(None, None, 1, None, None, None, None, None, 1, 10, 48, 256,
+                              None) == INVALID  # blocksize not a power of two
+    assert lib.cm_nf4_dequant(None, None, 1, None, None, None, None, None, 1, 10, 16, 256,
+                              None) == INVALID  # blocksize below 32
+    assert lib.cm_rope(None, 1, 0, 0, 0, 1, None, 1, None, 1, 0, 0, 0, 0, None, 1, None, None,
+                       1, 0, 0, 1, 1, 7, 0, None) == INVALID  # odd head_dim
+    assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, -1, 1, None) == INVALID
+    assert lib.cm_rmsnorm_fwd(None, 1, 4, None, 0, None, 1, None, None, None, None, 1, 2, 8,
+                              1e-6, None) == INVALID  # row stride < n_cols
+    assert lib.cm_xent_rows(None, 1, 4, None, None, None, None, 1, 8, 0, 1.0, None) == INVALID
+
+
+def test_empty_inputs_are_no_ops(lib):
+    assert lib.cm_nf4_dequant(None, None, 0, None, None, None, None, None, 1, 0, 64, 256,
+                              None) == 0
+    assert lib.cm_lora_pack(None, 0, None, None, None, 0, 1.0, None) == 0
+    assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, 0, 1, None) == 0
+    assert lib.cm_rmsnorm_bwd_partials(0) == 0
+    assert lib.cm_rmsnorm_bwd_partials(10) == 12
+
+
+def test_call_raises_with_the_library_message():
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.call("cm_lora_pack", None, 0, None, None, None, 7, 1.0, None)
+
+
+def test_missing_library_raises_import_error(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libnothing.so")
+    with pytest.raises(ImportError, match="missing"):
+        _lib.load()
+
+
+def test_dtype_codes():
+    import torch
+
+    assert _lib.dtype_code(torch.float16) == 1 and _lib.dtype_code(torch.bool) == 3
+    with pytest.raises(TypeError):
+        _lib.dtype_code(torch.complex64)
+    assert ctypes.sizeof(ctypes.c_void_p) == 8

@@ -1,0 +1,106 @@
+"""NF4 dequant on the GPU against the oracle: bit-exact (fp16, fp32, bf16 outputs)."""
+
+import numpy as np
+import pytest
+import torch
+
+from claudemaxing_amd import _lib
+from claudemaxing_amd.nf4 import QuantState, dequantize_nf4, quantize_nf4
+from oracle import inputs, nf4 as O
+from tests.conftest import banner
+from tests.helpers import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+NP_OUT = {torch.float16: "f16", torch.float32: "f32", torch.bfloat16: "bf16"}
+
+
+def oracle_of(packed, state, dtype):
+    nested = state.nested
+    kw = dict(nested=nested, blocksize=state.blocksize, out_dtype=NP_OUT[dtype])
+    if nested:
+        kw.update(code2=state.state2.code.cpu().numpy(), absmax2=state.state2.absmax.cpu().numpy(),
+                  offset=np.float32(state.offset.cpu().item()), blocksize2=state.state2.blocksize)
+    ref = O.dequant(packed.cpu().numpy(), state.absmax.cpu().numpy(), **kw)
+    t = torch.from_numpy(ref.view(np.int16) if dtype == torch.bfloat16 else ref)
+    if dtype == torch.bfloat16:
+        t = t.view(torch.bfloat16)
+    return t.reshape(tuple(state.shape))
+
+
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("shape", [(8960, 1536), (1536, 1536), (256, 1536), (1536, 8960), (3, 64)])
+def test_matches_oracle_bitwise(nested, shape, dev):
+    banner(f"nf4 shape={shape} nested={nested}")
+    w = torch.randn(*shape, generator=torch.Generator().manual_seed(0)) * 0.05
+    w[0, :5] = torch.tensor([0.0, -0.0, 1e-7, 3.0, -2.5])  # tests_local/test_nf4.py:21
+    packed, state = quantize_nf4(w, 64, nested)
+    packed_d, state_d = packed.to(dev), state.to(dev)
+    for dtype in (torch.float16, torch.float32, torch.bfloat16):
+        out = dequantize_nf4(packed_d, state_d, dtype)
+        torch.cuda.synchronize()
+        assert_bits_equal(out, oracle_of(packed, state, dtype), f"{shape} {dtype}")
+
+
+def test_config1_gate_proj(dev):
+    banner("nf4 config 1")
+    w = inputs.nf4_weight(0)
+    packed, state = quantize_nf4(w, 64, True)
+    out = dequantize_nf4(packed.to(dev), state.to(dev), torch.float16)
+    assert_bits_equal(out, oracle_of(packed, state, torch.float16), "config 1")
+    # reconstruction error of NF4 itself stays small (sanity of the whole chain)
+    err = (out.float().cpu() - w).abs().max().item()
+    assert err < 0.02, err
+
+
+def test_every_byte_with_every_q8_code(dev):
+    banner("nf4 exhaustive bytes x q8")
+    code2 = torch.from_numpy(O.dynamic_map())
+    packed = torch.arange(256, dtype=torch.uint8).repeat(256)
+    q8 = torch.arange(256, dtype=torch.uint8)
+    absmax2 = torch.tensor([0.37, 1.5])
+    state2 = QuantState(absmax=absmax2, code=code2, blocksize=128, dtype=torch.float32)
+    state = QuantState(absmax=q8, shape=torch.Size([256, 512]), code=torch.tensor(O.NF4_TABLE),
+                       blocksize=512, offset=torch.tensor(0.0123), state2=state2)
+    out = dequantize_nf4(packed.to(dev), state.to(dev), torch.float16)
+    assert_bits_equal(out, oracle_of(packed, state, torch.float16), "exhaustive")
+
+
+@pytest.mark.parametrize("blocksize,blocksize2", [(32, 256), (128, 256), (4096, 256), (64, 100),
+                                                  (64, 1)])
+@pytest.mark.parametrize("n_bytes", [1, 3, 5, 1029, 65536 + 7])
+def test_random_bytes_blocksizes_and_tails(blocksize, blocksize2, n_bytes, dev):
+    banner(f"nf4 random bs={blocksize} bs2={blocksize2} n_bytes={n_bytes}")
+    g = torch.Generator().manual_seed(n_bytes)
+    n_blk = (2 * n_bytes + blocksize - 1) // blocksize
+    packed = torch.randint(0, 256, (n_bytes,), dtype=torch.uint8, generator=g)
+    q8 = torch.randint(0, 256, (n_blk,), dtype=torch.uint8, generator=g)
+    absmax2 = torch.rand((n_blk + blocksize2 - 1) // blocksize2, generator=g) + 0.1
+    code2 = torch.from_numpy(O.dynamic_map())
+    code = torch.tensor(O.NF4_TABLE)
+    offset = torch.tensor([0.03125], dtype=torch.float32)
+    out = torch.empty(2 * n_bytes, dtype=torch.float16, device=dev)
+    d = {k: v.to(dev) for k, v in dict(p=packed, q8=q8, a2=absmax2, c2=code2, c=code,
+                                        off=offset).items()}
+    _lib.call("cm_nf4_dequant", d["p"].data_ptr(), d["q8"].data_ptr(), 1, d["c"].data_ptr(),
+              d["c2"].data_ptr(), d["a2"].data_ptr(), d["off"].data_ptr(), out.data_ptr(),
+              _lib.F16, n_bytes, blocksize, blocksize2, _lib.stream(dev))
+    ref = O.dequant(packed.numpy(), q8.numpy(), nested=True, code2=code2.numpy(),
+                    absmax2=absmax2.numpy(), offset=np.float32(0.03125), blocksize=blocksize,
+                    blocksize2=blocksize2)
+    assert_bits_equal(out, torch.from_numpy(ref), "random")
+
+
+def test_misaligned_output_takes_the_byte_path(dev):
+    banner("nf4 misaligned output")
+    w = torch.randn(16, 64, generator=torch.Generator().manual_seed(2)) * 0.05
+    packed, state = quantize_nf4(w, 64, True)
+    sd = state.to(dev)
+    buf = torch.empty(16 * 64 + 1, dtype=torch.float16, device=dev)
+    out = buf[1:]  # 2-byte aligned view
+    code = sd.code
+    _lib.call("cm_nf4_dequant", packed.to(dev).data_ptr(), sd.absmax.data_ptr(), 1,
+              code.data_ptr(), sd.state2.code.data_ptr(), sd.state2.absmax.data_ptr(),
+              sd.offset.reshape(1).data_ptr(), out.data_ptr(), _lib.F16, 16 * 32, 64, 256,
+              _lib.stream(dev))
+    assert_bits_equal(out.reshape(16, 64), oracle_of(packed, state, torch.float16), "misaligned")
