@@ -27,10 +27,21 @@ struct Conv<float> {
   static __device__ __forceinline__ float store(float v) { return v; }
 };
 
+// Pins an fp32 value in a register as it is. The compiler would otherwise fold an fp32
+// multiply followed by the conversion to fp16 into one mixed-precision instruction
+// (v_fma_mix*_f16) that rounds the exact product once; the reference rounds twice (to fp32,
+// then to fp16), and the two differ in the last fp16 bit for a few products in 10^5.
+__device__ __forceinline__ float materialize(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 template <>
 struct Conv<_Float16> {
   static __device__ __forceinline__ float load(_Float16 v) { return static_cast<float>(v); }
-  static __device__ __forceinline__ _Float16 store(float v) { return static_cast<_Float16>(v); }
+  static __device__ __forceinline__ _Float16 store(float v) {
+    return static_cast<_Float16>(materialize(v));
+  }
 };
 
 template <>

@@ -45,7 +45,7 @@ struct Pack8<_Float16> {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     h8 h;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(v[i]);
+    for (int i = 0; i < 8; ++i) h[i] = cm::from_f32<_Float16>(v[i]);
     *reinterpret_cast<h8*>(out) = h;
   }
 };

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
         if (k < cnt) {
           const int sl = slot[c + k];
           if (sl >= 0) small16[row * static_cast<int64_t>(n_small) + sl] =
-              static_cast<_Float16>(nv[k]);
+              cm::from_f32<_Float16>(nv[k]);
         }
       }
     }

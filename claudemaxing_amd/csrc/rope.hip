@@ -44,7 +44,7 @@ struct VecN<_Float16, 4> {
   static __device__ __forceinline__ void store(_Float16* p, const float (&v)[4]) {
     h4 h;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = static_cast<_Float16>(v[i]);
+    for (int i = 0; i < 4; ++i) h[i] = cm::from_f32<_Float16>(v[i]);
     *reinterpret_cast<h4*>(p) = h;
   }
 };

@@ -37,7 +37,7 @@ struct Vec8<_Float16, true> {
     if (cnt == 8) {
       h8 h;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(v[i]);
+      for (int i = 0; i < 8; ++i) h[i] = from_f32<_Float16>(v[i]);
       *reinterpret_cast<h8*>(p) = h;
     } else {
       Vec8<_Float16, false>::store(p, v, cnt);
