@@ -16,7 +16,10 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnits = 2;
+#ifndef CM_SWIGLU_UNITS
+#define CM_SWIGLU_UNITS 2
+#endif
+constexpr int kUnits = CM_SWIGLU_UNITS;
 constexpr float kNegLog2e = -1.4426950408889634f;
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
