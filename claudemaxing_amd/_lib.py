@@ -43,8 +43,7 @@ SIGNATURES = {
     "cm_lora_pack": (_I, [_P, _I, _P, _P, _P, _L, _F, _P]),
     "cm_lora_unpack": (_I, [_P, _P, _P, _P, _P, _I, _L, _F, _P]),
     "cm_xent_rows": (_I, [_P, _I, _L, _P, _P, _P, _P, _L, _L, _I, _F, _P]),
-    "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L,
-                          _P]),
+    "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L, _P]),
     "cm_lmhead_ce_workspace_bytes": (_L, [_L, _L, _I, _L]),
 }
 

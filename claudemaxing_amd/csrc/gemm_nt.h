@@ -1,0 +1,194 @@
+// fp16 "NT" GEMM core on the gfx950 matrix cores: C[m][n] = sum_k A[m][k] B[n][k], fp32
+// accumulation in v_mfma_f32_32x32x16_f16 tiles, the accumulators handed to an epilogue functor.
+//
+// Operands are K-contiguous and come in two layouts:
+//   RowMajor  element (r, k) at p[r * ld + k];
+//   Blocked64 element (r, k) at p[((k / 64) * rows + r) * 64 + k % 64], i.e. 64-column panels,
+//             so a (rows x 64) tile of one panel is a single contiguous span. Panels are padded
+//             to 64 columns (the padding must hold finite values; the LM head keeps zeros there).
+// Each pipeline stage moves a BM x 64 tile of A and a BN x 64 tile of B global -> registers ->
+// LDS with 16-byte accesses. Tiles entirely inside the matrices take a branch-free path (one
+// scalar test per tile); edge tiles fall back to per-element bounds checks. LDS rows of 64 fp16
+// (128 B = 8 chunks of 16 B) are XOR-swizzled (chunk ^ row % 8): the fragment reads of 8
+// consecutive rows hit all 32 banks. With STAGES = 2 the LDS is double-buffered (one barrier per
+// stage, the next stage's global loads overlap this stage's MFMAs); with STAGES = 1 a single LDS
+// buffer halves the footprint so that two workgroups share a CU.
+#pragma once
+
+#include "common.h"
+
+namespace cm {
+namespace gemm {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;        // 4 wavefronts per workgroup
+constexpr int kBK = 64;              // K elements per stage
+constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per tile row
+
+struct RowMajor {
+  const _Float16* p;
+  int64_t ld;
+  int rows;   // valid rows
+  int k_len;  // valid columns
+  __device__ __forceinline__ const _Float16* at(int r, int k) const {
+    return p + static_cast<int64_t>(r) * ld + k;
+  }
+  __device__ __forceinline__ bool tile_inside(int r0, int n_rows, int k0) const {
+    return r0 + n_rows <= rows && k0 + kBK <= k_len;
+  }
+  __device__ __forceinline__ bool col_ok(int k) const { return k < k_len; }
+};
+
+struct Blocked64 {
+  const _Float16* p;
+  int rows;   // valid rows (= rows of a panel)
+  int k_len;  // columns, padded panels beyond it hold finite values
+  __device__ __forceinline__ const _Float16* at(int r, int k) const {
+    return p + ((static_cast<int64_t>(k / kBK) * rows + r) * kBK + k % kBK);
+  }
+  __device__ __forceinline__ bool tile_inside(int r0, int n_rows, int k0) const {
+    return r0 + n_rows <= rows && k0 < k_len;
+  }
+  // the panel holding k exists (padding columns are read as stored)
+  __device__ __forceinline__ bool col_ok(int k) const { return (k / kBK) * kBK < k_len; }
+};
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+template <int ROWS>
+struct TileLoad {
+  static constexpr int kPer = ROWS * kRowChunks / kThreads;
+  static_assert(kPer * kThreads == ROWS * kRowChunks, "tile rows must split over the threads");
+  uint4 v[kPer];
+
+  template <class Src>
+  __device__ __forceinline__ void load(const Src& src, int r0, int k0) {
+    if (src.tile_inside(r0, ROWS, k0)) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        v[i] = *reinterpret_cast<const uint4*>(src.at(r0 + c / kRowChunks,
+                                                      k0 + (c % kRowChunks) * 8));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        const int r = r0 + c / kRowChunks;
+        const int k = k0 + (c % kRowChunks) * 8;
+        if (r < src.rows && src.col_ok(k) && src.col_ok(k + 7)) {
+          v[i] = *reinterpret_cast<const uint4*>(src.at(r, k));
+        } else if (r < src.rows && src.col_ok(k)) {
+          union {
+            uint4 u;
+            _Float16 h[8];
+          } t;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t.h[e] = src.col_ok(k + e) ? *src.at(r, k + e) : _Float16(0);
+          v[i] = t.u;
+        } else {
+          v[i] = zero4();
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint4* lds) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      const int row = c / kRowChunks;
+      lds[row * kRowChunks + ((c % kRowChunks) ^ (row & 7))] = v[i];
+    }
+  }
+};
+
+__device__ __forceinline__ half8 frag(const uint4* lds, int row, int ch) {
+  return __builtin_bit_cast(half8, lds[row * kRowChunks + (ch ^ (row & 7))]);
+}
+
+// Workgroup -> (tile_m, tile_n), tile_n fastest. With remap (grid a multiple of 8), logical tile
+// ids are laid out so that consecutive ones run on the same XCD (hardware dispatches workgroup
+// ids round-robin over the 8 XCDs), so workgroups that share operand tiles share an L2.
+__device__ __forceinline__ void tile_of_block(int tiles_n, int remap, int& tm, int& tn) {
+  int bid = blockIdx.x;
+  if (remap) {
+    const int per = gridDim.x / 8;
+    bid = (bid % 8) * per + bid / 8;
+  }
+  tm = bid / tiles_n;
+  tn = bid % tiles_n;
+}
+
+// acc[mt][nt][r] of wavefront (wm, wn) holds
+//   row m = m0 + wm * BM/WM + 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4
+//   col n = n0 + wn * BN/WN + 32 nt + lane % 32
+// The K range [k_begin, k_end) is a multiple of 64 except at the end of the operands.
+template <int BM, int BN, int WM, int WN, int STAGES, class SrcA, class SrcB, class Epi>
+__device__ __forceinline__ void gemm_body(const SrcA& A, const SrcB& B, int k_begin, int k_end,
+                                          int tm, int tn, Epi& epi, uint4* lds) {
+  static_assert(WM * WN == kThreads / kWave, "four wavefronts");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles are multiples of 32");
+  constexpr int kStage = (BM + BN) * kRowChunks;  // uint4 per stage
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / WN, wn = wave % WN;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  TileLoad<BM> la;
+  TileLoad<BN> lb;
+  la.load(A, m0, k_begin);
+  lb.load(B, n0, k_begin);
+  la.store(lds);
+  lb.store(lds + BM * kRowChunks);
+  __syncthreads();
+
+  const int kt_count = (k_end - k_begin + kBK - 1) / kBK;
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int cur = STAGES == 2 ? (kt & 1) : 0;
+    const bool more = kt + 1 < kt_count;
+    if (more) {
+      la.load(A, m0, k_begin + (kt + 1) * kBK);
+      lb.load(B, n0, k_begin + (kt + 1) * kBK);
+    }
+    const uint4* As = lds + cur * kStage;
+    const uint4* Bs = As + BM * kRowChunks;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int ch = ks * 2 + lane / 32;
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = frag(As, wm * WTM + i * 32 + lane % 32, ch);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = frag(Bs, wn * WTN + j * 32 + lane % 32, ch);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      if (STAGES == 1) __syncthreads();  // every wavefront is done reading the single buffer
+      uint4* nxt = lds + (STAGES == 2 ? (cur ^ 1) * kStage : 0);
+      la.store(nxt);
+      lb.store(nxt + BM * kRowChunks);
+    }
+    __syncthreads();
+  }
+  epi.template apply<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
+}
+
+}  // namespace gemm
+}  // namespace cm

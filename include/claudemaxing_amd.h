@@ -166,17 +166,18 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
  *   grad (if not NULL) [n_rows, H] fp32 = grad_scale * sum_v (softmax_v - [v == t_r]) W[v,:]
  *     (zero rows for unlabelled targets)
  * hidden fp16 [n_rows, H] (row stride ld_h), W fp16 [V, H] (row stride ld_w), target int64.
- * weight_t (may be NULL) is W transposed, fp16 [H, V] with row stride ld_wt; without it the
- * gradient pass transposes each weight chunk into the workspace. H, ld_h, ld_w, ld_wt must be
- * multiples of 8 and the bases 16-byte aligned.
+ * weight_t (may be NULL) is W transposed in 64-row panels: fp16 [ceil(V/64), H, 64] with
+ * weight_t[p][h][j] = W[64 p + j][h] and zeros for 64 p + j >= V; without it the gradient pass
+ * transposes each weight chunk into the workspace. H, ld_h, ld_w must be multiples of 8 and the
+ * bases 16-byte aligned.
  * The vocabulary is walked in chunks of chunk_cols columns (0 = the library's default); the
  * result does not depend on the chunk size beyond fp32 rounding.
  * workspace: device memory of cm_lmhead_ce_workspace_bytes(n_rows, V, H, chunk_cols) bytes,
  * 256-B aligned.
  */
 int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-                 const void* weight_t, int64_t ld_wt, const int64_t* target, int64_t n_rows,
-                 int64_t vocab, int hidden_size,
+                 const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
+                 int hidden_size,
                  int64_t chunk_cols, float* loss, float* entropy, int32_t* correct, float* grad,
                  float grad_scale, void* workspace, int64_t workspace_bytes, void* stream);
 /* Workspace bytes cm_lmhead_ce needs for these sizes (chunk_cols as passed to cm_lmhead_ce). */
