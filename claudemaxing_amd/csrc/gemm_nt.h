@@ -6,8 +6,8 @@
 //   Blocked64 element (r, k) at p[((k / 64) * rows + r) * 64 + k % 64], i.e. 64-column panels,
 //             so a (rows x 64) tile of one panel is a single contiguous span. Panels are padded
 //             to 64 columns (the padding must hold finite values; the LM head keeps zeros there).
-// Each pipeline stage moves a BM x 64 tile of A and a BN x 64 tile of B global -> registers ->
-// LDS with 16-byte accesses. Tiles entirely inside the matrices take a branch-free path (one
+// A workgroup has WM x WN wavefronts (4 or 8). Each pipeline stage moves a BM x 64 tile of A and
+// a BN x 64 tile of B global -> registers -> LDS with 16-byte accesses. Tiles entirely inside the matrices take a branch-free path (one
 // scalar test per tile); edge tiles fall back to per-element bounds checks. LDS rows of 64 fp16
 // (128 B = 8 chunks of 16 B) are XOR-swizzled (chunk ^ row % 8): the fragment reads of 8
 // consecutive rows hit all 32 banks. With STAGES = 2 the LDS is double-buffered (one barrier per
@@ -23,7 +23,6 @@ namespace gemm {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;        // 4 wavefronts per workgroup
 constexpr int kBK = 64;              // K elements per stage
 constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per tile row
 
@@ -57,25 +56,38 @@ struct Blocked64 {
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
-template <int ROWS>
+// Identity operand transform (tile data goes to LDS unchanged).
+struct NoXform {
+  __device__ __forceinline__ void prepare(int, int) {}
+  __device__ __forceinline__ void apply(uint4&, int) const {}
+};
+// An A transform X sees chunk i of the calling thread (tile row (threadIdx.x + i THREADS) / 8)
+// through X::apply(chunk, i); X::prepare(m0, tile_rows) runs once per workgroup.
+
+template <int ROWS, int THREADS>
 struct TileLoad {
-  static constexpr int kPer = ROWS * kRowChunks / kThreads;
-  static_assert(kPer * kThreads == ROWS * kRowChunks, "tile rows must split over the threads");
+  static constexpr int kPer = ROWS * kRowChunks / THREADS;
+  static_assert(kPer * THREADS == ROWS * kRowChunks, "tile rows must split over the threads");
   uint4 v[kPer];
+
+  // Row of the tile that chunk i of this thread belongs to.
+  static __device__ __forceinline__ int row_of(int i) {
+    return (threadIdx.x + i * THREADS) / kRowChunks;
+  }
 
   template <class Src>
   __device__ __forceinline__ void load(const Src& src, int r0, int k0) {
     if (src.tile_inside(r0, ROWS, k0)) {
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const int c = threadIdx.x + i * kThreads;
+        const int c = threadIdx.x + i * THREADS;
         v[i] = *reinterpret_cast<const uint4*>(src.at(r0 + c / kRowChunks,
                                                       k0 + (c % kRowChunks) * 8));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const int c = threadIdx.x + i * kThreads;
+        const int c = threadIdx.x + i * THREADS;
         const int r = r0 + c / kRowChunks;
         const int k = k0 + (c % kRowChunks) * 8;
         if (r < src.rows && src.col_ok(k) && src.col_ok(k + 7)) {
@@ -95,10 +107,16 @@ struct TileLoad {
     }
   }
 
+  template <class X>
+  __device__ __forceinline__ void transform(const X& x) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) x.apply(v[i], i);
+  }
+
   __device__ __forceinline__ void store(uint4* lds) const {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = threadIdx.x + i * THREADS;
       const int row = c / kRowChunks;
       lds[row * kRowChunks + ((c % kRowChunks) ^ (row & 7))] = v[i];
     }
@@ -126,10 +144,13 @@ __device__ __forceinline__ void tile_of_block(int tiles_n, int remap, int& tm, i
 //   row m = m0 + wm * BM/WM + 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4
 //   col n = n0 + wn * BN/WN + 32 nt + lane % 32
 // The K range [k_begin, k_end) is a multiple of 64 except at the end of the operands.
-template <int BM, int BN, int WM, int WN, int STAGES, class SrcA, class SrcB, class Epi>
+// XA transforms each A tile in registers before it is written to LDS.
+template <int BM, int BN, int WM, int WN, int STAGES, class SrcA, class SrcB, class Epi,
+          class XA = NoXform>
 __device__ __forceinline__ void gemm_body(const SrcA& A, const SrcB& B, int k_begin, int k_end,
-                                          int tm, int tn, Epi& epi, uint4* lds) {
-  static_assert(WM * WN == kThreads / kWave, "four wavefronts");
+                                          int tm, int tn, Epi& epi, uint4* lds,
+                                          XA xa = XA()) {
+  constexpr int THREADS = WM * WN * kWave;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles are multiples of 32");
@@ -147,10 +168,12 @@ __device__ __forceinline__ void gemm_body(const SrcA& A, const SrcB& B, int k_be
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  TileLoad<BM> la;
-  TileLoad<BN> lb;
+  TileLoad<BM, THREADS> la;
+  TileLoad<BN, THREADS> lb;
+  xa.prepare(m0, BM);
   la.load(A, m0, k_begin);
   lb.load(B, n0, k_begin);
+  la.transform(xa);
   la.store(lds);
   lb.store(lds + BM * kRowChunks);
   __syncthreads();
@@ -182,6 +205,7 @@ __device__ __forceinline__ void gemm_body(const SrcA& A, const SrcB& B, int k_be
     if (more) {
       if (STAGES == 1) __syncthreads();  // every wavefront is done reading the single buffer
       uint4* nxt = lds + (STAGES == 2 ? (cur ^ 1) * kStage : 0);
+      la.transform(xa);
       la.store(nxt);
       lb.store(nxt + BM * kRowChunks);
     }

@@ -11,12 +11,12 @@
 //               statistics (max, sum e^{z-max}, sum e^{z-max} z, first argmax) straight from the
 //               accumulators: in the transposed tile a lane holds the logits of one token.
 //   K2 rows     per token: merge the partials into the running statistics, record the label
-//               logit and the rescale factor e^{lse_before - lse_after}; with a gradient,
-//               overwrite the chunk in place by P = fp16(e^{z - lse_after} * 1024) (zero for
-//               unlabelled tokens; the power-of-two scale keeps the small probabilities of a
-//               152K vocabulary out of fp16's subnormal range).
+//               logit, the running log-sum-exp and the rescale factor e^{lse_before - lse_after}.
 //   K3 grad     G_s = G_s * factor + P W_c for K-slices s of the chunk (split-K over separate fp32
-//               accumulators so the grid fills the chip), on the matrix cores.
+//               accumulators so the grid fills the chip), on the matrix cores, where
+//               P = fp16(e^{z - lse} * 1024) is formed from the fp16 logits while the operand tile
+//               is loaded (zero for unlabelled tokens; the power-of-two scale keeps the small
+//               probabilities of a 152K vocabulary out of fp16's subnormal range).
 //   K4 final    (after the last chunk) lse, loss, entropy, correct; G = scale (sum_s G_s / 1024
 //               - W_t).
 //
@@ -39,27 +39,34 @@ constexpr float kPScale = 1024.0f;  // P16 = fp16(p * kPScale)
 constexpr int kStatThreads = 256;
 constexpr int kMaxSplit = 4;
 
-// Tile configurations (BM, BN, wave grid, LDS stages, workgroups per CU).
+// Tile configurations: BM, BN, wavefront grid WM x WN (4 or 8 wavefronts), LDS stages, and the
+// minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront).
 #ifndef CM_LMH_K1
-#define CM_LMH_K1 0
+#define CM_LMH_K1 3
 #endif
 #ifndef CM_LMH_K3
-#define CM_LMH_K3 0
+#define CM_LMH_K3 3
 #endif
 #if CM_LMH_K1 == 0
 constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 2, kST1 = 2, kOcc1 = 1;
 #elif CM_LMH_K1 == 1
 constexpr int kBM1 = 256, kBN1 = 128, kWM1 = 2, kWN1 = 2, kST1 = 1, kOcc1 = 2;
-#else
+#elif CM_LMH_K1 == 2
 constexpr int kBM1 = 128, kBN1 = 256, kWM1 = 1, kWN1 = 4, kST1 = 1, kOcc1 = 2;
+#else
+constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kST1 = 2, kOcc1 = 2;
 #endif
 #if CM_LMH_K3 == 0
 constexpr int kBM3 = 128, kBN3 = 128, kWM3 = 2, kWN3 = 2, kST3 = 2, kOcc3 = 2;
 #elif CM_LMH_K3 == 1
 constexpr int kBM3 = 256, kBN3 = 128, kWM3 = 2, kWN3 = 2, kST3 = 2, kOcc3 = 1;
+#elif CM_LMH_K3 == 2
+constexpr int kBM3 = 256, kBN3 = 256, kWM3 = 2, kWN3 = 4, kST3 = 2, kOcc3 = 2;
 #else
-constexpr int kBM3 = 128, kBN3 = 256, kWM3 = 2, kWN3 = 2, kST3 = 2, kOcc3 = 1;
+constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 4, kWN3 = 2, kST3 = 2, kOcc3 = 2;
 #endif
+constexpr int kThreads1 = kWM1 * kWN1 * cm::kWave;
+constexpr int kThreads3 = kWM3 * kWN3 * cm::kWave;
 constexpr int kGroup = kBM1 / kWM1;  // vocabulary columns per partial-statistics group
 
 __device__ __forceinline__ int64_t panel_index(int64_t row, int64_t col, int64_t rows) {
@@ -175,13 +182,46 @@ struct EpiGrad {
 // __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD (OCC
 // workgroups of 4 wavefronts per CU), which caps the registers per wavefront accordingly.
 template <class Epi, int BM, int BN, int WM, int WN, int ST, int OCC>
-__global__ __launch_bounds__(cm::gemm::kThreads, OCC) void lmh_gemm1(RowMajor A, RowMajor B,
-                                                                     int remap, Epi epi) {
+__global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm1(RowMajor A, RowMajor B,
+                                                                       int remap, Epi epi) {
   __shared__ uint4 lds[ST * (BM + BN) * cm::gemm::kRowChunks];
   int tm, tn;
   cm::gemm::tile_of_block((B.rows + BN - 1) / BN, remap, tm, tn);
   cm::gemm::gemm_body<BM, BN, WM, WN, ST>(A, B, 0, A.k_len, tm, tn, epi, lds);
 }
+
+// K3's A operand transform: the fp16 logits chunk becomes P = fp16(e^{z - lse} * 1024) for
+// labelled tokens and 0 otherwise, in registers, between the global load and the LDS store.
+// Padding columns of a panel turn into finite values; the weight panels are zero there.
+template <int KPER, int THREADS>
+struct XformP {
+  const float* lse;
+  const int64_t* target;
+  int n_tok;
+  float l[KPER];
+  float on[KPER];
+
+  __device__ __forceinline__ void prepare(int m0, int) {
+#pragma unroll
+    for (int i = 0; i < KPER; ++i) {
+      const int r = m0 + (threadIdx.x + i * THREADS) / cm::gemm::kRowChunks;
+      const bool valid = r < n_tok;
+      l[i] = valid ? lse[r] : 0.0f;
+      on[i] = valid && target[r] != -100 ? kPScale : 0.0f;
+    }
+  }
+  __device__ __forceinline__ void apply(uint4& chunk, int i) const {
+    union {
+      uint4 u;
+      _Float16 h[8];
+    } v;
+    v.u = chunk;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v.h[e] = cm::from_f32<_Float16>(cm::exp_f(static_cast<float>(v.h[e]) - l[i]) * on[i]);
+    chunk = v.u;
+  }
+};
 
 // K3: blockIdx.y is the K-slice; each slice accumulates into its own buffer.
 struct GradSlices {
@@ -189,9 +229,10 @@ struct GradSlices {
 };
 
 template <int BM, int BN, int WM, int WN, int ST, int OCC>
-__global__ __launch_bounds__(cm::gemm::kThreads, OCC) void lmh_gemm3(
+__global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm3(
     Blocked64 A, Blocked64 B, int k_slice, int remap, GradSlices out, int n_tok, int hidden,
-    const float* factor, int first) {
+    const float* factor, int first, const float* lse, const int64_t* target) {
+  constexpr int THREADS = WM * WN * cm::kWave;
   __shared__ uint4 lds[ST * (BM + BN) * cm::gemm::kRowChunks];
   int tm, tn;
   cm::gemm::tile_of_block((B.rows + BN - 1) / BN, remap, tm, tn);
@@ -201,7 +242,8 @@ __global__ __launch_bounds__(cm::gemm::kThreads, OCC) void lmh_gemm3(
   // initialised on the first chunk and rescaled on later ones.
   const int k_end = max(k_begin, min(A.k_len, k_begin + k_slice));
   EpiGrad epi{out.g[s], n_tok, hidden, factor, first};
-  cm::gemm::gemm_body<BM, BN, WM, WN, ST>(A, B, k_begin, k_end, tm, tn, epi, lds);
+  XformP<BM * cm::gemm::kRowChunks / THREADS, THREADS> xp{lse, target, n_tok, {}, {}};
+  cm::gemm::gemm_body<BM, BN, WM, WN, ST>(A, B, k_begin, k_end, tm, tn, epi, lds, xp);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -257,25 +299,7 @@ __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
     rs.factor[row] = first ? 0.0f : cm::exp_f(lse_prev - lse_now);
     if (hit) rs.label_logit[row] = static_cast<float>(s16[panel_index(row, local, n_tok)]);
   }
-  if (!write_p) return;
-  __syncthreads();  // the label logit is read before the row is overwritten
-  // 8-element vectors: vector i covers columns [8i, 8i + 8) of one 64-column panel
-  const int n8 = (n_voc + 7) / 8;
-  for (int i = threadIdx.x; i < n8; i += kStatThreads) {
-    _Float16* v8 = s16 + panel_index(row, 8 * i, n_tok);
-    union {
-      uint4 u;
-      _Float16 h[8];
-    } v;
-    v.u = *reinterpret_cast<const uint4*>(v8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bool valid = labelled && 8 * i + e < n_voc;
-      const float p = valid ? cm::exp_f(static_cast<float>(v.h[e]) - lse_now) * kPScale : 0.0f;
-      v.h[e] = cm::from_f32<_Float16>(p);
-    }
-    *reinterpret_cast<uint4*>(v8) = v.u;
-  }
+  (void)write_p;
 }
 
 // K4: final per-row outputs; G = scale * (sum_s G_s / 1024 - W[t]) for labelled rows, else 0.
@@ -433,7 +457,7 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
       RowMajor B{H16, ld_h, n_tok, hidden_size};
       EpiLogits epi{s16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups)};
       hipLaunchKernelGGL((lmh_gemm1<EpiLogits, kBM1, kBN1, kWM1, kWN1, kST1, kOcc1>), dim3(grid),
-                         dim3(cm::gemm::kThreads), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
+                         dim3(kThreads1), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
       int st = cm::launch_status();
       if (st) return st;
     }
@@ -465,8 +489,9 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
       Blocked64 A{s16, n_tok, n_voc};
       Blocked64 B{wt, hidden_size, n_voc};
       hipLaunchKernelGGL((lmh_gemm3<kBM3, kBN3, kWM3, kWN3, kST3, kOcc3>),
-                         dim3(grid, L.n_split), dim3(cm::gemm::kThreads), 0, s, A, B, k_slice,
-                         grid % 8 == 0 ? 1 : 0, gs, n_tok, hidden_size, rs.factor, first ? 1 : 0);
+                         dim3(grid, L.n_split), dim3(kThreads3), 0, s, A, B, k_slice,
+                         grid % 8 == 0 ? 1 : 0, gs, n_tok, hidden_size, rs.factor, first ? 1 : 0,
+                         rs.lse, target);
       st = cm::launch_status();
       if (st) return st;
     }
