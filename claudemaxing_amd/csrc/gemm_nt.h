@@ -9,8 +9,8 @@
 // A workgroup has WM x WN wavefronts (4 or 8). Each pipeline stage moves a BM x 64 tile of A and
 // a BN x 64 tile of B global -> registers -> LDS with 16-byte accesses. Tiles entirely inside the matrices take a branch-free path (one
 // scalar test per tile); edge tiles fall back to per-element bounds checks. LDS rows of 64 fp16
-// (128 B = 8 chunks of 16 B) are XOR-swizzled (chunk ^ row % 8): the fragment reads of 8
-// consecutive rows hit all 32 banks. With STAGES = 2 the LDS is double-buffered (one barrier per
+// (128 B = 8 chunks of 16 B) are XOR-swizzled so that the fragment reads of a wavefront do not
+// collide on LDS banks (see swz()). With STAGES = 2 the LDS is double-buffered (one barrier per
 // stage, the next stage's global loads overlap this stage's MFMAs); with STAGES = 1 a single LDS
 // buffer halves the footprint so that two workgroups share a CU.
 #pragma once
@@ -25,6 +25,18 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;              // K elements per stage
 constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per tile row
+
+// LDS swizzle: physical 16-byte chunk = logical chunk ^ swz(row). With SHIFT = 0 eight
+// consecutive rows use eight distinct chunks (all 32 banks of a 128-byte span); SHIFT = 1 pairs
+// rows instead (distinct banks for 16 rows of a 64-bank view). Measured on MI355X for the LM
+// head GEMMs, SHIFT = 0 is faster although the bank-conflict counter reads higher.
+#ifndef CM_SCHED_HINTS
+#define CM_SCHED_HINTS 0
+#endif
+#ifndef CM_SWZ_SHIFT
+#define CM_SWZ_SHIFT 0
+#endif
+__device__ __forceinline__ int swz(int row) { return (row >> CM_SWZ_SHIFT) & 7; }
 
 struct RowMajor {
   const _Float16* p;
@@ -118,13 +130,13 @@ struct TileLoad {
     for (int i = 0; i < kPer; ++i) {
       const int c = threadIdx.x + i * THREADS;
       const int row = c / kRowChunks;
-      lds[row * kRowChunks + ((c % kRowChunks) ^ (row & 7))] = v[i];
+      lds[row * kRowChunks + ((c % kRowChunks) ^ swz(row))] = v[i];
     }
   }
 };
 
 __device__ __forceinline__ half8 frag(const uint4* lds, int row, int ch) {
-  return __builtin_bit_cast(half8, lds[row * kRowChunks + (ch ^ (row & 7))]);
+  return __builtin_bit_cast(half8, lds[row * kRowChunks + (ch ^ swz(row))]);
 }
 
 // Workgroup -> (tile_m, tile_n), tile_n fastest. With remap (grid a multiple of 8), logical tile
@@ -188,19 +200,38 @@ __device__ __forceinline__ void gemm_body(const SrcA& A, const SrcB& B, int k_be
     }
     const uint4* As = lds + cur * kStage;
     const uint4* Bs = As + BM * kRowChunks;
+    // Fragments are double-buffered across the four 16-wide K substeps: the LDS reads of
+    // substep ks + 1 are issued before the MFMAs of substep ks, so their latency hides behind
+    // the matrix work instead of stalling it.
+    half8 af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[0][i] = frag(As, wm * WTM + i * 32 + lane % 32, lane / 32);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[0][j] = frag(Bs, wn * WTN + j * 32 + lane % 32, lane / 32);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int ch = ks * 2 + lane / 32;
-      half8 af[TM], bf[TN];
+      const int b = ks & 1;
+      if (ks + 1 < kBK / 16) {
+        const int ch = (ks + 1) * 2 + lane / 32;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = frag(As, wm * WTM + i * 32 + lane % 32, ch);
+        for (int i = 0; i < TM; ++i) af[b ^ 1][i] = frag(As, wm * WTM + i * 32 + lane % 32, ch);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = frag(Bs, wn * WTN + j * 32 + lane % 32, ch);
+        for (int j = 0; j < TN; ++j) bf[b ^ 1][j] = frag(Bs, wn * WTN + j * 32 + lane % 32, ch);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[b][i], bf[b][j], acc[i][j], 0,
+                                                             0, 0);
+#if CM_SCHED_HINTS
+      // interleave: one LDS fragment read between consecutive MFMAs
+#pragma unroll
+      for (int g = 0; g < TM * TN; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+#endif
     }
     if (more) {
       if (STAGES == 1) __syncthreads();  // every wavefront is done reading the single buffer

@@ -10,8 +10,10 @@
 // Work split: a lane handles 4-byte units (8 outputs, one 16-byte fp16 store), all 8 in one
 // absmax block because blocksize >= 32. A workgroup of 256 lanes handles UNITS consecutive
 // 1 KiB slices of the packed weight, so every load and store instruction of a wavefront covers
-// one contiguous span (256 B in, 1 KiB out for fp16). The 16-entry code table sits in LDS:
-// the 16 entries fall in 16 distinct banks, so the per-lane lookups never conflict.
+// one contiguous span (256 B in, 1 KiB out for fp16). The fp16 outputs go out as nontemporal
+// stores (measured on MI355X: 8.7 -> 7.5 us on the [8960,1536] weight, cold caches). The
+// 16-entry code table sits in LDS: the 16 entries fall in 16 distinct banks, so the per-lane
+// lookups never conflict.
 #include "common.h"
 
 namespace {
@@ -21,13 +23,13 @@ namespace {
 
 constexpr int kThreads = 256;
 #ifndef CM_NF4_UNITS
-#define CM_NF4_UNITS 4
+#define CM_NF4_UNITS 8
 #endif
 #ifndef CM_NF4_WIDE
 #define CM_NF4_WIDE 0
 #endif
 #ifndef CM_NF4_NT_STORE
-#define CM_NF4_NT_STORE 0
+#define CM_NF4_NT_STORE 1
 #endif
 constexpr int kUnits = CM_NF4_UNITS;  // 4-byte units per lane
 

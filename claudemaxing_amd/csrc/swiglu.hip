@@ -10,14 +10,18 @@
 // elements per vector (16-byte fp16 accesses), UNITS vectors per lane, 256 lanes per workgroup;
 // consecutive lanes touch consecutive 16-byte vectors so each wavefront access is one
 // contiguous 1 KiB span. 2^x is v_exp_f32 and 1/x is v_rcp_f32 (about 1 ulp each; the
-// reference's Triton exp2 and division are not correctly rounded either).
+// reference's Triton exp2 and division are not correctly rounded either). Every input element
+// is read exactly once, so loads and stores are both nontemporal.
+#ifndef CM_VEC_NT_LOAD
+#define CM_VEC_NT_LOAD 1
+#endif
 #include "vec.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 #ifndef CM_SWIGLU_UNITS
-#define CM_SWIGLU_UNITS 2
+#define CM_SWIGLU_UNITS 1
 #endif
 constexpr int kUnits = CM_SWIGLU_UNITS;
 constexpr float kNegLog2e = -1.4426950408889634f;

@@ -5,7 +5,43 @@
 
 #include "common.h"
 
+// Streaming hints for the aligned 16-byte accesses: with CM_VEC_NT_STORE / CM_VEC_NT_LOAD set,
+// they are issued as nontemporal (streaming) accesses. Measured on MI355X with cold caches,
+// nontemporal stores speed up every elementwise kernel here (SwiGLU forward 21.0 -> 18.6 us,
+// RMSNorm backward 8.0 -> 6.5 us, LoRA unpack 5.7 -> 4.9 us); nontemporal loads help only
+// kernels that read each input once (SwiGLU backward 35.8 -> 30.9 us) and slow RMSNorm, which
+// reads its rows twice, so a file opts into them by defining CM_VEC_NT_LOAD before this header.
+#ifndef CM_VEC_NT_STORE
+#define CM_VEC_NT_STORE 1
+#endif
+#ifndef CM_VEC_NT_LOAD
+#define CM_VEC_NT_LOAD 0
+#endif
+
 namespace cm {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes at p (16-byte aligned), as any 16-byte type V.
+template <typename V>
+__device__ __forceinline__ V load16(const void* p) {
+  static_assert(sizeof(V) == 16, "16-byte accesses only");
+#if CM_VEC_NT_LOAD
+  return __builtin_bit_cast(V, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
+#else
+  return __builtin_bit_cast(V, *static_cast<const u32x4*>(p));
+#endif
+}
+
+template <typename V>
+__device__ __forceinline__ void store16(void* p, V v) {
+  static_assert(sizeof(V) == 16, "16-byte accesses only");
+#if CM_VEC_NT_STORE
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), static_cast<u32x4*>(p));
+#else
+  *static_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v);
+#endif
+}
 
 template <typename T, bool ALIGNED>
 struct Vec8 {
@@ -26,7 +62,7 @@ struct Vec8<_Float16, true> {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   static __device__ __forceinline__ void load(const _Float16* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const h8 h = *reinterpret_cast<const h8*>(p);
+      const h8 h = load16<h8>(p);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(h[i]);
     } else {
@@ -38,7 +74,7 @@ struct Vec8<_Float16, true> {
       h8 h;
 #pragma unroll
       for (int i = 0; i < 8; ++i) h[i] = from_f32<_Float16>(v[i]);
-      *reinterpret_cast<h8*>(p) = h;
+      store16(p, h);
     } else {
       Vec8<_Float16, false>::store(p, v, cnt);
     }
@@ -49,7 +85,7 @@ template <>
 struct Vec8<bf16_t, true> {
   static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const uint4 w = *reinterpret_cast<const uint4*>(p);
+      const uint4 w = load16<uint4>(p);
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -67,7 +103,7 @@ struct Vec8<bf16_t, true> {
       for (int i = 0; i < 4; ++i)
         u[i] = static_cast<uint32_t>(from_f32<bf16_t>(v[2 * i]).bits) |
                (static_cast<uint32_t>(from_f32<bf16_t>(v[2 * i + 1]).bits) << 16);
-      *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+      store16(p, make_uint4(u[0], u[1], u[2], u[3]));
     } else {
       Vec8<bf16_t, false>::store(p, v, cnt);
     }
@@ -78,8 +114,8 @@ template <>
 struct Vec8<float, true> {
   static __device__ __forceinline__ void load(const float* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const float4 a = reinterpret_cast<const float4*>(p)[0];
-      const float4 b = reinterpret_cast<const float4*>(p)[1];
+      const float4 a = load16<float4>(p);
+      const float4 b = load16<float4>(p + 4);
       v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
       v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
@@ -88,8 +124,8 @@ struct Vec8<float, true> {
   }
   static __device__ __forceinline__ void store(float* p, const float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
-      reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+      store16(p, make_float4(v[0], v[1], v[2], v[3]));
+      store16(p + 4, make_float4(v[4], v[5], v[6], v[7]));
     } else {
       Vec8<float, false>::store(p, v, cnt);
     }
