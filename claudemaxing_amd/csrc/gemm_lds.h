@@ -1,0 +1,259 @@
+// fp16 "NT" GEMM core on the gfx950 matrix cores with direct global -> LDS loads:
+// C[m][n] = sum_k A[m][k] B[n][k], fp32 accumulation in v_mfma_f32_32x32x16_f16 tiles, the
+// accumulators handed to an epilogue functor.
+//
+// Operand tiles travel HBM/L2 -> LDS through global_load_lds_dwordx4: the data never passes
+// through VGPRs, so the load path costs one issue slot per 16 bytes and no registers. Each
+// such instruction writes 64 consecutive 16-byte LDS slots (M0 base + 16 * lane); the XOR
+// swizzle of the LDS rows (swz()) is therefore applied on the global side: the lane that owns
+// LDS slot (row, physical chunk) fetches logical chunk physical ^ swz(row) of that row.
+// Chunks outside the operands (rows past the end, columns past k_len) are fetched from a
+// 16-byte zero block instead, so edge tiles need no separate path (hidden sizes are multiples
+// of 8, so a 16-byte chunk is either wholly inside or wholly outside).
+//
+// The LDS holds a ring of S stages of BK (64 or 32) columns; stages kt + 1 .. kt + S - 1 are in
+// flight while stage kt is multiplied. One barrier per stage: after it every wavefront has finished reading stage
+// kt - 1 (so its buffer can be refilled) and every wavefront's loads of stage kt have landed.
+//
+// An A-fragment transform FX may rescale each 8-element A fragment between the LDS read and the
+// MFMA (used by the LM head's gradient GEMM to turn stored e^{z - m} into probabilities). The
+// epilogue's prepare() runs before the main loop (to issue its own loads early); apply() receives
+// the accumulators and the LDS ring, which it may reuse after a barrier.
+#pragma once
+
+#include "common.h"
+#include "gemm_nt.h"
+
+namespace cm {
+namespace gemm {
+
+// Source of the chunks that lie outside an operand.
+static __device__ const uint4 kZeroChunk[1] = {{0u, 0u, 0u, 0u}};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One global_load_lds_dwordx4: 64 lanes x 16 bytes into 64 consecutive 16-byte LDS slots from
+// lds_slot0 (wave-uniform, passed in M0). Issued through inline assembly: the compiler models the
+// builtin like a FLAT access that may complete out of order with LDS reads, and then turns every
+// later fragment wait into lgkmcnt(0), which ties the LDS reads of each substep to the freshly
+// issued ds_reads. Completion of these loads is waited for explicitly (wait_vmcnt before the
+// stage barrier); a counter the compiler does not know about can only make its own waits
+// longer, never shorter.
+// M0 is set inside the statement; no other code in these kernels keeps a value in M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint4* lds_slot0) {
+  const uint32_t m0v = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)lds_slot0));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(m0v), "v"(g)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS tile rows of BK fp16 = BK / 8 chunks of 16 bytes. Physical chunk = logical chunk ^
+// swz(row), chosen for the 64 banks of 4 bytes of the gfx950 LDS: a ds_read_b128 is served 16
+// lanes (256 bytes) at a time, and the 16 lanes of a fragment read are 16 consecutive rows at
+// one logical chunk, so those rows must land in 16 distinct 16-byte bank groups. With 8-chunk
+// rows the row parity already picks the half of the 256-byte bank span and (row >> 1) & 7 the
+// chunk; with 4-chunk rows row & 3 picks the quarter and (row >> 2) & 3 the chunk.
+template <int BK>
+struct LdsRows {
+  static constexpr int kRC = BK / 8;
+  static_assert(kRC == 8 || kRC == 4, "stages of 64 or 32 columns");
+  static __device__ __forceinline__ int swz(int row) {
+    return kRC == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+  }
+  static __device__ __forceinline__ half8 frag(const uint4* lds, int row, int ch) {
+    return __builtin_bit_cast(half8, lds[row * kRC + (ch ^ swz(row))]);
+  }
+};
+
+// Direct loads of one ROWS x BK operand tile by NW wavefronts. Each lane keeps the 32-bit byte
+// offsets of its chunks relative to the tile's origin; a stage's origin is a wave-uniform
+// pointer, so a load is a scalar base plus a constant lane offset. Tiles that are wholly inside
+// the operand take that path; the others select the zero chunk per lane.
+template <int ROWS, int NW, int BK>
+struct DmaTile {
+  using L = LdsRows<BK>;
+  static constexpr int kChunks = ROWS * L::kRC;
+  static constexpr int kPer = kChunks / (NW * kWave);  // instructions per lane
+  static_assert(kPer * NW * kWave == kChunks, "tile chunks must split over the wavefronts");
+  uint32_t off[kPer];  // byte offset of the lane's chunk from the stage origin
+  int row[kPer];       // tile row of the chunk
+  int col[kPer];       // column of the chunk within the stage
+
+  template <class Src>
+  __device__ __forceinline__ void init(const Src& src, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = (i * NW + wave) * kWave + lane;
+      row[i] = c / L::kRC;
+      col[i] = ((c % L::kRC) ^ L::swz(row[i])) * 8;
+      off[i] = src.tile_offset(row[i], col[i]);
+    }
+  }
+
+  // Instruction i of the stage whose origin is (r0, k0); `inside` = the tile is wholly inside
+  // the operand (one wave-uniform test per stage).
+  template <class Src>
+  __device__ __forceinline__ void issue(const Src& src, int r0, int k0, uint4* tile, int wave,
+                                        int i, bool inside) const {
+    const char* base = reinterpret_cast<const char*>(src.at(r0, k0));
+    const bool ok = inside || (r0 + row[i] < src.rows && src.col_ok(k0 + col[i]));
+    const void* g = ok ? static_cast<const void*>(base + off[i])
+                       : static_cast<const void*>(kZeroChunk);
+    dma16(g, tile + (i * NW + wave) * kWave);
+  }
+};
+
+// Workgroup barrier that orders LDS only: the loads into LDS are waited for explicitly
+// (vmcnt), so the barrier must not wait for every outstanding global load.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Identity A-fragment transform with no per-stage data (the default FX of gemm_lds). An FX
+// provides bind(row) (the A row of the calling lane's fragment 0; fragment i is row + 32 i),
+// prefetch(k0) (register loads for the stage at column k0, issued one stage ahead),
+// advance() (the prefetched values become current) and apply(frag, i) on the A fragment of the
+// wavefront's tile row i.
+struct PlainA {
+  __device__ __forceinline__ void bind(int) {}
+  __device__ __forceinline__ void prefetch(int) {}
+  __device__ __forceinline__ void advance() {}
+  __device__ __forceinline__ half8 apply(half8 f, int) const { return f; }
+};
+
+// Main loop, per stage kt: wait until stage kt has landed, one barrier (stage kt visible; every
+// wavefront is done with stage kt - 1, whose buffer is refilled next), then for each 16-column
+// substep: read the next substep's fragments, issue half of the MFMAs, issue this substep's
+// share of the loads of stage kt + S - 1, issue the other half of the MFMAs. Spreading the
+// LDS-direct loads between MFMAs keeps the texture unit's queue short, so a wavefront never
+// stalls in issue with the matrix core idle (issued as one burst after the barrier, the loads
+// of a 256 x 256 x 64 stage held every wavefront for ~1000 cycles). sched_barrier pins that order.
+template <int BM, int BN, int WM, int WN, int BK, int S, class SrcA, class SrcB, class Epi,
+          class FX = PlainA>
+__device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_begin, int k_end,
+                                         int tm, int tn, Epi& epi, uint4* lds, FX fx = FX()) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  using L = LdsRows<BK>;
+  constexpr int KS = BK / 16;  // MFMA substeps per stage
+  static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles are multiples of 32");
+  static_assert(S >= 2, "at least a double buffer");
+  constexpr int kStage = (BM + BN) * L::kRC;  // uint4 per stage
+  using TA = DmaTile<BM, NW, BK>;
+  using TB = DmaTile<BN, NW, BK>;
+  constexpr int kDma = TA::kPer + TB::kPer;     // LDS-direct loads per lane per stage
+  constexpr int kPart = (kDma + KS - 1) / KS;   // of them issued per substep
+  constexpr int kHalf = (TM * TN) / 2;          // MFMAs before the loads of a substep
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave / WN, wn = wave % WN;
+  TA la;
+  TB lb;
+  la.init(A, wave, lane);
+  lb.init(B, wave, lane);
+  epi.template prepare<TM, TN>(m0 + wm * WTM, n0 + wn * WTN, lane);
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int n_kt = (k_end - k_begin + BK - 1) / BK;
+  // load instruction q (< kDma) of stage kt: A's instructions first, then B's
+  auto issue = [&](int kt, int q, bool in_a, bool in_b) {
+    uint4* st = lds + (kt % S) * kStage;
+    const int k0 = k_begin + kt * BK;
+    if (q < TA::kPer) {
+      la.issue(A, m0, k0, st, wave, q, in_a);
+    } else {
+      lb.issue(B, n0, k0, st + BM * L::kRC, wave, q - TA::kPer, in_b);
+    }
+  };
+  auto inside_a = [&](int kt) { return A.tile_inside(m0, BM, k_begin + kt * BK); };
+  auto inside_b = [&](int kt) { return B.tile_inside(n0, BN, k_begin + kt * BK); };
+  const int arow = wm * WTM + lane % 32, brow = wn * WTN + lane % 32;
+  half8 af[2][TM], bf[2][TN];
+  auto read = [&](int kt, int ks, int buf) {
+    const uint4* As = lds + (kt % S) * kStage;
+    const uint4* Bs = As + BM * L::kRC;
+    const int ch = ks * 2 + lane / 32;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[buf][i] = fx.apply(L::frag(As, arow + i * 32, ch), i);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[buf][j] = L::frag(Bs, brow + j * 32, ch);
+  };
+  auto mfma = [&](int b, int g0, int g1) {
+#pragma unroll
+    for (int g = g0; g < g1; ++g) {
+      const int i = g / TN, j = g % TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[b][i], bf[b][j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // Prologue: stages 0 .. S - 2 in flight (the FX prefetch of stage 0 first).
+  fx.bind(m0 + wm * WTM + lane % 32);
+  if (n_kt > 0) fx.prefetch(k_begin);
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) {
+    if (s < n_kt) {
+      const bool ia = inside_a(s), ib = inside_b(s);
+#pragma unroll
+      for (int q = 0; q < kDma; ++q) issue(s, q, ia, ib);
+    }
+  }
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    // stage kt has landed once at most the loads of stages kt + 1 .. kt + S - 2 are outstanding
+    if (kt + S - 2 < n_kt) {
+      wait_vmcnt<(S - 2) * kDma>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    fx.advance();
+    if (kt + 1 < n_kt) fx.prefetch(k_begin + (kt + 1) * BK);
+    const int kl = kt + S - 1;  // the stage loaded during this one
+    const bool load = kl < n_kt;
+    const bool ia = load && inside_a(kl), ib = load && inside_b(kl);
+    read(kt, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int b = ks & 1;
+      if (ks + 1 < KS) read(kt, ks + 1, b ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(b, 0, kHalf);
+      __builtin_amdgcn_sched_barrier(0);
+      if (load) {
+#pragma unroll
+        for (int q = ks * kPart; q < (ks + 1) * kPart; ++q)
+          if (q < kDma) issue(kl, q, ia, ib);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(b, kHalf, TM * TN);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  epi.template apply<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds);
+}
+
+}  // namespace gemm
+}  // namespace cm

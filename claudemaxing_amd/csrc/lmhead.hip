@@ -5,33 +5,38 @@
 // chunk torch.mm -> lm_head_vocab_chunk_kernel (108-160) -> torch.mm, then the label fix-up
 // 230-236). The vocabulary is walked in chunks of C columns; per chunk, on the caller's stream:
 //
-//   K1 logits   Z^T = W_c H^T on the matrix cores (csrc/gemm_nt.h). The epilogue rounds every
-//               logit to fp16 (the base path's fp16 logits), stores the chunk, and reduces each
-//               token's logits of the wavefront's vocabulary slice to partial online-softmax
-//               statistics (max, sum e^{z-max}, sum e^{z-max} z, first argmax) straight from the
-//               accumulators: in the transposed tile a lane holds the logits of one token.
-//   K2 rows     per token: merge the partials into the running statistics, record the label
-//               logit, the running log-sum-exp and the rescale factor e^{lse_before - lse_after}.
+//   K1 logits   Z^T = W_c H^T on the matrix cores (csrc/gemm_lds.h). The epilogue rounds every
+//               logit to fp16 (the base path's fp16 logits) and reduces each token's logits of
+//               the wavefront's 128-column vocabulary group to partial online-softmax statistics
+//               (group max m_g, sum e^{z-m_g}, sum e^{z-m_g} z, first argmax) straight from the
+//               accumulators: in the transposed tile a lane holds the logits of one token. It
+//               stores E = fp16(e^{z - m_g}) for the gradient, and the label's logit.
+//   K2 rows     per token: merge the partials into the running statistics, record the running
+//               log-sum-exp and the rescale factor e^{lse_before - lse_after}, and turn each
+//               group max into the group's probability scale s_g = e^{m_g - lse} * 1024 (zero
+//               for unlabelled tokens).
 //   K3 grad     G_s = G_s * factor + P W_c for K-slices s of the chunk (split-K over separate fp32
 //               accumulators so the grid fills the chip), on the matrix cores, where
-//               P = fp16(e^{z - lse} * 1024) is formed from the fp16 logits while the operand tile
-//               is loaded (zero for unlabelled tokens; the power-of-two scale keeps the small
-//               probabilities of a 152K vocabulary out of fp16's subnormal range).
+//               P = E * s_g (= e^{z - lse} * 1024 in fp16) is formed from each A fragment with
+//               packed fp16 multiplies between the LDS read and the MFMA. The power-of-two scale
+//               keeps the small probabilities of a 152K vocabulary out of fp16's subnormal
+//               range.
 //   K4 final    (after the last chunk) lse, loss, entropy, correct; G = scale (sum_s G_s / 1024
 //               - W_t).
 //
-// The full [tokens, vocab] logits never exist: one fp16 chunk lives in the workspace, sized so
-// that it, the weight chunk and its transpose stay inside the 256 MB Infinity Cache. The chunk
-// and the transposed weight are stored in 64-column panels ([C/64][tokens][64],
+// The full [tokens, vocab] logits never exist: one fp16 chunk of E lives in the workspace, sized
+// so that it, the weight chunk and its transpose stay inside the 256 MB Infinity Cache. The
+// chunk and the transposed weight are stored in 64-column panels ([C/64][tokens][64],
 // [V/64][H][64]) so that every K3 operand tile is one contiguous 16 KiB read.
 #include "common.h"
-#include "gemm_nt.h"
+#include "gemm_lds.h"
 #include "softmax_state.h"
 
 namespace {
 
 using cm::gemm::Blocked64;
 using cm::gemm::floatx16;
+using cm::gemm::half8;
 using cm::gemm::RowMajor;
 
 constexpr int kPanel = 64;          // columns per panel of the blocked layouts
@@ -39,112 +44,171 @@ constexpr float kPScale = 1024.0f;  // P16 = fp16(p * kPScale)
 constexpr int kStatThreads = 256;
 constexpr int kMaxSplit = 4;
 
-// Tile configurations: BM, BN, wavefront grid WM x WN (4 or 8 wavefronts), LDS stages, and the
-// minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront).
+// Tile configurations: BM, BN, wavefront grid WM x WN, stage depth BK, LDS ring stages, and the
+// minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront:
+// 2 gives 256, 1 gives 512). Variant 0 is the default; variant 1 of each is the alternative
+// measured beside it (a deeper ring of 32-column stages; for K3 four wavefronts of 128 x 96).
 #ifndef CM_LMH_K1
-#define CM_LMH_K1 3
+#define CM_LMH_K1 0
 #endif
 #ifndef CM_LMH_K3
-#define CM_LMH_K3 3
+#define CM_LMH_K3 0
 #endif
-#if CM_LMH_K1 == 0
-constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 2, kST1 = 2, kOcc1 = 1;
-#elif CM_LMH_K1 == 1
-constexpr int kBM1 = 256, kBN1 = 128, kWM1 = 2, kWN1 = 2, kST1 = 1, kOcc1 = 2;
-#elif CM_LMH_K1 == 2
-constexpr int kBM1 = 128, kBN1 = 256, kWM1 = 1, kWN1 = 4, kST1 = 1, kOcc1 = 2;
+#if CM_LMH_K1 == 1
+constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 32, kST1 = 4, kOcc1 = 2;
 #else
-constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kST1 = 2, kOcc1 = 2;
+constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 64, kST1 = 2, kOcc1 = 2;
 #endif
-#if CM_LMH_K3 == 0
-constexpr int kBM3 = 128, kBN3 = 128, kWM3 = 2, kWN3 = 2, kST3 = 2, kOcc3 = 2;
-#elif CM_LMH_K3 == 1
-constexpr int kBM3 = 256, kBN3 = 128, kWM3 = 2, kWN3 = 2, kST3 = 2, kOcc3 = 1;
-#elif CM_LMH_K3 == 2
-constexpr int kBM3 = 256, kBN3 = 256, kWM3 = 2, kWN3 = 4, kST3 = 2, kOcc3 = 2;
+#if CM_LMH_K3 == 1
+constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 2, kWN3 = 2, kBK3 = 32, kST3 = 4, kOcc3 = 1;
 #else
-constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 4, kWN3 = 2, kST3 = 2, kOcc3 = 2;
+constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 4, kWN3 = 2, kBK3 = 64, kST3 = 2, kOcc3 = 2;
 #endif
 constexpr int kThreads1 = kWM1 * kWN1 * cm::kWave;
 constexpr int kThreads3 = kWM3 * kWN3 * cm::kWave;
 constexpr int kGroup = kBM1 / kWM1;  // vocabulary columns per partial-statistics group
+static_assert(kGroup % kPanel == 0, "a statistics group is whole panels");
 
 __device__ __forceinline__ int64_t panel_index(int64_t row, int64_t col, int64_t rows) {
   return ((col / kPanel) * rows + row) * kPanel + col % kPanel;
 }
 
-// Partial statistics of one (token, group): max, sum, dot, first argmax (-1 when empty).
+// Partial statistics of one (token, group): group max, sum e^{z - max}, sum e^{z - max} z, first
+// argmax as a vocabulary index (-1 when the group holds no valid column).
 struct Partial {
   float max, sum, dot;
   int32_t best;
 };
 
 // ---------------------------------------------------------------------------------------------
-// K1 epilogue: the tile is Z^T (rows = vocabulary columns of the chunk, cols = tokens).
-struct EpiLogits {
-  _Float16* s16;  // chunk, panels [C/64][n_tok][64]
+// K1 epilogue: the tile is Z^T (rows = vocabulary columns of the chunk, cols = tokens). A
+// wavefront's rows are one statistics group of kGroup columns. E is staged in the LDS in the
+// output's panel layout and written with 16-byte stores, 1 KiB contiguous per wavefront
+// instruction: the tile's BM vocabulary rows are BM / 64 panels, and in each the BN tokens are one
+// contiguous span of BN x 128 bytes.
+struct EpiProbs {
+  static constexpr int kTN = kBN1 / kWN1 / 32;
+  _Float16* e16;        // chunk of E = fp16(e^{z - m_g}), panels [C/64][n_tok][64]
   int n_tok;
-  int n_voc;      // valid columns of the chunk
-  int64_t c0;     // first vocabulary index of the chunk
-  Partial* part;  // [n_tok, n_groups]
+  int n_voc;            // valid columns of the chunk
+  int64_t c0;           // first vocabulary index of the chunk
+  Partial* part;        // [n_tok, n_groups]
   int n_groups;
+  const int64_t* target;
+  float* label_logit;   // [n_tok]: z of the label, written by the one lane that holds it
+  int store;            // write E (the gradient needs it)
+  int64_t tgt[kTN];     // targets of the lane's tokens, loaded before the main loop
+
+  // 16-byte chunk slot of (token t, chunk c) within the staging rows of panel p: rows of 128
+  // bytes, chunk XOR-swizzled by the token so that 16 consecutive tokens hit distinct banks.
+  static __device__ __forceinline__ int stage_slot(int p, int t, int c) {
+    return (p * kBN1 + t) * 8 + (c ^ ((t >> 1) & 7));
+  }
 
   template <int TM, int TN>
-  __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb,
-                                        int lane) const {
-    static_assert(TM * 32 == kGroup, "a wavefront covers one statistics group");
-    const int half_id = lane / 32;
+  __device__ __forceinline__ void prepare(int, int nb, int lane) {
+    static_assert(TN == kTN, "epilogue configured for K1's wavefront tile");
 #pragma unroll
     for (int nt = 0; nt < TN; ++nt) {
       const int tok = nb + nt * 32 + lane % 32;
-      // fp16 logits of this lane's token, rows in increasing vocabulary order
+      tgt[nt] = tok < n_tok ? target[tok] : int64_t{-100};
+    }
+  }
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb, int lane,
+                                        uint4* lds) {
+    static_assert(TM * 32 == kGroup, "a wavefront covers one statistics group");
+    static_assert(kBM1 * kBN1 * 2 <= kST1 * (kBM1 + kBN1) * kBK1 * 2,
+                  "the E tile is staged in the LDS ring");
+    const int half_id = lane / 32;
+    const int m0 = mb - mb % kBM1, n0 = nb - nb % kBN1;  // tile origin
+    // accumulator element e of a lane is vocabulary row mb + vrow(e)
+    auto vrow = [&](int e) { return (e / 16) * 32 + ((e % 16) / 4) * 8 + half_id * 4 + e % 4; };
+    if (store) cm::gemm::lds_barrier();  // every wavefront is done reading the last stage
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) {
+      const int tok = nb + nt * 32 + lane % 32;
+      const bool tok_ok = tok < n_tok;
+      // fp16 logits of this lane's token
       float z[TM * 16];
 #pragma unroll
-      for (int mt = 0; mt < TM; ++mt) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int v0 = mb + mt * 32 + q * 8 + half_id * 4;
-          union {
-            uint2 u;
-            _Float16 h[4];
-          } pk;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            pk.h[j] = cm::from_f32<_Float16>(acc[mt][nt][q * 4 + j]);
-            z[mt * 16 + q * 4 + j] = static_cast<float>(pk.h[j]);
-          }
-          if (tok < n_tok) *reinterpret_cast<uint2*>(s16 + panel_index(tok, v0, n_tok)) = pk.u;
-        }
-      }
-      // max and first argmax, then the sums: no data-dependent branches
+      for (int e = 0; e < TM * 16; ++e)
+        z[e] = static_cast<float>(cm::from_f32<_Float16>(acc[e / 16][nt][e % 16]));
+      // group max and first argmax over both halves of the wavefront (branch-free)
       float m = -__builtin_huge_valf();
       int best = -1;
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e) {
-        const int v = mb + (e / 16) * 32 + ((e % 16) / 4) * 8 + half_id * 4 + e % 4;
-        const bool take = v < n_voc && z[e] > m;
+        const bool take = mb + vrow(e) < n_voc && z[e] > m;
         m = take ? z[e] : m;
-        best = take ? v : best;
+        best = take ? mb + vrow(e) : best;
       }
+      const float m_o = __shfl_xor(m, 32, cm::kWave);
+      const int best_o = __shfl_xor(best, 32, cm::kWave);
+      const bool other = m_o > m || (m_o == m && best_o >= 0 && (best < 0 || best_o < best));
+      const float mg = other ? m_o : m;
+      best = other ? best_o : best;
+      // the label's logit, if this lane holds it (rare: a divergent branch around the search)
+      const int64_t local = tgt[nt] - c0 - mb;
+      if (tok_ok && local >= 0 && local < kGroup && ((local % 8) / 4) == half_id &&
+          mb + local < n_voc) {
+        float zt = 0.0f;
+#pragma unroll
+        for (int e = 0; e < TM * 16; ++e) zt = vrow(e) == local ? z[e] : zt;
+        label_logit[tok] = zt;
+      }
+      // E = e^{z - m_g} (in place of z) and the sums, relative to the group max
       float s = 0.0f, d = 0.0f;
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e) {
-        const int v = mb + (e / 16) * 32 + ((e % 16) / 4) * 8 + half_id * 4 + e % 4;
-        const float x = v < n_voc ? cm::exp_f(z[e] - m) : 0.0f;
+        const bool ok = mb + vrow(e) < n_voc;
+        const float x = ok ? cm::exp_f(z[e] - mg) : 0.0f;
         s += x;
-        d += v < n_voc ? x * z[e] : 0.0f;
+        d += ok ? x * z[e] : 0.0f;
+        z[e] = x;
       }
-      cm::SoftmaxState st{m, s, d, best >= 0 ? c0 + best : int64_t{0x7fffffffffffffff}};
-      if (best < 0) st = cm::SoftmaxState::empty();
-      st.merge(cm::shfl_xor_state(st, 32));
-      if (half_id == 0 && tok < n_tok) {
+      s += __shfl_xor(s, 32, cm::kWave);
+      d += __shfl_xor(d, 32, cm::kWave);
+      if (store) {
+        // stage: 4 consecutive vocabulary rows (8 bytes) per (mt, q)
+        const int t = tok - n0;
+#pragma unroll
+        for (int mt = 0; mt < TM; ++mt) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            union {
+              uint2 u;
+              _Float16 h[4];
+            } pk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pk.h[j] = cm::from_f32<_Float16>(z[mt * 16 + q * 4 + j]);
+            const int v = mb - m0 + mt * 32 + q * 8 + half_id * 4;  // tile-local vocabulary row
+            uint2* dst = reinterpret_cast<uint2*>(lds + stage_slot(v / 64, t, (v % 64) / 8));
+            dst[half_id] = pk.u;
+          }
+        }
+      }
+      if (half_id == 0 && tok_ok) {
         Partial p;
-        p.max = st.max;
-        p.sum = st.sum;
-        p.dot = st.dot;
-        p.best = st.max == -__builtin_huge_valf() ? -1 : static_cast<int32_t>(st.best);
+        p.max = mg;
+        p.sum = s;
+        p.dot = d;
+        p.best = best >= 0 ? static_cast<int32_t>(c0 + best) : -1;
         part[static_cast<int64_t>(tok) * n_groups + mb / kGroup] = p;
       }
+    }
+    if (!store) return;
+    cm::gemm::lds_barrier();
+    // copy out: slot = (p * BN + t) * 8 + physical chunk; 8 consecutive threads = one token row
+    constexpr int kSlots = kBM1 / 64 * kBN1 * 8;
+    for (int slot = threadIdx.x; slot < kSlots; slot += kThreads1) {
+      const int row = slot / 8, pc = slot % 8;
+      const int p = row / kBN1, t = row % kBN1;
+      if (n0 + t >= n_tok) continue;
+      const int c = pc ^ ((t >> 1) & 7);
+      const int64_t dst = ((static_cast<int64_t>((m0 / 64) + p) * n_tok + n0 + t) * 64) + c * 8;
+      *reinterpret_cast<uint4*>(e16 + dst) = lds[slot];
     }
   }
 };
@@ -158,8 +222,11 @@ struct EpiGrad {
   int first;            // first chunk: G = acc
 
   template <int TM, int TN>
-  __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb,
-                                        int lane) const {
+  __device__ __forceinline__ void prepare(int, int, int) {}
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb, int lane,
+                                        uint4*) const {
 #pragma unroll
     for (int mt = 0; mt < TM; ++mt) {
 #pragma unroll
@@ -179,48 +246,43 @@ struct EpiGrad {
   }
 };
 
-// __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD (OCC
-// workgroups of 4 wavefronts per CU), which caps the registers per wavefront accordingly.
-template <class Epi, int BM, int BN, int WM, int WN, int ST, int OCC>
+// __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD, which caps
+// the registers per wavefront accordingly.
+template <class Epi, int BM, int BN, int WM, int WN, int BK, int ST, int OCC>
 __global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm1(RowMajor A, RowMajor B,
                                                                        int remap, Epi epi) {
-  __shared__ uint4 lds[ST * (BM + BN) * cm::gemm::kRowChunks];
+  __shared__ uint4 lds[ST * (BM + BN) * (BK / 8)];
   int tm, tn;
   cm::gemm::tile_of_block((B.rows + BN - 1) / BN, remap, tm, tn);
-  cm::gemm::gemm_body<BM, BN, WM, WN, ST>(A, B, 0, A.k_len, tm, tn, epi, lds);
+  cm::gemm::gemm_lds<BM, BN, WM, WN, BK, ST>(A, B, 0, A.k_len, tm, tn, epi, lds);
 }
 
-// K3's A operand transform: the fp16 logits chunk becomes P = fp16(e^{z - lse} * 1024) for
-// labelled tokens and 0 otherwise, in registers, between the global load and the LDS store.
-// Padding columns of a panel turn into finite values; the weight panels are zero there.
-template <int KPER, int THREADS>
-struct XformP {
-  const float* lse;
-  const int64_t* target;
+// K3's A-fragment transform: E (fp16 e^{z - m_g}) times the (token, group) scale
+// s_g = e^{m_g - lse} * 1024 (0 for unlabelled tokens) gives P16 = e^{z - lse} * 1024. The
+// scales of the next stage are loaded one stage ahead; each A fragment (8 columns of one token,
+// all inside one group) then costs four packed fp16 multiplies.
+template <int TM>
+struct ScaleP {
+  const float* scale;  // [groups][n_tok]
   int n_tok;
-  float l[KPER];
-  float on[KPER];
+  int row = 0;
+  float nxt[TM];
+  _Float16 cur[TM];
 
-  __device__ __forceinline__ void prepare(int m0, int) {
+  __device__ __forceinline__ void bind(int r) { row = r; }
+  __device__ __forceinline__ void prefetch(int k0) {
+    const float* s = scale + static_cast<int64_t>(k0 / kGroup) * n_tok;
 #pragma unroll
-    for (int i = 0; i < KPER; ++i) {
-      const int r = m0 + (threadIdx.x + i * THREADS) / cm::gemm::kRowChunks;
-      const bool valid = r < n_tok;
-      l[i] = valid ? lse[r] : 0.0f;
-      on[i] = valid && target[r] != -100 ? kPScale : 0.0f;
+    for (int i = 0; i < TM; ++i) {
+      const int r = row + 32 * i;
+      nxt[i] = r < n_tok ? s[r] : 0.0f;
     }
   }
-  __device__ __forceinline__ void apply(uint4& chunk, int i) const {
-    union {
-      uint4 u;
-      _Float16 h[8];
-    } v;
-    v.u = chunk;
+  __device__ __forceinline__ void advance() {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v.h[e] = cm::from_f32<_Float16>(cm::exp_f(static_cast<float>(v.h[e]) - l[i]) * on[i]);
-    chunk = v.u;
+    for (int i = 0; i < TM; ++i) cur[i] = static_cast<_Float16>(nxt[i]);
   }
+  __device__ __forceinline__ half8 apply(half8 f, int i) const { return f * cur[i]; }
 };
 
 // K3: blockIdx.y is the K-slice; each slice accumulates into its own buffer.
@@ -228,22 +290,20 @@ struct GradSlices {
   float* g[kMaxSplit];
 };
 
-template <int BM, int BN, int WM, int WN, int ST, int OCC>
+template <int BM, int BN, int WM, int WN, int BK, int ST, int OCC>
 __global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm3(
     Blocked64 A, Blocked64 B, int k_slice, int remap, GradSlices out, int n_tok, int hidden,
-    const float* factor, int first, const float* lse, const int64_t* target) {
-  constexpr int THREADS = WM * WN * cm::kWave;
-  __shared__ uint4 lds[ST * (BM + BN) * cm::gemm::kRowChunks];
-  int tm, tn;
-  cm::gemm::tile_of_block((B.rows + BN - 1) / BN, remap, tm, tn);
-  const int s = blockIdx.y;
+    const float* factor, int first, const float* scale) {
+  __shared__ uint4 lds[ST * (BM + BN) * (BK / 8)];
+  int tm, tn, s;
+  cm::gemm::tile_of_block_2d((B.rows + BN - 1) / BN, remap, tm, tn, s);
   const int k_begin = s * k_slice;
   // An empty slice still runs the epilogue (with zero accumulators) so that its buffer is
   // initialised on the first chunk and rescaled on later ones.
   const int k_end = max(k_begin, min(A.k_len, k_begin + k_slice));
   EpiGrad epi{out.g[s], n_tok, hidden, factor, first};
-  XformP<BM * cm::gemm::kRowChunks / THREADS, THREADS> xp{lse, target, n_tok, {}, {}};
-  cm::gemm::gemm_body<BM, BN, WM, WN, ST>(A, B, k_begin, k_end, tm, tn, epi, lds, xp);
+  ScaleP<BM / WM / 32> xp{scale, n_tok};
+  cm::gemm::gemm_lds<BM, BN, WM, WN, BK, ST>(A, B, k_begin, k_end, tm, tn, epi, lds, xp);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -258,11 +318,12 @@ struct RowState {
   float* factor;  // e^{lse_before - lse_after} of the last merged chunk
 };
 
-// K2: merge the chunk's partials; record label logit and factor; optionally P in place.
+// K2: merge the chunk's partials into the running state; the factor; with a scale array, the
+// group scales s_g = e^{m_g - lse} * 1024 of labelled tokens ([groups][n_tok], 0 otherwise).
 __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
-    _Float16* __restrict__ s16, const Partial* __restrict__ part, int n_groups, RowState rs,
-    const int64_t* __restrict__ target, int n_tok, int n_voc, int64_t c0, int first,
-    int write_p) {
+    const Partial* __restrict__ part, int n_groups, RowState rs,
+    const int64_t* __restrict__ target, int n_tok, int n_voc, int first,
+    float* __restrict__ scale) {
   const int row = blockIdx.x;
   cm::SoftmaxState st = cm::SoftmaxState::empty();
   const int n_valid = (n_voc + kGroup - 1) / kGroup;  // groups K1 wrote for this chunk
@@ -286,10 +347,6 @@ __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
   cm::SoftmaxState now = prev;
   now.merge(st);
   const float lse_now = now.lse();
-  const int64_t t = target[row];
-  const bool labelled = t != -100;
-  const int64_t local = t - c0;
-  const bool hit = labelled && local >= 0 && local < n_voc;
   if (threadIdx.x == 0) {
     rs.max[row] = now.max;
     rs.sum[row] = now.sum;
@@ -297,9 +354,14 @@ __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
     rs.best[row] = static_cast<int32_t>(now.best);
     rs.lse[row] = lse_now;
     rs.factor[row] = first ? 0.0f : cm::exp_f(lse_prev - lse_now);
-    if (hit) rs.label_logit[row] = static_cast<float>(s16[panel_index(row, local, n_tok)]);
   }
-  (void)write_p;
+  if (scale == nullptr) return;
+  const bool labelled = target[row] != -100;
+  for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
+    const float m = part[static_cast<int64_t>(row) * n_groups + g].max;
+    scale[static_cast<int64_t>(g) * n_tok + row] =
+        labelled ? cm::exp_f(m - lse_now) * kPScale : 0.0f;
+  }
 }
 
 // K4: final per-row outputs; G = scale * (sum_s G_s / 1024 - W[t]) for labelled rows, else 0.
@@ -377,7 +439,7 @@ int n_split_for(int64_t n_rows, int hidden) {
 struct Layout {
   int64_t chunk, n_groups;
   int n_split;
-  int64_t off_s16, off_part, off_rows, off_g, off_wt, total;
+  int64_t off_e16, off_part, off_rows, off_scale, off_g, off_wt, total;
 };
 
 Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad,
@@ -388,12 +450,14 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   L.n_groups = L.chunk / kGroup;
   L.n_split = want_grad ? n_split_for(n_rows, hidden) : 1;
   int64_t off = 0;
-  L.off_s16 = off;
+  L.off_e16 = off;
   off += round_up(n_rows * L.chunk * 2, 256);
   L.off_part = off;
   off += round_up(n_rows * L.n_groups * static_cast<int64_t>(sizeof(Partial)), 256);
   L.off_rows = off;
   off += 8 * round_up(n_rows * 4, 256);
+  L.off_scale = off;
+  off += round_up(n_rows * L.n_groups * 4, 256);
   L.off_g = off;
   off += (L.n_split - 1) * round_up(n_rows * hidden * 4, 256);
   L.off_wt = off;
@@ -428,8 +492,9 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
   CM_CHECK_ARG(workspace_bytes >= L.total && cm::aligned(workspace, 256));
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  _Float16* s16 = reinterpret_cast<_Float16*>(ws + L.off_s16);
+  _Float16* e16 = reinterpret_cast<_Float16*>(ws + L.off_e16);
   Partial* part = reinterpret_cast<Partial*>(ws + L.off_part);
+  float* scale = want_grad ? reinterpret_cast<float*>(ws + L.off_scale) : nullptr;
   const int64_t rstride = round_up(n_rows * 4, 256);
   char* rb = ws + L.off_rows;
   RowState rs{reinterpret_cast<float*>(rb), reinterpret_cast<float*>(rb + rstride),
@@ -448,23 +513,24 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
   for (int64_t c0 = 0; c0 < vocab; c0 += L.chunk) {
     const int n_voc = static_cast<int>(vocab - c0 < L.chunk ? vocab - c0 : L.chunk);
     const bool first = c0 == 0;
-    // K1: Z^T tile = W_c H^T
+    // K1: Z^T tile = W_c H^T, statistics, E and the label logit
     {
       const int tiles_m = (n_voc + kBM1 - 1) / kBM1;
       const int tiles_n = (n_tok + kBN1 - 1) / kBN1;
       const int grid = tiles_m * tiles_n;
       RowMajor A{W16 + c0 * ld_w, ld_w, n_voc, hidden_size};
       RowMajor B{H16, ld_h, n_tok, hidden_size};
-      EpiLogits epi{s16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups)};
-      hipLaunchKernelGGL((lmh_gemm1<EpiLogits, kBM1, kBN1, kWM1, kWN1, kST1, kOcc1>), dim3(grid),
+      EpiProbs epi{e16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups), target,
+                   rs.label_logit, want_grad ? 1 : 0};
+      hipLaunchKernelGGL((lmh_gemm1<EpiProbs, kBM1, kBN1, kWM1, kWN1, kBK1, kST1, kOcc1>), dim3(grid),
                          dim3(kThreads1), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
       int st = cm::launch_status();
       if (st) return st;
     }
-    // K2: running statistics (+ P in place)
-    hipLaunchKernelGGL(lmh_rows_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, s16, part,
-                       static_cast<int>(L.n_groups), rs, target, n_tok, n_voc, c0, first ? 1 : 0,
-                       want_grad ? 1 : 0);
+    // K2: running statistics and the group scales
+    hipLaunchKernelGGL(lmh_rows_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, part,
+                       static_cast<int>(L.n_groups), rs, target, n_tok, n_voc, first ? 1 : 0,
+                       scale);
     int st = cm::launch_status();
     if (st) return st;
     if (!want_grad) continue;
@@ -485,13 +551,16 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
       const int tiles_n = (hidden_size + kBN3 - 1) / kBN3;
       const int grid = tiles_m * tiles_n;
       const int panels = (n_voc + kPanel - 1) / kPanel;
-      const int k_slice = ((panels + L.n_split - 1) / L.n_split) * kPanel;
-      Blocked64 A{s16, n_tok, n_voc};
+      // slices are whole statistics groups, so a stage never straddles two group scales
+      const int groups = (panels * kPanel + kGroup - 1) / kGroup;
+      const int k_slice = ((groups + L.n_split - 1) / L.n_split) * kGroup;
+      Blocked64 A{e16, n_tok, n_voc};
       Blocked64 B{wt, hidden_size, n_voc};
-      hipLaunchKernelGGL((lmh_gemm3<kBM3, kBN3, kWM3, kWN3, kST3, kOcc3>),
+      hipLaunchKernelGGL((lmh_gemm3<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, kOcc3>),
                          dim3(grid, L.n_split), dim3(kThreads3), 0, s, A, B, k_slice,
-                         grid % 8 == 0 ? 1 : 0, gs, n_tok, hidden_size, rs.factor, first ? 1 : 0,
-                         rs.lse, target);
+                         (grid * L.n_split) % 8 == 0 ? 1 : 0, gs, n_tok, hidden_size, rs.factor,
+                         first ? 1 : 0,
+                         scale);
       st = cm::launch_status();
       if (st) return st;
     }
