@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", default="")
+    p.add_argument("--step-steps", type=int, default=10, help="timed QLoRA steps (config 5)")
+    p.add_argument("--no-step", action="store_true", help="skip the QLoRA step (config 5)")
     return p.parse_args()
 
 
@@ -426,6 +428,37 @@ def cpu_baseline(headline):
                        f"median of 3 ({dt * 1e3:.0f} ms)")
 
 
+def qlora_step_bench(dev, steps, warmup=2):
+    """Config 5: one QLoRA training step of the 28-layer Qwen2.5-1.5B-shaped model (random
+    init, NF4 base weights, LoRA r16/a32/p0.05 on q/v, fp16 autocast, AdamW + GradScaler, batch
+    of 4 rows of U[64,512] tokens packed out). Each step is timed between two device syncs, as
+    the reference's harness times its trainer steps; the median is reported with the peak HBM
+    of the timed steps."""
+    import torch
+
+    from claudemaxing_amd import qlora_step
+
+    t0 = time.perf_counter()
+    model = qlora_step.build_model(dev, seed=0)
+    batch, lengths = qlora_step.make_batch(dev, seed=0)
+    opt = qlora_step.make_optimizer(model)
+    scaler = torch.amp.GradScaler("cuda")
+    build_s = time.perf_counter() - t0
+    r = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup)
+    tokens = int(lengths.sum())
+    out = dict(config="Qwen2.5-1.5B shape, 28 layers, NF4 + LoRA r16 q/v, batch 4, "
+                      f"{tokens} real tokens (lengths {lengths.tolist()}), fp16 autocast",
+               median_ms=round(r["median_ms"], 2), step_ms=[round(x, 2) for x in r["step_ms"]],
+               tokens_per_s=round(tokens / (r["median_ms"] * 1e-3), 1),
+               peak_allocated_gb=round(r["peak_allocated_gb"], 3),
+               peak_reserved_gb=round(r["peak_reserved_gb"], 3),
+               losses=[round(x, 4) for x in r["losses"]], build_s=round(build_s, 1),
+               warmup=warmup, steps=steps)
+    del model, opt
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -453,6 +486,8 @@ def main():
                                   in_step=kern.step)
         print(f"[bench] {kern.name}: {ms * 1e3:.2f} us, {achieved:.1f} {unit} "
               f"({100 * achieved / peak:.1f}% of peak)", file=sys.stderr, flush=True)
+    if not results:
+        sys.exit("bench.py: --only must name at least one kernel")
     headline = "lmhead_ce" if "lmhead_ce" in results else next(iter(results))
     hr = results[headline]
     line = {
@@ -476,6 +511,12 @@ def main():
                      "traffic": traffic_from_profile(headline)},
         "kernels": results,
     }
+    if not args.no_step and (not only or "qlora_step" in only):
+        print("[bench] qlora_step ...", file=sys.stderr, flush=True)
+        line["qlora_step"] = qlora_step_bench(dev, args.step_steps)
+        print(f"[bench] qlora_step: {line['qlora_step']['median_ms']} ms per step, peak "
+              f"{line['qlora_step']['peak_allocated_gb']} GB allocated", file=sys.stderr,
+              flush=True)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(headline)
     print(json.dumps(line), flush=True)

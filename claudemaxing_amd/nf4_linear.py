@@ -37,20 +37,23 @@ def matmul_nf4(x, packed, state):
 
 
 class NF4Linear(torch.nn.Module):
-    """Bias-free frozen linear layer stored as NF4 (blocksize 64, double-quantized absmax)."""
+    """Frozen linear layer stored as NF4 (blocksize 64, double-quantized absmax), with an
+    optional frozen bias added in the compute dtype (as Linear4bit adds its bias)."""
 
-    def __init__(self, packed, state, compute_dtype=torch.float16):
+    def __init__(self, packed, state, compute_dtype=torch.float16, bias=None):
         super().__init__()
         self.register_buffer("packed", packed, persistent=False)
+        self.register_buffer("bias", None if bias is None else bias.detach().clone(),
+                             persistent=False)
         self.quant_state = state
         self.compute_dtype = compute_dtype
         self.out_features, self.in_features = state.shape
 
     @classmethod
-    def from_weight(cls, weight, compute_dtype=torch.float16, blocksize=64):
+    def from_weight(cls, weight, compute_dtype=torch.float16, blocksize=64, bias=None):
         packed, state = quantize_nf4(weight.detach(), blocksize=blocksize,
                                      compress_statistics=True)
-        return cls(packed, state, compute_dtype)
+        return cls(packed, state, compute_dtype, bias)
 
     def _apply(self, fn, recurse=True):
         super()._apply(fn, recurse)
@@ -61,7 +64,10 @@ class NF4Linear(torch.nn.Module):
 
     def forward(self, x):
         out = matmul_nf4(x.to(self.compute_dtype), self.packed, self.quant_state)
+        if self.bias is not None:
+            out = out + self.bias.to(self.compute_dtype)
         return out.to(x.dtype)
 
     def extra_repr(self):
-        return f"in_features={self.in_features}, out_features={self.out_features}, nf4"
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, nf4")

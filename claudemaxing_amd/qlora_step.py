@@ -1,0 +1,166 @@
+"""One QLoRA training step of a Qwen2.5-1.5B-shaped model on one GPU, on this kernel set.
+
+The reference measures its kernels inside a Soup/TRL SFT run of Qwen2.5-1.5B-Instruct
+(task/task.yaml: 4-bit quantization, LoRA r=16 / alpha=32, lr 2e-4, batch 4, max_length 512)
+driven by harness/_train.py, which times each trainer step between two
+`torch.cuda.synchronize()` calls (_train.py:145-157). The trainer step is fp16 autocast +
+GradScaler, AdamW on the LoRA parameters, and TRL's compute_loss asking the causal LM for the
+fused head (solution/lm_head_loss.py:475-512), which packs the pad tokens out (300-363).
+
+This module builds the same step without the network and without bitsandbytes/peft/TRL:
+
+* `build_model`: transformers' Qwen2ForCausalLM from a local config (random init), every
+  linear of the decoder stored as NF4 (`NF4Linear`, blocksize 64 with double-quantized absmax),
+  LoRA (`LoRALinear`, fp32 parameters, dropout 0.05) on q_proj and v_proj, everything else
+  frozen, tied fp32 embedding, and the kernel set's patches applied (`apply()`);
+* `make_batch`: 4 rows with token lengths uniform in [64, 512], right-padded, labels = ids with
+  -100 at the pads;
+* `train_step`: the fused-head request TRL's compute_loss makes, the forward under fp16 autocast,
+  the scaled backward, the AdamW step through the GradScaler, zeroed gradients.
+
+`unpatched()` restores the stock transformers code paths for the duration of a `with` block,
+so the same model can be run through both (the parity test of the step).
+"""
+
+import contextlib
+import time
+
+import torch
+
+from . import apply
+from .lm_head_loss import _REQUEST_ATTR
+from .lora import LoRALinear
+from .nf4_linear import NF4Linear
+
+# Qwen2.5-1.5B (config.json of Qwen/Qwen2.5-1.5B-Instruct, restated).
+QWEN25_1P5B = dict(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                   num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
+                   max_position_embeddings=32768, rope_theta=1000000.0, rms_norm_eps=1e-6,
+                   tie_word_embeddings=True, hidden_act="silu", attention_dropout=0.0,
+                   use_sliding_window=False, initializer_range=0.02)
+
+LORA_TARGETS = ("q_proj", "v_proj")
+NF4_TARGETS = (("self_attn", ("q_proj", "k_proj", "v_proj", "o_proj")),
+               ("mlp", ("gate_proj", "up_proj", "down_proj")))
+
+
+def qwen2_config(**overrides):
+    from transformers import Qwen2Config
+
+    cfg = Qwen2Config(**{**QWEN25_1P5B, **overrides})
+    cfg._attn_implementation = "sdpa"
+    return cfg
+
+
+def build_model(device, seed=0, r=16, alpha=32, dropout=0.05, patch=True, **overrides):
+    """The QLoRA model: random-init Qwen2 weights (seeded), NF4 decoder linears, LoRA on q/v."""
+    from transformers import Qwen2ForCausalLM
+
+    if patch:
+        apply()
+    cfg = qwen2_config(**overrides)
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = Qwen2ForCausalLM(cfg)
+    model.requires_grad_(False)
+    for layer in model.model.layers:
+        for block_name, names in NF4_TARGETS:
+            block = getattr(layer, block_name)
+            for name in names:
+                lin = getattr(block, name)
+                setattr(block, name, NF4Linear.from_weight(lin.weight, bias=lin.bias))
+                del lin
+        for name in LORA_TARGETS:
+            base = getattr(layer.self_attn, name)
+            with torch.device(device):
+                setattr(layer.self_attn, name, LoRALinear(base, r=r, alpha=alpha,
+                                                          dropout=dropout))
+    model.train()
+    if device != "cpu" and torch.device(device).type == "cuda":
+        torch.cuda.empty_cache()
+    return model
+
+
+def lora_parameters(model):
+    return [p for n, p in model.named_parameters() if "lora_" in n]
+
+
+def make_batch(device, seed=0, batch=4, lo=64, hi=512, vocab=QWEN25_1P5B["vocab_size"]):
+    """Right-padded ids [batch, max_len], attention mask and labels (-100 at the pads); the
+    row lengths are uniform in [lo, hi] (seeded)."""
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(lo, hi + 1, (batch,), generator=g)
+    width = int(lengths.max())
+    ids = torch.randint(0, vocab, (batch, width), generator=g)
+    mask = (torch.arange(width)[None, :] < lengths[:, None]).to(torch.int64)
+    ids = ids * mask
+    labels = torch.where(mask.bool(), ids, torch.full_like(ids, -100))
+    return dict(input_ids=ids.to(device), attention_mask=mask.to(device),
+                labels=labels.to(device)), lengths
+
+
+def make_optimizer(model, lr=2e-4):
+    return torch.optim.AdamW(lora_parameters(model), lr=lr)
+
+
+def train_step(model, opt, scaler, batch, fused=True):
+    """Forward (fp16 autocast), scaled backward, optimizer step; returns the loss tensor."""
+    if fused:
+        model.__dict__[_REQUEST_ATTR] = True
+    try:
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = model(**batch, use_cache=False)
+    finally:
+        model.__dict__.pop(_REQUEST_ATTR, None)
+    scaler.scale(out.loss).backward()
+    scaler.step(opt)
+    scaler.update()
+    opt.zero_grad(set_to_none=True)
+    return out.loss.detach()
+
+
+def time_steps(model, opt, scaler, batch, steps, warmup):
+    """Median and all per-step wall times (ms), each step between two device syncs as the
+    reference's harness probe times them; peak HBM over the timed steps."""
+    for _ in range(warmup):
+        train_step(model, opt, scaler, batch)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    times, losses = [], []
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        losses.append(train_step(model, opt, scaler, batch))
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    ordered = sorted(times)
+    return dict(median_ms=ordered[len(ordered) // 2], step_ms=times,
+                peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
+                peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30,
+                losses=[float(x) for x in losses])
+
+
+@contextlib.contextmanager
+def unpatched():
+    """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, causal-LM forward) and the
+    plain LoRA computation (nn.Dropout + two linears) for the duration of the block; the kernel
+    set's paths are put back afterwards. NF4Linear keeps its dequant kernel (bit-exact to the
+    NF4 oracle, so the weights are the same either way)."""
+    from transformers.models.qwen2 import modeling_qwen2 as mq
+
+    from . import lora
+
+    saved = [(lora, "_branch_applies", lora._branch_applies)]
+    lora._branch_applies = lambda *args: False
+    for owner, attr in ((mq.Qwen2RMSNorm, "forward"), (mq.Qwen2MLP, "forward"),
+                        (mq.Qwen2ForCausalLM, "forward"), (mq, "apply_rotary_pos_emb")):
+        current = getattr(owner, attr)
+        original = getattr(current, "_original", None)
+        if original is not None:
+            saved.append((owner, attr, current))
+            setattr(owner, attr, original)
+    try:
+        yield
+    finally:
+        for owner, attr, current in saved:
+            setattr(owner, attr, current)
