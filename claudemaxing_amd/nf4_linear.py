@@ -13,27 +13,37 @@ input's dtype, as Linear4bit does).
 import torch
 
 from .nf4 import dequantize_nf4, quantize_nf4
+from .rmsnorm import fp16_copy_of
 
 
 class MatMulNF4(torch.autograd.Function):
-    """x @ W.T for a frozen NF4 weight W [out, in]; W is expanded in x's dtype each way."""
+    """x @ W.T (+ bias) for a frozen NF4 weight W [out, in], computed in `compute` dtype (x's
+    own when None) with W expanded in that dtype each way; an optional frozen bias in that
+    dtype. An fp32 x is taken through the fp16 copy the preceding norm wrote of it when there
+    is one (rmsnorm.fp16_copy_of: the same values as x.to(fp16)), else cast. The output is in
+    the compute dtype; the input gradient is returned in x's dtype."""
 
     @staticmethod
-    def forward(ctx, x, packed, state):
-        w = dequantize_nf4(packed, state, x.dtype)
-        ctx.packed, ctx.state = packed, state
-        return torch.nn.functional.linear(x, w)
+    def forward(ctx, x, packed, state, bias=None, compute=None):
+        compute = compute or x.dtype
+        xc = x
+        if x.dtype != compute:
+            low = fp16_copy_of(x) if compute == torch.float16 else None
+            xc = low if low is not None else x.to(compute)
+        w = dequantize_nf4(packed, state, compute)
+        ctx.packed, ctx.state, ctx.x_dtype = packed, state, x.dtype
+        return torch.nn.functional.linear(xc, w, bias)
 
     @staticmethod
     def backward(ctx, grad):
         if not ctx.needs_input_grad[0]:
-            return None, None, None
+            return None, None, None, None, None
         w = dequantize_nf4(ctx.packed, ctx.state, grad.dtype)
-        return torch.matmul(grad, w), None, None
+        return torch.matmul(grad, w).to(ctx.x_dtype), None, None, None, None
 
 
-def matmul_nf4(x, packed, state):
-    return MatMulNF4.apply(x, packed, state)
+def matmul_nf4(x, packed, state, bias=None, compute=None):
+    return MatMulNF4.apply(x, packed, state, bias, compute)
 
 
 class NF4Linear(torch.nn.Module):
@@ -48,6 +58,7 @@ class NF4Linear(torch.nn.Module):
         self.quant_state = state
         self.compute_dtype = compute_dtype
         self.out_features, self.in_features = state.shape
+        self._bias_c = None  # (version, dtype, bias in the compute dtype)
 
     @classmethod
     def from_weight(cls, weight, compute_dtype=torch.float16, blocksize=64, bias=None):
@@ -62,10 +73,20 @@ class NF4Linear(torch.nn.Module):
             self.quant_state = self.quant_state.to(dev)
         return self
 
+    def _bias_in(self, dtype):
+        """The frozen bias in `dtype`, converted once per bias version."""
+        if self.bias is None:
+            return None
+        cached = self._bias_c
+        key = (self.bias._version, self.bias.data_ptr(), dtype)
+        if cached is None or cached[0] != key:
+            cached = (key, self.bias.to(dtype))
+            self._bias_c = cached
+        return cached[1]
+
     def forward(self, x):
-        out = matmul_nf4(x.to(self.compute_dtype), self.packed, self.quant_state)
-        if self.bias is not None:
-            out = out + self.bias.to(self.compute_dtype)
+        out = matmul_nf4(x, self.packed, self.quant_state, self._bias_in(self.compute_dtype),
+                         self.compute_dtype)
         return out.to(x.dtype)
 
     def extra_repr(self):

@@ -142,16 +142,22 @@ def time_steps(model, opt, scaler, batch, steps, warmup):
 
 @contextlib.contextmanager
 def unpatched():
-    """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, causal-LM forward) and the
-    plain LoRA computation (nn.Dropout + two linears) for the duration of the block; the kernel
+    """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, causal-LM forward, sdpa
+    attention) and the plain LoRA computation (nn.Dropout + two linears) for the duration of the block; the kernel
     set's paths are put back afterwards. NF4Linear keeps its dequant kernel (bit-exact to the
     NF4 oracle, so the weights are the same either way)."""
     from transformers.models.qwen2 import modeling_qwen2 as mq
 
     from . import lora
 
+    from transformers.modeling_utils import AttentionInterface
+
     saved = [(lora, "_branch_applies", lora._branch_applies)]
     lora._branch_applies = lambda *args: False
+    sdpa = AttentionInterface._global_mapping.get("sdpa")
+    if getattr(sdpa, "_original", None) is not None:
+        saved.append((AttentionInterface._global_mapping, "sdpa", sdpa))
+        AttentionInterface._global_mapping["sdpa"] = sdpa._original
     for owner, attr in ((mq.Qwen2RMSNorm, "forward"), (mq.Qwen2MLP, "forward"),
                         (mq.Qwen2ForCausalLM, "forward"), (mq, "apply_rotary_pos_emb")):
         current = getattr(owner, attr)
@@ -163,4 +169,7 @@ def unpatched():
         yield
     finally:
         for owner, attr, current in saved:
-            setattr(owner, attr, current)
+            if isinstance(owner, dict):
+                owner[attr] = current
+            else:
+                setattr(owner, attr, current)

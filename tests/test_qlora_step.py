@@ -75,10 +75,18 @@ def test_unpatched_restores_and_reapplies():
 
     from claudemaxing_amd import apply, lora
 
+    from transformers.modeling_utils import AttentionInterface
+
+    from claudemaxing_amd import patch_qwen2_grouped_sdpa
+
     apply()
+    patch_qwen2_grouped_sdpa()
+    sdpa = AttentionInterface._global_mapping["sdpa"]
+    assert getattr(sdpa, "_grouped_sdpa", False)
     patched = (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
                mq.apply_rotary_pos_emb, lora._branch_applies)
     with qlora_step.unpatched():
+        assert AttentionInterface._global_mapping["sdpa"] is sdpa._original
         assert mq.Qwen2RMSNorm.forward is patched[0]._original
         assert mq.Qwen2MLP.forward is patched[1]._original
         assert mq.Qwen2ForCausalLM.forward is patched[2]._original
@@ -86,3 +94,4 @@ def test_unpatched_restores_and_reapplies():
         assert lora._branch_applies(None, 0.5, None, None, True) is False
     assert (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
             mq.apply_rotary_pos_emb, lora._branch_applies) == patched
+    assert AttentionInterface._global_mapping["sdpa"] is sdpa
