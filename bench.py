@@ -433,7 +433,8 @@ def qlora_step_bench(dev, steps, warmup=2):
     init, NF4 base weights, LoRA r16/a32/p0.05 on q/v, fp16 autocast, AdamW + GradScaler, batch
     of 4 rows of U[64,512] tokens packed out). Each step is timed between two device syncs, as
     the reference's harness times its trainer steps; the median is reported with the peak HBM
-    of the timed steps."""
+    of the timed steps, for the eager step and for the step replayed from a HIP graph (the same
+    model and optimizer continue, so the graphed steps start from the eager steps' weights)."""
     import torch
 
     from claudemaxing_amd import qlora_step
@@ -445,6 +446,7 @@ def qlora_step_bench(dev, steps, warmup=2):
     scaler = torch.amp.GradScaler("cuda")
     build_s = time.perf_counter() - t0
     r = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup)
+    rg = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup, graphed=True)
     tokens = int(lengths.sum())
     out = dict(config="Qwen2.5-1.5B shape, 28 layers, NF4 + LoRA r16 q/v, batch 4, "
                       f"{tokens} real tokens (lengths {lengths.tolist()}), fp16 autocast",
@@ -453,7 +455,14 @@ def qlora_step_bench(dev, steps, warmup=2):
                peak_allocated_gb=round(r["peak_allocated_gb"], 3),
                peak_reserved_gb=round(r["peak_reserved_gb"], 3),
                losses=[round(x, 4) for x in r["losses"]], build_s=round(build_s, 1),
-               warmup=warmup, steps=steps)
+               warmup=warmup, steps=steps,
+               graphed=dict(median_ms=round(rg["median_ms"], 2),
+                            step_ms=[round(x, 2) for x in rg["step_ms"]],
+                            tokens_per_s=round(tokens / (rg["median_ms"] * 1e-3), 1),
+                            peak_allocated_gb=round(rg["peak_allocated_gb"], 3),
+                            losses=[round(x, 4) for x in rg["losses"]],
+                            note="forward + backward replayed from one HIP graph per packed "
+                                 "shape; packing and the GradScaler/AdamW step eager"))
     del model, opt
     torch.cuda.empty_cache()
     return out
@@ -514,7 +523,8 @@ def main():
     if not args.no_step and (not only or "qlora_step" in only):
         print("[bench] qlora_step ...", file=sys.stderr, flush=True)
         line["qlora_step"] = qlora_step_bench(dev, args.step_steps)
-        print(f"[bench] qlora_step: {line['qlora_step']['median_ms']} ms per step, peak "
+        print(f"[bench] qlora_step: {line['qlora_step']['median_ms']} ms per step eager, "
+              f"{line['qlora_step']['graphed']['median_ms']} ms graphed, peak "
               f"{line['qlora_step']['peak_allocated_gb']} GB allocated", file=sys.stderr,
               flush=True)
     if not args.no_cpu:

@@ -28,7 +28,8 @@ import time
 import torch
 
 from . import apply
-from .lm_head_loss import _REQUEST_ATTR
+from .attention import packed_rows
+from .lm_head_loss import _REQUEST_ATTR, _pack_batch, _packed_forward
 from .lora import LoRALinear
 from .nf4_linear import NF4Linear
 
@@ -119,18 +120,89 @@ def train_step(model, opt, scaler, batch, fused=True):
     return out.loss.detach()
 
 
-def time_steps(model, opt, scaler, batch, steps, warmup):
+class GraphedStep:
+    """The same training step with the packed forward and the scaled backward replayed from one
+    HIP graph. The step issues ~5000 kernels, and in eager mode the host's launch cost exceeds
+    their device time; a replay issues them without the host.
+
+    What stays outside the graph, because it synchronises with the host: packing the batch
+    (`_pack_batch` reads the number of real tokens), and the GradScaler step (its inf check) with
+    AdamW. The graph is captured for one packed batch; `load` copies another batch of the same
+    packed shape into its inputs. The gradients live in the graph's buffers: they are
+    overwritten by each replay and must not be set to None. Nothing in the captured region
+    allocates outside torch's graph pool or synchronises (the kernel library never does; the
+    RMSNorm tiny-column map is computed in the warm-up), and LoRA dropout draws from torch's
+    graph-safe generator, so every replay has fresh masks."""
+
+    def __init__(self, model, opt, scaler, batch, warmup=3):
+        self.model, self.opt, self.scaler = model, opt, scaler
+        self.params = lora_parameters(model)
+        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                      use_cache=False)
+        self.packed = _pack_batch(model, kwargs, batch["labels"])
+        if self.packed is None:
+            raise ValueError("GraphedStep needs a padded batch with pads to pack out")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._zero()
+                self._forward_backward()
+        torch.cuda.current_stream().wait_stream(side)
+        self._zero()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.loss = self._forward_backward()
+
+    def _zero(self):
+        for p in self.params:
+            p.grad = None
+
+    def _forward_backward(self):
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = _packed_forward(self.model, dict(use_cache=False), self.packed)
+        self.scaler.scale(out.loss).backward()
+        return out.loss.detach()
+
+    def load(self, batch):
+        """Copy a batch with the same packed shape into the graph's inputs."""
+        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                      use_cache=False)
+        packed = _pack_batch(self.model, kwargs, batch["labels"])
+        if (packed is None or packed.ids.shape != self.packed.ids.shape
+                or packed_rows(packed.mask) != packed_rows(self.packed.mask)):
+            # the row structure matters to the opt-in packed-row attention, baked into a capture
+            raise ValueError("the batch packs to another shape: capture a new GraphedStep")
+        for name in ("ids", "pos", "mask", "target", "index"):
+            getattr(self.packed, name).copy_(getattr(packed, name))
+
+    def step(self):
+        """Replay forward + backward, then the GradScaler step with AdamW; the loss tensor."""
+        self.graph.replay()
+        self.scaler.step(self.opt)
+        self.scaler.update()
+        return self.loss.clone()
+
+
+def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
     """Median and all per-step wall times (ms), each step between two device syncs as the
-    reference's harness probe times them; peak HBM over the timed steps."""
+    reference's harness probe times them; peak HBM over the timed steps. With graphed, the
+    steps replay a GraphedStep captured first (the capture and its warm-up are not timed)."""
+    if graphed:
+        gstep = GraphedStep(model, opt, scaler, batch)
+        run = gstep.step
+    else:
+        def run():
+            return train_step(model, opt, scaler, batch)
     for _ in range(warmup):
-        train_step(model, opt, scaler, batch)
+        run()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     times, losses = [], []
     for _ in range(steps):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        losses.append(train_step(model, opt, scaler, batch))
+        losses.append(run())
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
     ordered = sorted(times)

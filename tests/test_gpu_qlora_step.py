@@ -82,3 +82,53 @@ def test_fused_step_matches_stock(dev):
     assert d_f <= max(2e-3 * abs(loss_r), 2 * d_s), report[0]
     for n, e_f, e_s in worst:
         assert e_f <= max(2e-2, 2 * e_s), (n, e_f, e_s)
+
+
+@pytest.mark.gpu
+def test_graphed_step_matches_eager(dev):
+    """Three steps replayed from the HIP graph against three eager steps of an identical model
+    (dropout off, so both draw no random numbers): the same loss and the same LoRA weights after
+    every step. The optimizer step between replays is eager work, and each step ends with a
+    device sync, as the graph tests of this platform require."""
+    banner("qlora step: graphed vs eager, 2 layers, 3 steps")
+    runs = []
+    for graphed in (False, True):
+        model = qlora_step.build_model(dev, seed=0, dropout=0.0, **TWO_LAYERS)
+        batch, _ = qlora_step.make_batch(dev, seed=4)
+        opt = qlora_step.make_optimizer(model)
+        scaler = torch.amp.GradScaler("cuda")
+        if graphed:
+            gstep = qlora_step.GraphedStep(model, opt, scaler, batch)
+            step = gstep.step
+        else:
+            def step():
+                return qlora_step.train_step(model, opt, scaler, batch)
+        trace = []
+        for _ in range(3):
+            loss = float(step())
+            torch.cuda.synchronize()
+            trace.append((loss, [p.detach().clone() for p in qlora_step.lora_parameters(model)]))
+        runs.append(trace)
+    for (le, pe), (lg, pg) in zip(*runs):
+        assert le == lg, (le, lg)
+        for a, b in zip(pe, pg):
+            assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_graphed_step_trains_with_dropout(dev):
+    banner("qlora step: graphed with dropout, 2 layers, 4 steps")
+    model = qlora_step.build_model(dev, seed=0, **TWO_LAYERS)
+    batch, _ = qlora_step.make_batch(dev, seed=0)
+    opt = qlora_step.make_optimizer(model)
+    gstep = qlora_step.GraphedStep(model, opt, torch.amp.GradScaler("cuda"), batch)
+    b0 = [p.detach().clone() for n, p in model.named_parameters() if "lora_B" in n]
+    losses = [float(gstep.step()) for _ in range(4)]
+    torch.cuda.synchronize()
+    assert all(9.0 < x < 14.0 for x in losses)
+    assert len(set(losses)) > 1  # fresh dropout masks and updated weights every replay
+    b1 = [p.detach() for n, p in model.named_parameters() if "lora_B" in n]
+    assert any(not torch.equal(a, b) for a, b in zip(b0, b1))
+    gstep.load(qlora_step.make_batch(dev, seed=0)[0])  # same packed shape: accepted
+    with pytest.raises(ValueError):
+        gstep.load(qlora_step.make_batch(dev, seed=1)[0])  # other lengths: a new capture
