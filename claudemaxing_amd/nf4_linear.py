@@ -48,10 +48,14 @@ def matmul_nf4(x, packed, state, bias=None, compute=None):
 
 class NF4Linear(torch.nn.Module):
     """Frozen linear layer stored as NF4 (blocksize 64, double-quantized absmax), with an
-    optional frozen bias added in the compute dtype (as Linear4bit adds its bias)."""
+    optional frozen bias added in the compute dtype (as Linear4bit adds its bias). The output is
+    in the input's dtype (Linear4bit's rule) unless `out_dtype` names another: a layer whose
+    output is added to an fp32 residual stream can hand over fp32 (the same values, widened
+    once), which spares torch's mixed-dtype add."""
 
-    def __init__(self, packed, state, compute_dtype=torch.float16, bias=None):
+    def __init__(self, packed, state, compute_dtype=torch.float16, bias=None, out_dtype=None):
         super().__init__()
+        self.out_dtype = out_dtype
         self.register_buffer("packed", packed, persistent=False)
         self.register_buffer("bias", None if bias is None else bias.detach().clone(),
                              persistent=False)
@@ -61,10 +65,11 @@ class NF4Linear(torch.nn.Module):
         self._bias_c = None  # (version, dtype, bias in the compute dtype)
 
     @classmethod
-    def from_weight(cls, weight, compute_dtype=torch.float16, blocksize=64, bias=None):
+    def from_weight(cls, weight, compute_dtype=torch.float16, blocksize=64, bias=None,
+                    out_dtype=None):
         packed, state = quantize_nf4(weight.detach(), blocksize=blocksize,
                                      compress_statistics=True)
-        return cls(packed, state, compute_dtype, bias)
+        return cls(packed, state, compute_dtype, bias, out_dtype)
 
     def _apply(self, fn, recurse=True):
         super()._apply(fn, recurse)
@@ -87,7 +92,7 @@ class NF4Linear(torch.nn.Module):
     def forward(self, x):
         out = matmul_nf4(x, self.packed, self.quant_state, self._bias_in(self.compute_dtype),
                          self.compute_dtype)
-        return out.to(x.dtype)
+        return out.to(self.out_dtype or x.dtype)
 
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -10,7 +10,8 @@ fused head (solution/lm_head_loss.py:475-512), which packs the pad tokens out (3
 This module builds the same step without the network and without bitsandbytes/peft/TRL:
 
 * `build_model`: transformers' Qwen2ForCausalLM from a local config (random init), every
-  linear of the decoder stored as NF4 (`NF4Linear`, blocksize 64 with double-quantized absmax),
+  linear of the decoder stored as NF4 (`NF4Linear`, blocksize 64 with double-quantized absmax;
+  o_proj and down_proj hand their output to the fp32 residual stream in fp32),
   LoRA (`LoRALinear`, fp32 parameters, dropout 0.05) on q_proj and v_proj, everything else
   frozen, tied fp32 embedding, and the kernel set's patches applied (`apply()`);
 * `make_batch`: 4 rows with token lengths uniform in [64, 512], right-padded, labels = ids with
@@ -41,6 +42,8 @@ QWEN25_1P5B = dict(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
                    use_sliding_window=False, initializer_range=0.02)
 
 LORA_TARGETS = ("q_proj", "v_proj")
+# linears whose output is added to the fp32 residual stream: they hand over fp32
+RESIDUAL_OUTPUTS = ("o_proj", "down_proj")
 NF4_TARGETS = (("self_attn", ("q_proj", "k_proj", "v_proj", "o_proj")),
                ("mlp", ("gate_proj", "up_proj", "down_proj")))
 
@@ -69,7 +72,9 @@ def build_model(device, seed=0, r=16, alpha=32, dropout=0.05, patch=True, **over
             block = getattr(layer, block_name)
             for name in names:
                 lin = getattr(block, name)
-                setattr(block, name, NF4Linear.from_weight(lin.weight, bias=lin.bias))
+                out_dtype = torch.float32 if name in RESIDUAL_OUTPUTS else None
+                setattr(block, name, NF4Linear.from_weight(lin.weight, bias=lin.bias,
+                                                           out_dtype=out_dtype))
                 del lin
         for name in LORA_TARGETS:
             base = getattr(layer.self_attn, name)

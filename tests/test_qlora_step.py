@@ -25,6 +25,8 @@ def test_model_surgery():
             assert torch.count_nonzero(lin.lora_B.weight) == 0
         assert isinstance(attn.k_proj, NF4Linear) and attn.k_proj.bias is not None
         assert isinstance(attn.o_proj, NF4Linear) and attn.o_proj.bias is None
+        assert attn.o_proj.out_dtype == torch.float32 and attn.k_proj.out_dtype is None
+        assert mlp.down_proj.out_dtype == torch.float32
         for name in ("gate_proj", "up_proj", "down_proj"):
             lin = getattr(mlp, name)
             assert isinstance(lin, NF4Linear) and lin.bias is None
