@@ -77,29 +77,31 @@ struct LdsRows {
   }
 };
 
-// Direct loads of one ROWS x BK operand tile by NW wavefronts. Each lane keeps the 32-bit byte
-// offsets of its chunks relative to the tile's origin; a stage's origin is a wave-uniform
-// pointer, so a load is a scalar base plus a constant lane offset. Tiles that are wholly inside
-// the operand take that path; the others select the zero chunk per lane.
+// Direct loads of one ROWS x BK operand tile by NW wavefronts. Instruction i of a lane fetches
+// chunk c = (i * NW + wave) * 64 + lane of the tile: row row0 + i * kRowStep, and (with NW >= 2)
+// the same swizzled column for every i, since kRowStep is a multiple of the swizzle's period.
+// So a lane keeps one byte offset from the stage origin, and instruction i adds i times a
+// wave-uniform row step; a stage's origin is a wave-uniform pointer. Tiles that are wholly
+// inside the operand take that path; the others select the zero chunk per lane.
 template <int ROWS, int NW, int BK>
 struct DmaTile {
   using L = LdsRows<BK>;
   static constexpr int kChunks = ROWS * L::kRC;
   static constexpr int kPer = kChunks / (NW * kWave);  // instructions per lane
+  static constexpr int kRowStep = NW * kWave / L::kRC;  // tile rows between instructions
   static_assert(kPer * NW * kWave == kChunks, "tile chunks must split over the wavefronts");
-  uint32_t off[kPer];  // byte offset of the lane's chunk from the stage origin
-  int row[kPer];       // tile row of the chunk
-  int col[kPer];       // column of the chunk within the stage
+  static_assert(NW >= 2, "one swizzled column per lane needs a row step of 16 or more");
+  uint32_t off0;      // byte offset of the lane's chunk of instruction 0 from the stage origin
+  uint32_t step;      // bytes between instructions (wave-uniform)
+  int row0, col0;     // tile row of instruction 0 and column of every chunk of the lane
 
   template <class Src>
   __device__ __forceinline__ void init(const Src& src, int wave, int lane) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = (i * NW + wave) * kWave + lane;
-      row[i] = c / L::kRC;
-      col[i] = ((c % L::kRC) ^ L::swz(row[i])) * 8;
-      off[i] = src.tile_offset(row[i], col[i]);
-    }
+    const int c = wave * kWave + lane;
+    row0 = c / L::kRC;
+    col0 = ((c % L::kRC) ^ L::swz(row0)) * 8;
+    off0 = src.tile_offset(row0, col0);
+    step = src.tile_offset(kRowStep, 0);
   }
 
   // Instruction i of the stage whose origin is (r0, k0); `inside` = the tile is wholly inside
@@ -108,8 +110,8 @@ struct DmaTile {
   __device__ __forceinline__ void issue(const Src& src, int r0, int k0, uint4* tile, int wave,
                                         int i, bool inside) const {
     const char* base = reinterpret_cast<const char*>(src.at(r0, k0));
-    const bool ok = inside || (r0 + row[i] < src.rows && src.col_ok(k0 + col[i]));
-    const void* g = ok ? static_cast<const void*>(base + off[i])
+    const bool ok = inside || (r0 + row0 + i * kRowStep < src.rows && src.col_ok(k0 + col0));
+    const void* g = ok ? static_cast<const void*>(base + off0 + i * step)
                        : static_cast<const void*>(kZeroChunk);
     dma16(g, tile + (i * NW + wave) * kWave);
   }
@@ -135,13 +137,16 @@ struct PlainA {
   __device__ __forceinline__ half8 apply(half8 f, int) const { return f; }
 };
 
-// Main loop, per stage kt: wait until stage kt has landed, one barrier (stage kt visible; every
-// wavefront is done with stage kt - 1, whose buffer is refilled next), then for each 16-column
-// substep: read the next substep's fragments, issue half of the MFMAs, issue this substep's
-// share of the loads of stage kt + S - 1, issue the other half of the MFMAs. Spreading the
-// LDS-direct loads between MFMAs keeps the texture unit's queue short, so a wavefront never
-// stalls in issue with the matrix core idle (issued as one burst after the barrier, the loads
-// of a 256 x 256 x 64 stage held every wavefront for ~1000 cycles). sched_barrier pins that order.
+// Main loop, per stage kt: wait until stage kt has landed and this wavefront's fragment reads of
+// stage kt - 1 have returned, one barrier (stage kt visible; every wavefront is done with stage
+// kt - 1, whose buffer is refilled next), then five MFMA groups: the last substep of stage
+// kt - 1 (its fragments are already in registers, so these MFMAs cover the latency of the first
+// fragment reads of stage kt), then substeps 0 .. KS - 2 of stage kt, each after the reads of the
+// next substep's fragments. Each group issues its share of the loads of stage kt + S - 1 between
+// its two halves. Spreading the LDS-direct loads between MFMAs keeps the texture unit's queue
+// short, so a wavefront never stalls in issue with the matrix core idle (issued as one burst
+// after the barrier, the loads of a 256 x 256 x 64 stage held every wavefront for ~1000
+// cycles). sched_barrier pins that order.
 template <int BM, int BN, int WM, int WN, int BK, int S, class SrcA, class SrcB, class Epi,
           class FX = PlainA>
 __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_begin, int k_end,
@@ -221,30 +226,46 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
     }
   }
 
+  // The last substep of stage kt - 1 is multiplied after the barrier of stage kt: its fragments
+  // are already in registers, so its MFMAs cover the latency of the first fragment reads of
+  // stage kt. Before the barrier each wavefront waits for its own reads (the buffer they read
+  // from is refilled after it).
+  static_assert(KS % 2 == 0, "substep buffers alternate within a stage");
   for (int kt = 0; kt < n_kt; ++kt) {
-    // stage kt has landed once at most the loads of stages kt + 1 .. kt + S - 2 are outstanding
     if (kt + S - 2 < n_kt) {
       wait_vmcnt<(S - 2) * kDma>();
     } else {
       wait_vmcnt<0>();
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own fragment reads have landed
     lds_barrier();
     fx.advance();
     if (kt + 1 < n_kt) fx.prefetch(k_begin + (kt + 1) * BK);
-    const int kl = kt + S - 1;  // the stage loaded during this one
+    const int kl = kt + S - 1;
     const bool load = kl < n_kt;
     const bool ia = load && inside_a(kl), ib = load && inside_b(kl);
     read(kt, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt > 0) mfma(1, 0, kHalf);
+    __builtin_amdgcn_sched_barrier(0);
+    if (load) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+      for (int q = 0; q < kPart; ++q)
+        if (q < kDma) issue(kl, q, ia, ib);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt > 0) mfma(1, kHalf, TM * TN);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
       const int b = ks & 1;
-      if (ks + 1 < KS) read(kt, ks + 1, b ^ 1);
+      read(kt, ks + 1, b ^ 1);
       __builtin_amdgcn_sched_barrier(0);
       mfma(b, 0, kHalf);
       __builtin_amdgcn_sched_barrier(0);
       if (load) {
 #pragma unroll
-        for (int q = ks * kPart; q < (ks + 1) * kPart; ++q)
+        for (int q = (ks + 1) * kPart; q < (ks + 2) * kPart; ++q)
           if (q < kDma) issue(kl, q, ia, ib);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -252,6 +273,7 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if (n_kt > 0) mfma(1, 0, TM * TN);
   epi.template apply<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds);
 }
 
