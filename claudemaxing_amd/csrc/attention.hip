@@ -1,0 +1,752 @@
+// Causal grouped-query attention over a packed batch of variable-length rows (gfx950):
+// forward, and backward as dQ / dK+dV passes, on v_mfma_f32_32x32x16_f16 with fp32
+// accumulation and fp32 softmax statistics.
+//
+// Replaces, for the packed batch of the fused training forward, what transformers' sdpa
+// attention computes from the packed block-diagonal causal mask (the reference builds that mask
+// in lm_head_loss.py:332-336 and hands it to grouped SDPA, attention.py:332-373): every query at
+// row position t attends the keys of its own row at positions 0..t. Here no mask exists: the
+// row bounds are kernel arguments, and only the blocks on or below each row's diagonal are
+// visited.
+//
+// Layout. Rows are laid out "row-aligned" in a padded position space: row r starts at position
+// pstart[r] = sum over earlier rows of round_up(len, 64), so every 64-token block of a row
+// starts 64-aligned and the MFMA operand tiles are whole 16-byte chunks. A relayout pass writes
+// fp16 copies of the operands in that space, zero in the pad slots:
+//   natural    X16[head][pos][d]                      (d contiguous)
+//   transposed XT16[head][d][pos] with the positions of every 16-group stored in the order
+//              0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the position swapped).
+// The order is the one in which a lane of a 32x32 MFMA accumulator holds its 16 rows: lane l
+// holds rows (e/4)*8 + (l/32)*4 + e%4, so accumulator elements 8j..8j+7 are, in that order, the 8
+// operand slots of k-step j for half l/32. A probability tile computed as an accumulator thus
+// feeds the next MFMA straight from registers, against a transposed operand tile read as one
+// 16-byte chunk per lane.
+//
+// Forward, per (64-query block, head): S^T = K Q^T (lane = query, so the row statistics are
+// lane-local up to one shuffle between the two lane halves), online softmax in the log2 domain,
+// O^T += V^T P^T. The log2-domain log-sum-exp of every position is kept for the backward.
+// Backward: Delta = rowsum(dO * O); per (64-key block, query head) S = Q K^T and dP = dO V^T,
+// P = exp2(S*c - lse2), dS = P (dP - Delta), dV^T += dO^T P, dK^T += Q^T dS, written as per-head
+// partials and summed over the heads of each key/value group by a last pass (no atomics: the
+// results are the same bits on every run); per (64-query block, head) S^T and dP^T again and
+// dQ^T += K^T dS^T.
+#include "common.h"
+#include "gemm_lds.h"
+
+namespace {
+
+using cm::gemm::floatx16;
+using cm::gemm::half8;
+
+constexpr int kD = 128;       // head dimension
+constexpr int kBlk = 64;      // tokens per block (rows are padded to multiples of it)
+constexpr int kMaxRows = 128; // rows of one packed batch
+constexpr int kThreads = 128; // two wavefronts of 32 queries (or keys) each
+
+struct Rows {
+  int start[kMaxRows + 1];   // first real token of row r; start[n] = number of tokens
+  int pstart[kMaxRows + 1];  // first padded position of row r (multiples of kBlk)
+  int n;
+};
+
+// Row holding padded block b (pstart[r] / kBlk <= b < pstart[r + 1] / kBlk).
+__device__ __forceinline__ int row_of_block(const Rows& rows, int b) {
+  int r = 0;
+  while (r + 1 < rows.n && rows.pstart[r + 1] / kBlk <= b) ++r;
+  return r;
+}
+
+// Stored slot of position p inside its 16-group (an involution: bits 2 and 3 swapped).
+__device__ __forceinline__ int perm16(int p) {
+  return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);
+}
+
+__device__ __forceinline__ floatx16 mfma(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 zero16() {
+  floatx16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// Accumulator elements 8j..8j+7 as the fp16 operand of k-step j.
+__device__ __forceinline__ half8 frag_of(const floatx16& a, int j) {
+  half8 f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = static_cast<_Float16>(a[8 * j + i]);
+  return f;
+}
+
+// Eight consecutive elements of a (fp32 or fp16) tensor as fp16 (round to nearest even).
+__device__ __forceinline__ half8 load8(const void* base, int dtype, int64_t off) {
+  half8 f;
+  if (dtype == CM_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+    const float4 a = p[0], b = p[1];
+    f[0] = static_cast<_Float16>(a.x); f[1] = static_cast<_Float16>(a.y);
+    f[2] = static_cast<_Float16>(a.z); f[3] = static_cast<_Float16>(a.w);
+    f[4] = static_cast<_Float16>(b.x); f[5] = static_cast<_Float16>(b.y);
+    f[6] = static_cast<_Float16>(b.z); f[7] = static_cast<_Float16>(b.w);
+  } else {
+    f = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(base) + off);
+  }
+  return f;
+}
+
+__device__ __forceinline__ half8 zero8() {
+  half8 f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = static_cast<_Float16>(0.0f);
+  return f;
+}
+
+// LDS tiles filled by global_load_lds_dwordx4 (64 lanes x 16 bytes into 64 consecutive slots).
+// A tile has ROWS rows of CH 16-byte chunks; the chunk of (row, logical c) is stored at
+// physical chunk c ^ swz(row), chosen so that a fragment read (16 consecutive rows at one
+// logical chunk per 16 lanes) hits 16 distinct bank groups:
+//   CH = 16 (256-byte rows): row & 15;  CH = 8: (row >> 1) & 7;  CH = 4: (row >> 2) & 3.
+template <int CH>
+__device__ __forceinline__ int swz(int row) {
+  return CH == 16 ? (row & 15) : CH == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+template <int CH>
+__device__ __forceinline__ half8 frag(const uint4* tile, int row, int c) {
+  return __builtin_bit_cast(half8, tile[row * CH + (c ^ swz<CH>(row))]);
+}
+
+// Issue this thread's loads of a ROWS x CH tile whose row i starts at src + i * row_bytes.
+template <int ROWS, int CH>
+__device__ __forceinline__ void load_tile(uint4* tile, const void* src, int64_t row_bytes,
+                                          int wave, int lane) {
+  constexpr int kNW = kThreads / cm::kWave;
+  constexpr int kPer = ROWS * CH / kThreads;
+  static_assert(kPer * kThreads == ROWS * CH, "tile chunks split over the threads");
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = (i * kNW + wave) * cm::kWave + lane;
+    const int row = c / CH, phys = c % CH;
+    const char* g = static_cast<const char*>(src) + row * row_bytes + (phys ^ swz<CH>(row)) * 16;
+    cm::gemm::dma16(g, tile + (i * kNW + wave) * cm::kWave);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Relayout: fp16 natural and/or transposed copies of a [heads][N][D] tensor in the padded
+// position space, and optionally Delta = rowsum(X * O) (X = dO).
+struct Job {
+  const void* src;
+  int64_t sh, st;       // element strides of src (head, token); d is contiguous
+  _Float16* nat;        // [heads][n_pad][D] or null
+  _Float16* tr;         // [heads][D][n_pad] (16-groups permuted) or null
+  const _Float16* o;    // with delta: O, element (t, h, d) at o[t * so_t + h * D + d]
+  float* delta;         // [heads][n_pad] or null
+  int64_t so_t;
+  int dtype;
+  int heads;
+};
+
+struct Jobs {
+  Job job[4];
+  int first[4];  // first blockIdx.y of each job
+  int n;
+};
+
+__global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, Rows rows, int n_pad) {
+  __shared__ _Float16 tile[kD * kBlk];  // transposed staging [d][slot]
+  const int y = blockIdx.y;
+  // the job of this blockIdx.y, selected with static indices only
+  Job job = jobs.job[0];
+  int first = 0;
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    if (i < jobs.n && y >= jobs.first[i]) {
+      job = jobs.job[i];
+      first = jobs.first[i];
+    }
+  }
+  const int h = y - first;
+  const int b = blockIdx.x;
+  const int r = row_of_block(rows, b);
+  const int len = rows.start[r + 1] - rows.start[r];
+  const int local0 = (b - rows.pstart[r] / kBlk) * kBlk;
+  const int pos0 = b * kBlk;
+  for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
+    const int t = c / (kD / 8), ch = c % (kD / 8);
+    const int local = local0 + t;
+    const bool ok = local < len;
+    const int64_t tok = rows.start[r] + local;
+    const half8 x = ok ? load8(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8) : zero8();
+    if (job.nat)
+      *reinterpret_cast<half8*>(job.nat + (static_cast<int64_t>(h) * n_pad + pos0 + t) * kD +
+                                ch * 8) = x;
+    if (job.tr) {
+      const int slot = (t & ~15) | perm16(t & 15);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tile[(ch * 8 + i) * kBlk + slot] = x[i];
+    }
+    if (job.delta) {
+      float d = 0.0f;
+      if (ok) {
+        const half8 o = *reinterpret_cast<const half8*>(job.o + tok * job.so_t + h * kD + ch * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d += static_cast<float>(x[i]) * static_cast<float>(o[i]);
+      }
+      // the 16 chunks of a token are 16 consecutive lanes
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) d += __shfl_xor(d, m, cm::kWave);
+      if (ch == 0) job.delta[static_cast<int64_t>(h) * n_pad + pos0 + t] = d;
+    }
+  }
+  if (!job.tr) return;
+  __syncthreads();
+  for (int c = threadIdx.x; c < kD * (kBlk / 8); c += 256) {
+    const int d = c / (kBlk / 8), ch = c % (kBlk / 8);
+    *reinterpret_cast<uint4*>(job.tr + (static_cast<int64_t>(h) * kD + d) * n_pad + pos0 +
+                              ch * 8) = *reinterpret_cast<const uint4*>(tile + d * kBlk + ch * 8);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Forward. Block (b, h): 64 queries of one row, query head h (key/value head h / hpg); wavefront
+// w owns queries 32w..32w+31 of the block. Loop over the row's 64-key blocks 0..qb.
+constexpr int kKTile = kBlk * (kD / 8);   // K tile: 64 keys x 16 chunks
+constexpr int kVTile = kD * (kBlk / 8);   // V^T tile: 128 d x 8 chunks
+
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
+    const void* __restrict__ q, int q_dtype, int64_t sq_h, int64_t sq_t,
+    const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16, Rows rows, int n_pad,
+    int hpg, int H, float c_log2, _Float16* __restrict__ out, float* __restrict__ lse2) {
+  __shared__ uint4 lds[2][kKTile + kVTile];
+  const int h = blockIdx.y, g = h / hpg;
+  const int b = blockIdx.x;
+  const int r = row_of_block(rows, b);
+  const int qb = b - rows.pstart[r] / kBlk;
+  const int len = rows.start[r + 1] - rows.start[r];
+  const int p0 = rows.pstart[r];
+  const int lane = threadIdx.x % cm::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int hh = lane / 32, ln = lane % 32;
+  const int ql = qb * kBlk + wave * 32 + ln;  // query position in the row
+  const bool q_ok = ql < len;
+
+  const _Float16* kbase = k16 + (static_cast<int64_t>(g) * n_pad + p0) * kD;
+  const _Float16* vbase = vt16 + static_cast<int64_t>(g) * kD * n_pad + p0;
+  auto issue = [&](int jb, int st) {
+    load_tile<kBlk, kD / 8>(lds[st], kbase + jb * kBlk * kD, kD * 2, wave, lane);
+    load_tile<kD, kBlk / 8>(lds[st] + kKTile, vbase + jb * kBlk, n_pad * 2, wave, lane);
+  };
+  issue(0, 0);
+
+  half8 qf[kD / 16];
+  {
+    const int64_t off = h * sq_h + static_cast<int64_t>(rows.start[r] + (q_ok ? ql : 0)) * sq_t;
+#pragma unroll
+    for (int ds = 0; ds < kD / 16; ++ds)
+      qf[ds] = q_ok ? load8(q, q_dtype, off + ds * 16 + hh * 8) : zero8();
+  }
+  floatx16 o[kD / 32];
+#pragma unroll
+  for (int i = 0; i < kD / 32; ++i) o[i] = zero16();
+  float m = -__builtin_huge_valf(), l = 0.0f;
+
+  for (int jb = 0; jb <= qb; ++jb) {
+    const int st = jb & 1;
+    cm::gemm::wait_vmcnt<0>();
+    cm::gemm::lds_barrier();
+    if (jb < qb) issue(jb + 1, st ^ 1);
+    const uint4* kt = lds[st];
+    const uint4* vt = lds[st] + kKTile;
+    floatx16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = zero16();
+#pragma unroll
+      for (int ds = 0; ds < kD / 16; ++ds)
+        s[t] = mfma(frag<kD / 8>(kt, t * 32 + ln, ds * 2 + hh), qf[ds], s[t]);
+    }
+    // scale to the log2 domain, causal mask on the diagonal block, online softmax
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = jb * kBlk + t * 32 + (e / 4) * 8 + hh * 4 + e % 4;
+        const float v = key <= ql ? s[t][e] * c_log2 : -__builtin_huge_valf();
+        s[t][e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, cm::kWave));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = exp2f(m - m_new);
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = exp2f(s[t][e] - m_new);
+        s[t][e] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 32, cm::kWave);
+    l = l * alpha + sum;
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+    half8 pf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pf[ks] = frag_of(s[ks / 2], ks % 2);
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        o[dt] = mfma(frag<kBlk / 8>(vt, dt * 32 + ln, ks * 2 + hh), pf[ks], o[dt]);
+  }
+
+  if (hh == 0) lse2[static_cast<int64_t>(h) * n_pad + p0 + ql] = m + __log2f(l);
+  if (!q_ok) return;
+  const float inv = 1.0f / l;
+  _Float16* orow = out + (static_cast<int64_t>(rows.start[r] + ql) * H + h) * kD;
+#pragma unroll
+  for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+      h4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(o[dt][g4 * 4 + i] * inv);
+      *reinterpret_cast<h4*>(orow + dt * 32 + g4 * 8 + hh * 4) = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward, dK and dV. Block (b, h): 64 keys of one row (wavefront w owns keys 32w..32w+31)
+// against query head h; loop over the row's 32-query tiles from the block's first key on.
+// Writes the head's partial dK (times the softmax scale) and dV, fp32 [H][n_pad][D].
+constexpr int kQTile = 32 * (kD / 8);   // Q / dO tile: 32 queries x 16 chunks
+constexpr int kQTTile = kD * (32 / 8);  // Q^T / dO^T tile: 128 d x 4 chunks
+
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
+    const _Float16* __restrict__ q16, const _Float16* __restrict__ qt16,
+    const _Float16* __restrict__ do16, const _Float16* __restrict__ dot16,
+    const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
+    const float* __restrict__ lse2, const float* __restrict__ delta, Rows rows, int n_pad,
+    int hpg, float c_log2, float scale, float* __restrict__ dk_part,
+    float* __restrict__ dv_part) {
+  __shared__ uint4 lds[2][2 * kQTile + 2 * kQTTile];
+  const int h = blockIdx.y, g = h / hpg;
+  const int b = blockIdx.x;
+  const int r = row_of_block(rows, b);
+  const int kb = b - rows.pstart[r] / kBlk;
+  const int len = rows.start[r + 1] - rows.start[r];
+  const int p0 = rows.pstart[r];
+  const int lane = threadIdx.x % cm::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int hh = lane / 32, ln = lane % 32;
+  const int key = kb * kBlk + wave * 32 + ln;  // this lane's key (row position)
+
+  const int64_t hq = static_cast<int64_t>(h) * n_pad;
+  auto issue = [&](int qt, int st) {
+    const int64_t pos = p0 + qt * 32;
+    uint4* t = lds[st];
+    load_tile<32, kD / 8>(t, q16 + (hq + pos) * kD, kD * 2, wave, lane);
+    load_tile<32, kD / 8>(t + kQTile, do16 + (hq + pos) * kD, kD * 2, wave, lane);
+    load_tile<kD, 32 / 8>(t + 2 * kQTile, qt16 + static_cast<int64_t>(h) * kD * n_pad + pos,
+                          n_pad * 2, wave, lane);
+    load_tile<kD, 32 / 8>(t + 2 * kQTile + kQTTile,
+                          dot16 + static_cast<int64_t>(h) * kD * n_pad + pos, n_pad * 2, wave,
+                          lane);
+  };
+  const int qt_first = 2 * kb;
+  const int qt_end = (len + 31) / 32;
+  issue(qt_first, 0);
+
+  half8 kf[kD / 16], vf[kD / 16];
+  {
+    const int64_t off = (static_cast<int64_t>(g) * n_pad + p0 + key) * kD;
+#pragma unroll
+    for (int ds = 0; ds < kD / 16; ++ds) {
+      kf[ds] = *reinterpret_cast<const half8*>(k16 + off + ds * 16 + hh * 8);
+      vf[ds] = *reinterpret_cast<const half8*>(v16 + off + ds * 16 + hh * 8);
+    }
+  }
+  floatx16 dk[kD / 32], dv[kD / 32];
+#pragma unroll
+  for (int i = 0; i < kD / 32; ++i) {
+    dk[i] = zero16();
+    dv[i] = zero16();
+  }
+
+  for (int qt = qt_first; qt < qt_end; ++qt) {
+    const int st = (qt - qt_first) & 1;
+    // this lane's 16 queries: positions qt*32 + (e/4)*8 + hh*4 + e%4
+    float ls[16], dl[16];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int64_t at = hq + p0 + qt * 32 + g4 * 8 + hh * 4;
+      const float4 a = *reinterpret_cast<const float4*>(lse2 + at);
+      const float4 d = *reinterpret_cast<const float4*>(delta + at);
+      ls[g4 * 4 + 0] = a.x; ls[g4 * 4 + 1] = a.y; ls[g4 * 4 + 2] = a.z; ls[g4 * 4 + 3] = a.w;
+      dl[g4 * 4 + 0] = d.x; dl[g4 * 4 + 1] = d.y; dl[g4 * 4 + 2] = d.z; dl[g4 * 4 + 3] = d.w;
+    }
+    cm::gemm::wait_vmcnt<0>();
+    cm::gemm::lds_barrier();
+    if (qt + 1 < qt_end) issue(qt + 1, st ^ 1);
+    // wavefront 1's keys start 32 positions later: its first tile is wholly above the diagonal
+    if (qt * 32 + 31 < kb * kBlk + wave * 32) continue;
+    const uint4* qs = lds[st];
+    const uint4* dos = qs + kQTile;
+    const uint4* qts = qs + 2 * kQTile;
+    const uint4* dots = qts + kQTTile;
+    floatx16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int ds = 0; ds < kD / 16; ++ds) {
+      s = mfma(frag<kD / 8>(qs, ln, ds * 2 + hh), kf[ds], s);
+      dp = mfma(frag<kD / 8>(dos, ln, ds * 2 + hh), vf[ds], dp);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int qpos = qt * 32 + (e / 4) * 8 + hh * 4 + e % 4;
+      const bool ok = key <= qpos && qpos < len;
+      const float p = ok ? exp2f(s[e] * c_log2 - ls[e]) : 0.0f;
+      s[e] = p;
+      dp[e] = ok ? p * (dp[e] - dl[e]) : 0.0f;
+    }
+    half8 pf[2], sf[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      pf[j] = frag_of(s, j);
+      sf[j] = frag_of(dp, j);
+    }
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        dv[dt] = mfma(frag<32 / 8>(dots, dt * 32 + ln, j * 2 + hh), pf[j], dv[dt]);
+        dk[dt] = mfma(frag<32 / 8>(qts, dt * 32 + ln, j * 2 + hh), sf[j], dk[dt]);
+      }
+  }
+
+  float* dkr = dk_part + (hq + p0 + key) * kD;
+  float* dvr = dv_part + (hq + p0 + key) * kD;
+#pragma unroll
+  for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = dt * 32 + g4 * 8 + hh * 4;
+      *reinterpret_cast<float4*>(dkr + d) =
+          make_float4(dk[dt][g4 * 4] * scale, dk[dt][g4 * 4 + 1] * scale,
+                      dk[dt][g4 * 4 + 2] * scale, dk[dt][g4 * 4 + 3] * scale);
+      *reinterpret_cast<float4*>(dvr + d) = make_float4(dv[dt][g4 * 4], dv[dt][g4 * 4 + 1],
+                                                        dv[dt][g4 * 4 + 2], dv[dt][g4 * 4 + 3]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward, dQ. Block (b, h): 64 queries of one row, head h; loop over 32-key tiles up to the
+// diagonal.
+constexpr int kKVTile = 32 * (kD / 8);  // K / V tile: 32 keys x 16 chunks
+constexpr int kKTTile = kD * (32 / 8);  // K^T tile: 128 d x 4 chunks
+
+template <typename OT>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
+    const _Float16* __restrict__ q16, const _Float16* __restrict__ do16,
+    const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
+    const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
+    const float* __restrict__ delta, Rows rows, int n_pad, int hpg, float c_log2, float scale,
+    OT* __restrict__ dq) {
+  __shared__ uint4 lds[2][2 * kKVTile + kKTTile];
+  const int h = blockIdx.y, g = h / hpg;
+  const int H = gridDim.y;
+  const int b = blockIdx.x;
+  const int r = row_of_block(rows, b);
+  const int qb = b - rows.pstart[r] / kBlk;
+  const int len = rows.start[r + 1] - rows.start[r];
+  const int p0 = rows.pstart[r];
+  const int lane = threadIdx.x % cm::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int hh = lane / 32, ln = lane % 32;
+  const int ql = qb * kBlk + wave * 32 + ln;
+
+  const int64_t gk = static_cast<int64_t>(g) * n_pad;
+  auto issue = [&](int kt, int st) {
+    const int64_t pos = p0 + kt * 32;
+    uint4* t = lds[st];
+    load_tile<32, kD / 8>(t, k16 + (gk + pos) * kD, kD * 2, wave, lane);
+    load_tile<32, kD / 8>(t + kKVTile, v16 + (gk + pos) * kD, kD * 2, wave, lane);
+    load_tile<kD, 32 / 8>(t + 2 * kKVTile, kt16 + static_cast<int64_t>(g) * kD * n_pad + pos,
+                          n_pad * 2, wave, lane);
+  };
+  const int kt_end = 2 * qb + 2;
+  issue(0, 0);
+
+  const int64_t at = static_cast<int64_t>(h) * n_pad + p0 + ql;
+  half8 qf[kD / 16], of[kD / 16];
+#pragma unroll
+  for (int ds = 0; ds < kD / 16; ++ds) {
+    qf[ds] = *reinterpret_cast<const half8*>(q16 + at * kD + ds * 16 + hh * 8);
+    of[ds] = *reinterpret_cast<const half8*>(do16 + at * kD + ds * 16 + hh * 8);
+  }
+  const float ls = lse2[at], dl = delta[at];
+  floatx16 acc[kD / 32];
+#pragma unroll
+  for (int i = 0; i < kD / 32; ++i) acc[i] = zero16();
+
+  for (int kt = 0; kt < kt_end; ++kt) {
+    const int st = kt & 1;
+    cm::gemm::wait_vmcnt<0>();
+    cm::gemm::lds_barrier();
+    if (kt + 1 < kt_end) issue(kt + 1, st ^ 1);
+    // wavefront 0's queries end 32 positions earlier: its last tile is wholly above the diagonal
+    if (kt * 32 > qb * kBlk + wave * 32 + 31) continue;
+    const uint4* ks = lds[st];
+    const uint4* vs = ks + kKVTile;
+    const uint4* kts = ks + 2 * kKVTile;
+    floatx16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int ds = 0; ds < kD / 16; ++ds) {
+      s = mfma(frag<kD / 8>(ks, ln, ds * 2 + hh), qf[ds], s);
+      dp = mfma(frag<kD / 8>(vs, ln, ds * 2 + hh), of[ds], dp);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kpos = kt * 32 + (e / 4) * 8 + hh * 4 + e % 4;
+      const bool ok = kpos <= ql;
+      const float p = ok ? exp2f(s[e] * c_log2 - ls) : 0.0f;
+      dp[e] = ok ? p * (dp[e] - dl) : 0.0f;
+    }
+    half8 sf[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sf[j] = frag_of(dp, j);
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[dt] = mfma(frag<32 / 8>(kts, dt * 32 + ln, j * 2 + hh), sf[j], acc[dt]);
+  }
+
+  if (ql >= len) return;
+  OT* row = dq + (static_cast<int64_t>(h) * rows.start[rows.n] + rows.start[r] + ql) * kD;
+  (void)H;
+#pragma unroll
+  for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      row[dt * 32 + (e / 4) * 8 + hh * 4 + e % 4] = cm::from_f32<OT>(acc[dt][e] * scale);
+}
+
+// dK, dV = sum of the partials of the query heads of each group, [G][N][D] in the output dtype.
+// Block (b, g): the 64 padded positions of block b, key/value head g.
+template <typename OT>
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
+    const float* __restrict__ dk_part, const float* __restrict__ dv_part, Rows rows, int n_pad,
+    int hpg, OT* __restrict__ dk, OT* __restrict__ dv) {
+  const int b = blockIdx.x, g = blockIdx.y;
+  const int r = row_of_block(rows, b);
+  const int len = rows.start[r + 1] - rows.start[r];
+  const int local0 = (b - rows.pstart[r] / kBlk) * kBlk;
+  const int n_tok = rows.start[rows.n];
+  for (int i = threadIdx.x; i < kBlk * (kD / 4); i += 256) {
+    const int t = i / (kD / 4), d = (i % (kD / 4)) * 4;
+    if (local0 + t >= len) continue;
+    const int64_t pos = static_cast<int64_t>(b) * kBlk + t;
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int j = 0; j < hpg; ++j) {
+      const int64_t at = ((static_cast<int64_t>(g) * hpg + j) * n_pad + pos) * kD + d;
+      const float4 a = *reinterpret_cast<const float4*>(dk_part + at);
+      const float4 c = *reinterpret_cast<const float4*>(dv_part + at);
+      sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
+      sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
+    }
+    const int64_t o = (static_cast<int64_t>(g) * n_tok + rows.start[r] + local0 + t) * kD + d;
+    dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
+    dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
+    dv[o] = cm::from_f32<OT>(sv.x); dv[o + 1] = cm::from_f32<OT>(sv.y);
+    dv[o + 2] = cm::from_f32<OT>(sv.z); dv[o + 3] = cm::from_f32<OT>(sv.w);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+int build_rows(const int64_t* bounds, int n_rows, Rows& rows, int64_t& n_pad) {
+  if (!bounds || n_rows < 1 || n_rows > kMaxRows || bounds[0] != 0) return hipErrorInvalidValue;
+  rows.n = n_rows;
+  int64_t p = 0;
+  for (int r = 0; r <= n_rows; ++r) {
+    if (r > 0 && bounds[r] < bounds[r - 1]) return hipErrorInvalidValue;
+    if (bounds[r] > 0x3fffffff) return hipErrorInvalidValue;
+    rows.start[r] = static_cast<int>(bounds[r]);
+    rows.pstart[r] = static_cast<int>(p);
+    if (r < n_rows) p += (bounds[r + 1] - bounds[r] + kBlk - 1) / kBlk * kBlk;
+  }
+  n_pad = p;
+  return 0;
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// 16-byte aligned base and strides that keep every 8-element chunk 16-byte aligned.
+bool aligned_operand(const void* p, int dtype, int64_t sh, int64_t st) {
+  const int64_t mult = dtype == CM_F32 ? 4 : 8;
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && sh % mult == 0 && st % mult == 0;
+}
+
+struct Workspace {
+  char* p;
+  size_t used = 0, size;
+  template <typename T>
+  T* take(size_t count) {
+    T* at = reinterpret_cast<T*>(p + used);
+    used += align256(count * sizeof(T));
+    return at;
+  }
+};
+
+size_t fwd_ws_bytes(int64_t n_pad, int G) {
+  return 2 * align256(static_cast<size_t>(G) * n_pad * kD * 2);
+}
+
+size_t bwd_ws_bytes(int64_t n_pad, int H, int G) {
+  const size_t hq = align256(static_cast<size_t>(H) * n_pad * kD * 2);
+  const size_t gk = align256(static_cast<size_t>(G) * n_pad * kD * 2);
+  const size_t part = align256(static_cast<size_t>(H) * n_pad * kD * 4);
+  return 4 * hq + 3 * gk + align256(static_cast<size_t>(H) * n_pad * 4) + 2 * part;
+}
+
+}  // namespace
+
+extern "C" int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows) {
+  Rows rows;
+  int64_t n_pad;
+  if (build_rows(bounds, n_rows, rows, n_pad)) return -1;
+  return n_pad;
+}
+
+extern "C" int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim,
+                                           int backward) {
+  if (n_pad < 0 || H <= 0 || G <= 0 || head_dim != kD) return -1;
+  return static_cast<int64_t>(backward ? bwd_ws_bytes(n_pad, H, G) : fwd_ws_bytes(n_pad, G));
+}
+
+extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                           int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                           int64_t sv_h, int64_t sv_t, const int64_t* bounds, int n_rows, int H,
+                           int G, int head_dim, float scale, void* out, float* lse2,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  Rows rows;
+  int64_t n_pad;
+  CM_CHECK_ARG(build_rows(bounds, n_rows, rows, n_pad) == 0);
+  CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
+  CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
+               (v_dtype == CM_F32 || v_dtype == CM_F16));
+  if (rows.start[n_rows] == 0) return 0;
+  CM_CHECK_ARG(q && k && v && out && lse2 && workspace);
+  CM_CHECK_ARG(aligned_operand(q, q_dtype, sq_h, sq_t) && aligned_operand(k, k_dtype, sk_h, sk_t) &&
+               aligned_operand(v, v_dtype, sv_h, sv_t));
+  CM_CHECK_ARG((reinterpret_cast<uintptr_t>(out) & 7) == 0 &&
+               (reinterpret_cast<uintptr_t>(workspace) & 255) == 0);
+  CM_CHECK_ARG(workspace_bytes >= static_cast<int64_t>(fwd_ws_bytes(n_pad, G)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Workspace ws{static_cast<char*>(workspace), 0, static_cast<size_t>(workspace_bytes)};
+  _Float16* k16 = ws.take<_Float16>(static_cast<size_t>(G) * n_pad * kD);
+  _Float16* vt16 = ws.take<_Float16>(static_cast<size_t>(G) * n_pad * kD);
+  Jobs jobs{};
+  jobs.job[0] = Job{k, sk_h, sk_t, k16, nullptr, nullptr, nullptr, 0, k_dtype, G};
+  jobs.job[1] = Job{v, sv_h, sv_t, nullptr, vt16, nullptr, nullptr, 0, v_dtype, G};
+  jobs.first[1] = G;
+  jobs.n = 2;
+  const int n_blocks = static_cast<int>(n_pad / kBlk);
+  hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * G), dim3(256), 0, s, jobs, rows,
+                     static_cast<int>(n_pad));
+  if (int st = cm::launch_status()) return st;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q, q_dtype, sq_h,
+                     sq_t, k16, vt16, rows, static_cast<int>(n_pad), H / G, H,
+                     scale * 1.4426950408889634f, static_cast<_Float16*>(out), lse2);
+  return cm::launch_status();
+}
+
+extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                           int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                           int64_t sv_h, int64_t sv_t, const void* out, const void* dout,
+                           const float* lse2, const int64_t* bounds, int n_rows, int H, int G,
+                           int head_dim, float scale, void* dq, int dq_dtype, void* dk,
+                           void* dv, int dkv_dtype, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  Rows rows;
+  int64_t n_pad;
+  CM_CHECK_ARG(build_rows(bounds, n_rows, rows, n_pad) == 0);
+  CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
+  CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
+               (v_dtype == CM_F32 || v_dtype == CM_F16));
+  CM_CHECK_ARG((dq_dtype == CM_F32 || dq_dtype == CM_F16) &&
+               (dkv_dtype == CM_F32 || dkv_dtype == CM_F16));
+  if (rows.start[n_rows] == 0) return 0;
+  CM_CHECK_ARG(q && k && v && out && dout && lse2 && dq && dk && dv && workspace);
+  CM_CHECK_ARG(aligned_operand(q, q_dtype, sq_h, sq_t) && aligned_operand(k, k_dtype, sk_h, sk_t) &&
+               aligned_operand(v, v_dtype, sv_h, sv_t));
+  CM_CHECK_ARG((reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(dout) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(lse2) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(workspace) & 255) == 0);
+  CM_CHECK_ARG(workspace_bytes >= static_cast<int64_t>(bwd_ws_bytes(n_pad, H, G)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Workspace ws{static_cast<char*>(workspace), 0, static_cast<size_t>(workspace_bytes)};
+  const size_t nq = static_cast<size_t>(H) * n_pad * kD, nk = static_cast<size_t>(G) * n_pad * kD;
+  _Float16* q16 = ws.take<_Float16>(nq);
+  _Float16* qt16 = ws.take<_Float16>(nq);
+  _Float16* do16 = ws.take<_Float16>(nq);
+  _Float16* dot16 = ws.take<_Float16>(nq);
+  _Float16* k16 = ws.take<_Float16>(nk);
+  _Float16* v16 = ws.take<_Float16>(nk);
+  _Float16* kt16 = ws.take<_Float16>(nk);
+  float* delta = ws.take<float>(static_cast<size_t>(H) * n_pad);
+  float* dk_part = ws.take<float>(nq);
+  float* dv_part = ws.take<float>(nq);
+  const int np = static_cast<int>(n_pad);
+  const int n_blocks = np / kBlk;
+  // dO and O: [N][H][D] contiguous (the forward's output layout)
+  Jobs jobs{};
+  jobs.job[0] = Job{q, sq_h, sq_t, q16, qt16, nullptr, nullptr, 0, q_dtype, H};
+  jobs.job[1] = Job{dout, kD, static_cast<int64_t>(H) * kD, do16, dot16,
+                    static_cast<const _Float16*>(out), delta, static_cast<int64_t>(H) * kD,
+                    CM_F16, H};
+  jobs.job[2] = Job{k, sk_h, sk_t, k16, kt16, nullptr, nullptr, 0, k_dtype, G};
+  jobs.job[3] = Job{v, sv_h, sv_t, v16, nullptr, nullptr, nullptr, 0, v_dtype, G};
+  jobs.first[1] = H;
+  jobs.first[2] = 2 * H;
+  jobs.first[3] = 2 * H + G;
+  jobs.n = 4;
+  hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * H + 2 * G), dim3(256), 0, s, jobs,
+                     rows, np);
+  if (int st = cm::launch_status()) return st;
+  const float c_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q16, qt16,
+                     do16, dot16, k16, v16, lse2, delta, rows, np, H / G, c_log2, scale, dk_part,
+                     dv_part);
+  if (int st = cm::launch_status()) return st;
+  if (dq_dtype == CM_F32) {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(n_blocks, H), dim3(kThreads), 0, s, q16,
+                       do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
+                       static_cast<float*>(dq));
+  } else {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(n_blocks, H), dim3(kThreads), 0, s,
+                       q16, do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
+                       static_cast<_Float16*>(dq));
+  }
+  if (int st = cm::launch_status()) return st;
+  if (dkv_dtype == CM_F32) {
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(n_blocks, G), dim3(256), 0, s,
+                       dk_part, dv_part, rows, np, H / G, static_cast<float*>(dk),
+                       static_cast<float*>(dv));
+  } else {
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(n_blocks, G), dim3(256), 0, s,
+                       dk_part, dv_part, rows, np, H / G, static_cast<_Float16*>(dk),
+                       static_cast<_Float16*>(dv));
+  }
+  return cm::launch_status();
+}

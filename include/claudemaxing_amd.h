@@ -184,6 +184,51 @@ int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t l
 int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_size,
                                      int64_t chunk_cols);
 
+/* ------------------------------------------------------------------------------------------ */
+/* Causal grouped-query attention over a packed batch of variable-length rows, forward. Replaces,
+ * for the packed batch of the fused training forward (solution/lm_head_loss.py:300-363, whose
+ * mask 332-336 is block-diagonal over the rows and causal inside each), the attention the
+ * reference computes with that dense mask through grouped SDPA (solution/attention.py:332-373,
+ * installed last by apply(), solution/__init__.py:25-34). No mask is read: query t of a row
+ * attends keys 0..t of the same row.
+ *   out[t, h, :] = sum_j softmax_j(scale * q[h,t] . k[h/(H/G), j]) v[h/(H/G), j]
+ * q [H][N][D] with element strides (sq_h, sq_t, 1); k, v [G][N][D] likewise; f32 or f16 inputs
+ * are rounded to fp16 (as fp16 autocast rounds them); fp16 MFMA products, fp32 accumulation and
+ * softmax. out fp16 [N][H][D] contiguous. lse2 f32 [H][n_pad] receives the log2-domain
+ * log-sum-exp of scale * q.k of every padded position (the backward's input).
+ * bounds: HOST array of n_rows + 1 row boundaries (0 = bounds[0] <= ... <= bounds[n_rows] = N),
+ * n_rows <= 128. n_pad = cm_attn_padded_tokens(bounds, n_rows) (rows padded to multiples of 64).
+ * head_dim must be 128, H a multiple of G. Bases 16-byte aligned (out 8), strides multiples of 8
+ * (f16) or 4 (f32) elements, workspace 256-byte aligned, cm_attn_workspace_bytes(n_pad, H, G,
+ * head_dim, 0) bytes.
+ */
+int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                int64_t sv_h, int64_t sv_t, const int64_t* bounds, int n_rows, int H, int G,
+                int head_dim, float scale, void* out, float* lse2, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Backward of cm_attn_fwd (the same q, k, v, bounds and scale; out and lse2 as it wrote them;
+ * dout fp16 [N][H][D] contiguous). Writes dq [H][N][D] (dq_dtype), dk and dv [G][N][D]
+ * (dkv_dtype), contiguous; f32 or f16. dk and dv sum the contributions of the H/G query heads of
+ * each group in a fixed order (no atomics: the same bits on every run). Workspace:
+ * cm_attn_workspace_bytes(n_pad, H, G, head_dim, 1) bytes, 256-byte aligned.
+ */
+int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                int64_t sv_h, int64_t sv_t, const void* out, const void* dout, const float* lse2,
+                const int64_t* bounds, int n_rows, int H, int G, int head_dim, float scale,
+                void* dq, int dq_dtype, void* dk, void* dv, int dkv_dtype, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Padded token count of a packed batch: sum over rows of round_up(length, 64); -1 for invalid
+ * bounds (not monotone, bounds[0] != 0, n_rows outside 1..128). */
+int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows);
+
+/* Workspace bytes of cm_attn_fwd (backward = 0) or cm_attn_bwd (backward = 1); -1 if the sizes
+ * are unsupported. */
+int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim, int backward);
+
 #ifdef __cplusplus
 }
 #endif
