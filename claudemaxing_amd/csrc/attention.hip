@@ -41,7 +41,8 @@ using cm::gemm::half8;
 constexpr int kD = 128;       // head dimension
 constexpr int kBlk = 64;      // tokens per block (rows are padded to multiples of it)
 constexpr int kMaxRows = 128; // rows of one packed batch
-constexpr int kThreads = 128; // two wavefronts of 32 queries (or keys) each
+constexpr int kThreads = 256; // two pairs of wavefronts of 32 queries (or keys) each
+constexpr int kPairThreads = 128;
 
 struct Rows {
   int start[kMaxRows + 1];   // first real token of row r; start[n] = number of tokens
@@ -118,13 +119,14 @@ __device__ __forceinline__ half8 frag(const uint4* tile, int row, int c) {
   return __builtin_bit_cast(half8, tile[row * CH + (c ^ swz<CH>(row))]);
 }
 
-// Issue this thread's loads of a ROWS x CH tile whose row i starts at src + i * row_bytes.
+// Issue this thread's loads of a ROWS x CH tile whose row i starts at src + i * row_bytes; the
+// two wavefronts of a pair (wave = 0, 1 within the pair) load a tile together.
 template <int ROWS, int CH>
 __device__ __forceinline__ void load_tile(uint4* tile, const void* src, int64_t row_bytes,
                                           int wave, int lane) {
-  constexpr int kNW = kThreads / cm::kWave;
-  constexpr int kPer = ROWS * CH / kThreads;
-  static_assert(kPer * kThreads == ROWS * CH, "tile chunks split over the threads");
+  constexpr int kNW = kPairThreads / cm::kWave;
+  constexpr int kPer = ROWS * CH / kPairThreads;
+  static_assert(kPer * kPairThreads == ROWS * CH, "tile chunks split over the pair");
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = (i * kNW + wave) * cm::kWave + lane;
@@ -133,6 +135,13 @@ __device__ __forceinline__ void load_tile(uint4* tile, const void* src, int64_t 
     cm::gemm::dma16(g, tile + (i * kNW + wave) * cm::kWave);
   }
 }
+
+// 128 bytes at src into LDS slots slot[0..7] (eight lanes of the pair's first wavefront).
+__device__ __forceinline__ void load_vec128(uint4* slot, const void* src, int wave, int lane) {
+  if (wave == 0 && lane < 8) cm::gemm::dma16(static_cast<const char*>(src) + lane * 16, slot);
+}
+
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------------------------
 // Relayout: fp16 natural and/or transposed copies of a [heads][N][D] tensor in the padded
@@ -184,7 +193,9 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, Rows rows
       *reinterpret_cast<half8*>(job.nat + (static_cast<int64_t>(h) * n_pad + pos0 + t) * kD +
                                 ch * 8) = x;
     if (job.tr) {
-      const int slot = (t & ~15) | perm16(t & 15);
+      // row d of the staging tile holds its 8-slot chunks XOR-swizzled by (d / 8) % 8, so the 16
+      // lanes of one token (16 values of d eight apart) write to 8 distinct banks, not one
+      const int slot = ((t & ~15) | perm16(t & 15)) ^ ((ch & 7) << 3);
 #pragma unroll
       for (int i = 0; i < 8; ++i) tile[(ch * 8 + i) * kBlk + slot] = x[i];
     }
@@ -205,14 +216,21 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, Rows rows
   __syncthreads();
   for (int c = threadIdx.x; c < kD * (kBlk / 8); c += 256) {
     const int d = c / (kBlk / 8), ch = c % (kBlk / 8);
+    const int pc = ch ^ ((d >> 3) & 7);
     *reinterpret_cast<uint4*>(job.tr + (static_cast<int64_t>(h) * kD + d) * n_pad + pos0 +
-                              ch * 8) = *reinterpret_cast<const uint4*>(tile + d * kBlk + ch * 8);
+                              ch * 8) = *reinterpret_cast<const uint4*>(tile + d * kBlk + pc * 8);
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Forward. Block (b, h): 64 queries of one row, query head h (key/value head h / hpg); wavefront
-// w owns queries 32w..32w+31 of the block. Loop over the row's 64-key blocks 0..qb.
+// The three attention kernels run four wavefronts per block in two pairs. Both pairs own the same
+// 64 queries (or keys), wavefront 2p + w the 32 of half w; the serial loop over the other side's
+// blocks is split between the pairs (pair p takes every other block), each pair double-buffers
+// its own tiles in its own LDS region, and at the end pair 1 hands its partial results to pair 0
+// through that region. Both pairs run the same number of iterations (one barrier each).
+
+// Forward. Block (b, h): 64 queries of one row, query head h (key/value head h / hpg). Pair p
+// takes the row's 64-key blocks p, p + 2, ... up to the diagonal block qb.
 constexpr int kKTile = kBlk * (kD / 8);   // K tile: 64 keys x 16 chunks
 constexpr int kVTile = kD * (kBlk / 8);   // V^T tile: 128 d x 8 chunks
 
@@ -220,7 +238,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
     const void* __restrict__ q, int q_dtype, int64_t sq_h, int64_t sq_t,
     const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16, Rows rows, int n_pad,
     int hpg, int H, float c_log2, _Float16* __restrict__ out, float* __restrict__ lse2) {
-  __shared__ uint4 lds[2][kKTile + kVTile];
+  constexpr int kStage = kKTile + kVTile;
+  __shared__ uint4 lds[2][2][kStage];  // [pair][stage]
   const int h = blockIdx.y, g = h / hpg;
   const int b = blockIdx.x;
   const int r = row_of_block(rows, b);
@@ -229,17 +248,19 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   const int p0 = rows.pstart[r];
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int pair = wave >> 1, wq = wave & 1;
   const int hh = lane / 32, ln = lane % 32;
-  const int ql = qb * kBlk + wave * 32 + ln;  // query position in the row
+  const int ql = qb * kBlk + wq * 32 + ln;  // query position in the row
   const bool q_ok = ql < len;
+  const int n_it = (qb + 2) / 2;
 
   const _Float16* kbase = k16 + (static_cast<int64_t>(g) * n_pad + p0) * kD;
   const _Float16* vbase = vt16 + static_cast<int64_t>(g) * kD * n_pad + p0;
   auto issue = [&](int jb, int st) {
-    load_tile<kBlk, kD / 8>(lds[st], kbase + jb * kBlk * kD, kD * 2, wave, lane);
-    load_tile<kD, kBlk / 8>(lds[st] + kKTile, vbase + jb * kBlk, n_pad * 2, wave, lane);
+    load_tile<kBlk, kD / 8>(lds[pair][st], kbase + jb * kBlk * kD, kD * 2, wq, lane);
+    load_tile<kD, kBlk / 8>(lds[pair][st] + kKTile, vbase + jb * kBlk, n_pad * 2, wq, lane);
   };
-  issue(0, 0);
+  if (pair <= qb) issue(pair, 0);
 
   half8 qf[kD / 16];
   {
@@ -251,15 +272,16 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   floatx16 o[kD / 32];
 #pragma unroll
   for (int i = 0; i < kD / 32; ++i) o[i] = zero16();
-  float m = -__builtin_huge_valf(), l = 0.0f;
+  float m = -__builtin_huge_valf(), l = 0.0f;  // reference max (log2 domain) and sum
 
-  for (int jb = 0; jb <= qb; ++jb) {
-    const int st = jb & 1;
+  for (int it = 0; it < n_it; ++it) {
+    const int jb = 2 * it + pair, st = it & 1;
     cm::gemm::wait_vmcnt<0>();
     cm::gemm::lds_barrier();
-    if (jb < qb) issue(jb + 1, st ^ 1);
-    const uint4* kt = lds[st];
-    const uint4* vt = lds[st] + kKTile;
+    if (jb + 2 <= qb) issue(jb + 2, st ^ 1);
+    if (jb > qb) continue;  // pair 1's last iteration when qb is even
+    const uint4* kt = lds[pair][st];
+    const uint4* vt = kt + kKTile;
     floatx16 s[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -268,36 +290,47 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
       for (int ds = 0; ds < kD / 16; ++ds)
         s[t] = mfma(frag<kD / 8>(kt, t * 32 + ln, ds * 2 + hh), qf[ds], s[t]);
     }
-    // scale to the log2 domain, causal mask on the diagonal block, online softmax
+    if (jb == qb) {  // the diagonal block: keys after the query are masked
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = jb * kBlk + t * 32 + (e / 4) * 8 + hh * 4 + e % 4;
+          s[t][e] = key <= ql ? s[t][e] : -__builtin_huge_valf();
+        }
+    }
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = jb * kBlk + t * 32 + (e / 4) * 8 + hh * 4 + e % 4;
-        const float v = key <= ql ? s[t][e] * c_log2 : -__builtin_huge_valf();
-        s[t][e] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, cm::kWave));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = exp2f(m - m_new);
+    // The exponentials are taken against a reference max m that moves only when some row's max
+    // exceeds it by more than 2^8 (then every row of the wavefront moves to its own max and O
+    // and l are rescaled): probabilities stay <= 256, exact to fp16's relative precision, and
+    // most blocks skip the rescale.
+    float alpha = 1.0f;
+    if (__builtin_amdgcn_ballot_w64(mx * c_log2 > m + 8.0f)) {
+      const float m_new = fmaxf(m, mx * c_log2);
+      alpha = exp2_raw(m - m_new);
+      m = m_new;
+#pragma unroll
+      for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+    }
+    const float m_new = m;
     float sum = 0.0f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = exp2f(s[t][e] - m_new);
+        const float p = exp2_raw(__builtin_fmaf(s[t][e], c_log2, -m_new));
         s[t][e] = p;
         sum += p;
       }
     sum += __shfl_xor(sum, 32, cm::kWave);
     l = l * alpha + sum;
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < kD / 32; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
     half8 pf[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) pf[ks] = frag_of(s[ks / 2], ks % 2);
@@ -308,7 +341,22 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
         o[dt] = mfma(frag<kBlk / 8>(vt, dt * 32 + ln, ks * 2 + hh), pf[ks], o[dt]);
   }
 
-  if (hh == 0) lse2[static_cast<int64_t>(h) * n_pad + p0 + ql] = m + __log2f(l);
+  // pair 1 hands (o, m, l) of its blocks to pair 0 through its LDS region
+  cm::gemm::lds_barrier();
+  float* xf = reinterpret_cast<float*>(lds[1][0]) + wq * 66 * cm::kWave + lane;
+  if (pair == 1) {
+#pragma unroll
+    for (int i = 0; i < kD / 2; ++i) xf[i * cm::kWave] = o[i / 16][i % 16];
+    xf[64 * cm::kWave] = m;
+    xf[65 * cm::kWave] = l;
+  }
+  cm::gemm::lds_barrier();
+  if (pair == 1) return;
+  const float m1 = xf[64 * cm::kWave], l1 = xf[65 * cm::kWave];
+  const float mt = fmaxf(m, m1);
+  const float a0 = exp2_raw(m - mt), a1 = exp2_raw(m1 - mt);  // a1 = 0 when pair 1 had none
+  l = l * a0 + l1 * a1;
+  if (hh == 0) lse2[static_cast<int64_t>(h) * n_pad + p0 + ql] = mt + __log2f(l);
   if (!q_ok) return;
   const float inv = 1.0f / l;
   _Float16* orow = out + (static_cast<int64_t>(rows.start[r] + ql) * H + h) * kD;
@@ -319,15 +367,19 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
       typedef _Float16 h4 __attribute__((ext_vector_type(4)));
       h4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(o[dt][g4 * 4 + i] * inv);
+      for (int i = 0; i < 4; ++i) {
+        const int e = g4 * 4 + i;
+        v[i] = static_cast<_Float16>((o[dt][e] * a0 + xf[(dt * 16 + e) * cm::kWave] * a1) * inv);
+      }
       *reinterpret_cast<h4*>(orow + dt * 32 + g4 * 8 + hh * 4) = v;
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, dK and dV. Block (b, h): 64 keys of one row (wavefront w owns keys 32w..32w+31)
-// against query head h; loop over the row's 32-query tiles from the block's first key on.
-// Writes the head's partial dK (times the softmax scale) and dV, fp32 [H][n_pad][D].
+// Backward, dK and dV. Block (b, h): 64 keys of one row against query head h; pair p takes the
+// row's 32-query tiles qt_first + p, qt_first + p + 2, ... from the block's first key on. Writes
+// the head's partial dK (times the softmax scale) and dV, fp32 [H][n_pad][D]. Queries past the
+// row end need no mask: their q and dO rows are zero, so they add exactly zero.
 constexpr int kQTile = 32 * (kD / 8);   // Q / dO tile: 32 queries x 16 chunks
 constexpr int kQTTile = kD * (32 / 8);  // Q^T / dO^T tile: 128 d x 4 chunks
 
@@ -338,7 +390,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
     const float* __restrict__ lse2, const float* __restrict__ delta, Rows rows, int n_pad,
     int hpg, float c_log2, float scale, float* __restrict__ dk_part,
     float* __restrict__ dv_part) {
-  __shared__ uint4 lds[2][2 * kQTile + 2 * kQTTile];
+  constexpr int kVec = 2 * kQTile + 2 * kQTTile;  // lse (8 chunks) and Delta (8) follow the tiles
+  constexpr int kStage = kVec + 16;
+  __shared__ uint4 lds[2][2][kStage];
   const int h = blockIdx.y, g = h / hpg;
   const int b = blockIdx.x;
   const int r = row_of_block(rows, b);
@@ -347,24 +401,29 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
   const int p0 = rows.pstart[r];
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int pair = wave >> 1, wq = wave & 1;
   const int hh = lane / 32, ln = lane % 32;
-  const int key = kb * kBlk + wave * 32 + ln;  // this lane's key (row position)
+  const int key0 = kb * kBlk + wq * 32;  // first key of the wavefront
+  const int key = key0 + ln;
 
   const int64_t hq = static_cast<int64_t>(h) * n_pad;
   auto issue = [&](int qt, int st) {
     const int64_t pos = p0 + qt * 32;
-    uint4* t = lds[st];
-    load_tile<32, kD / 8>(t, q16 + (hq + pos) * kD, kD * 2, wave, lane);
-    load_tile<32, kD / 8>(t + kQTile, do16 + (hq + pos) * kD, kD * 2, wave, lane);
+    uint4* t = lds[pair][st];
+    load_tile<32, kD / 8>(t, q16 + (hq + pos) * kD, kD * 2, wq, lane);
+    load_tile<32, kD / 8>(t + kQTile, do16 + (hq + pos) * kD, kD * 2, wq, lane);
     load_tile<kD, 32 / 8>(t + 2 * kQTile, qt16 + static_cast<int64_t>(h) * kD * n_pad + pos,
-                          n_pad * 2, wave, lane);
+                          n_pad * 2, wq, lane);
     load_tile<kD, 32 / 8>(t + 2 * kQTile + kQTTile,
-                          dot16 + static_cast<int64_t>(h) * kD * n_pad + pos, n_pad * 2, wave,
+                          dot16 + static_cast<int64_t>(h) * kD * n_pad + pos, n_pad * 2, wq,
                           lane);
+    load_vec128(t + kVec, lse2 + hq + pos, wq, lane);
+    load_vec128(t + kVec + 8, delta + hq + pos, wq, lane);
   };
   const int qt_first = 2 * kb;
   const int qt_end = (len + 31) / 32;
-  issue(qt_first, 0);
+  const int n_it = (qt_end - qt_first + 1) / 2;
+  if (qt_first + pair < qt_end) issue(qt_first + pair, 0);
 
   half8 kf[kD / 16], vf[kD / 16];
   {
@@ -382,40 +441,39 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
     dv[i] = zero16();
   }
 
-  for (int qt = qt_first; qt < qt_end; ++qt) {
-    const int st = (qt - qt_first) & 1;
-    // this lane's 16 queries: positions qt*32 + (e/4)*8 + hh*4 + e%4
-    float ls[16], dl[16];
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int64_t at = hq + p0 + qt * 32 + g4 * 8 + hh * 4;
-      const float4 a = *reinterpret_cast<const float4*>(lse2 + at);
-      const float4 d = *reinterpret_cast<const float4*>(delta + at);
-      ls[g4 * 4 + 0] = a.x; ls[g4 * 4 + 1] = a.y; ls[g4 * 4 + 2] = a.z; ls[g4 * 4 + 3] = a.w;
-      dl[g4 * 4 + 0] = d.x; dl[g4 * 4 + 1] = d.y; dl[g4 * 4 + 2] = d.z; dl[g4 * 4 + 3] = d.w;
-    }
+  for (int it = 0; it < n_it; ++it) {
+    const int qt = qt_first + 2 * it + pair, st = it & 1;
     cm::gemm::wait_vmcnt<0>();
     cm::gemm::lds_barrier();
-    if (qt + 1 < qt_end) issue(qt + 1, st ^ 1);
-    // wavefront 1's keys start 32 positions later: its first tile is wholly above the diagonal
-    if (qt * 32 + 31 < kb * kBlk + wave * 32) continue;
-    const uint4* qs = lds[st];
+    if (qt + 2 < qt_end) issue(qt + 2, st ^ 1);
+    if (qt >= qt_end) continue;           // pair 1's last iteration
+    if (qt * 32 + 31 < key0) continue;    // the tile's queries all precede this wavefront's keys
+    const uint4* qs = lds[pair][st];
     const uint4* dos = qs + kQTile;
     const uint4* qts = qs + 2 * kQTile;
     const uint4* dots = qts + kQTTile;
+    // lse and Delta of the lane's 16 queries qt*32 + (e/4)*8 + hh*4 + e%4
+    const float4* lv = reinterpret_cast<const float4*>(qs + kVec);
+    const float4* dlv = reinterpret_cast<const float4*>(qs + kVec + 8);
     floatx16 s = zero16(), dp = zero16();
 #pragma unroll
     for (int ds = 0; ds < kD / 16; ++ds) {
       s = mfma(frag<kD / 8>(qs, ln, ds * 2 + hh), kf[ds], s);
       dp = mfma(frag<kD / 8>(dos, ln, ds * 2 + hh), vf[ds], dp);
     }
+    const bool diag = qt * 32 < key0 + 31;  // some query of the tile precedes some key
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int qpos = qt * 32 + (e / 4) * 8 + hh * 4 + e % 4;
-      const bool ok = key <= qpos && qpos < len;
-      const float p = ok ? exp2f(s[e] * c_log2 - ls[e]) : 0.0f;
-      s[e] = p;
-      dp[e] = ok ? p * (dp[e] - dl[e]) : 0.0f;
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const float4 lq = lv[g4 * 2 + hh], dq4 = dlv[g4 * 2 + hh];
+      const float lsv[4] = {lq.x, lq.y, lq.z, lq.w}, dlq[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = g4 * 4 + i;
+        float p = exp2_raw(__builtin_fmaf(s[e], c_log2, -lsv[i]));
+        if (diag) p = key <= qt * 32 + g4 * 8 + hh * 4 + i ? p : 0.0f;
+        s[e] = p;
+        dp[e] = p * (dp[e] - dlq[i]);
+      }
     }
     half8 pf[2], sf[2];
 #pragma unroll
@@ -432,24 +490,41 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
       }
   }
 
+  cm::gemm::lds_barrier();
+  float* xf = reinterpret_cast<float*>(lds[1][0]) + wq * 128 * cm::kWave + lane;
+  if (pair == 1) {
+#pragma unroll
+    for (int i = 0; i < kD / 2; ++i) {
+      xf[i * cm::kWave] = dk[i / 16][i % 16];
+      xf[(64 + i) * cm::kWave] = dv[i / 16][i % 16];
+    }
+  }
+  cm::gemm::lds_barrier();
+  if (pair == 1) return;
   float* dkr = dk_part + (hq + p0 + key) * kD;
   float* dvr = dv_part + (hq + p0 + key) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = dt * 32 + g4 * 8 + hh * 4;
-      *reinterpret_cast<float4*>(dkr + d) =
-          make_float4(dk[dt][g4 * 4] * scale, dk[dt][g4 * 4 + 1] * scale,
-                      dk[dt][g4 * 4 + 2] * scale, dk[dt][g4 * 4 + 3] * scale);
-      *reinterpret_cast<float4*>(dvr + d) = make_float4(dv[dt][g4 * 4], dv[dt][g4 * 4 + 1],
-                                                        dv[dt][g4 * 4 + 2], dv[dt][g4 * 4 + 3]);
+      const int d = dt * 32 + g4 * 8 + hh * 4, e = dt * 16 + g4 * 4;
+      float4 a, c;
+      a.x = (dk[dt][g4 * 4] + xf[e * cm::kWave]) * scale;
+      a.y = (dk[dt][g4 * 4 + 1] + xf[(e + 1) * cm::kWave]) * scale;
+      a.z = (dk[dt][g4 * 4 + 2] + xf[(e + 2) * cm::kWave]) * scale;
+      a.w = (dk[dt][g4 * 4 + 3] + xf[(e + 3) * cm::kWave]) * scale;
+      c.x = dv[dt][g4 * 4] + xf[(64 + e) * cm::kWave];
+      c.y = dv[dt][g4 * 4 + 1] + xf[(65 + e) * cm::kWave];
+      c.z = dv[dt][g4 * 4 + 2] + xf[(66 + e) * cm::kWave];
+      c.w = dv[dt][g4 * 4 + 3] + xf[(67 + e) * cm::kWave];
+      *reinterpret_cast<float4*>(dkr + d) = a;
+      *reinterpret_cast<float4*>(dvr + d) = c;
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, dQ. Block (b, h): 64 queries of one row, head h; loop over 32-key tiles up to the
-// diagonal.
+// Backward, dQ. Block (b, h): 64 queries of one row, head h; pair p takes the 32-key tiles p,
+// p + 2, ... up to the diagonal.
 constexpr int kKVTile = 32 * (kD / 8);  // K / V tile: 32 keys x 16 chunks
 constexpr int kKTTile = kD * (32 / 8);  // K^T tile: 128 d x 4 chunks
 
@@ -460,9 +535,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
     const float* __restrict__ delta, Rows rows, int n_pad, int hpg, float c_log2, float scale,
     OT* __restrict__ dq) {
-  __shared__ uint4 lds[2][2 * kKVTile + kKTTile];
+  constexpr int kStage = 2 * kKVTile + kKTTile;
+  __shared__ uint4 lds[2][2][kStage];
   const int h = blockIdx.y, g = h / hpg;
-  const int H = gridDim.y;
   const int b = blockIdx.x;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
@@ -470,20 +545,22 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   const int p0 = rows.pstart[r];
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+  const int pair = wave >> 1, wq = wave & 1;
   const int hh = lane / 32, ln = lane % 32;
-  const int ql = qb * kBlk + wave * 32 + ln;
+  const int q0 = qb * kBlk + wq * 32;  // first query of the wavefront
+  const int ql = q0 + ln;
 
   const int64_t gk = static_cast<int64_t>(g) * n_pad;
   auto issue = [&](int kt, int st) {
     const int64_t pos = p0 + kt * 32;
-    uint4* t = lds[st];
-    load_tile<32, kD / 8>(t, k16 + (gk + pos) * kD, kD * 2, wave, lane);
-    load_tile<32, kD / 8>(t + kKVTile, v16 + (gk + pos) * kD, kD * 2, wave, lane);
+    uint4* t = lds[pair][st];
+    load_tile<32, kD / 8>(t, k16 + (gk + pos) * kD, kD * 2, wq, lane);
+    load_tile<32, kD / 8>(t + kKVTile, v16 + (gk + pos) * kD, kD * 2, wq, lane);
     load_tile<kD, 32 / 8>(t + 2 * kKVTile, kt16 + static_cast<int64_t>(g) * kD * n_pad + pos,
-                          n_pad * 2, wave, lane);
+                          n_pad * 2, wq, lane);
   };
-  const int kt_end = 2 * qb + 2;
-  issue(0, 0);
+  const int n_it = qb + 1;  // 32-key tiles 0 .. 2 qb + 1, every other one per pair
+  issue(pair, 0);
 
   const int64_t at = static_cast<int64_t>(h) * n_pad + p0 + ql;
   half8 qf[kD / 16], of[kD / 16];
@@ -497,14 +574,13 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
 #pragma unroll
   for (int i = 0; i < kD / 32; ++i) acc[i] = zero16();
 
-  for (int kt = 0; kt < kt_end; ++kt) {
-    const int st = kt & 1;
+  for (int it = 0; it < n_it; ++it) {
+    const int kt = 2 * it + pair, st = it & 1;
     cm::gemm::wait_vmcnt<0>();
     cm::gemm::lds_barrier();
-    if (kt + 1 < kt_end) issue(kt + 1, st ^ 1);
-    // wavefront 0's queries end 32 positions earlier: its last tile is wholly above the diagonal
-    if (kt * 32 > qb * kBlk + wave * 32 + 31) continue;
-    const uint4* ks = lds[st];
+    if (kt + 2 < 2 * n_it) issue(kt + 2, st ^ 1);
+    if (kt * 32 > q0 + 31) continue;  // the tile's keys all follow this wavefront's queries
+    const uint4* ks = lds[pair][st];
     const uint4* vs = ks + kKVTile;
     const uint4* kts = ks + 2 * kKVTile;
     floatx16 s = zero16(), dp = zero16();
@@ -513,12 +589,12 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
       s = mfma(frag<kD / 8>(ks, ln, ds * 2 + hh), qf[ds], s);
       dp = mfma(frag<kD / 8>(vs, ln, ds * 2 + hh), of[ds], dp);
     }
+    const bool diag = kt * 32 + 31 > q0;  // some key of the tile follows some query
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int kpos = kt * 32 + (e / 4) * 8 + hh * 4 + e % 4;
-      const bool ok = kpos <= ql;
-      const float p = ok ? exp2f(s[e] * c_log2 - ls) : 0.0f;
-      dp[e] = ok ? p * (dp[e] - dl) : 0.0f;
+      float p = exp2_raw(__builtin_fmaf(s[e], c_log2, -ls));
+      if (diag) p = kt * 32 + (e / 4) * 8 + hh * 4 + e % 4 <= ql ? p : 0.0f;
+      dp[e] = p * (dp[e] - dl);
     }
     half8 sf[2];
 #pragma unroll
@@ -530,45 +606,49 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
         acc[dt] = mfma(frag<32 / 8>(kts, dt * 32 + ln, j * 2 + hh), sf[j], acc[dt]);
   }
 
-  if (ql >= len) return;
+  cm::gemm::lds_barrier();
+  float* xf = reinterpret_cast<float*>(lds[1][0]) + wq * 64 * cm::kWave + lane;
+  if (pair == 1) {
+#pragma unroll
+    for (int i = 0; i < kD / 2; ++i) xf[i * cm::kWave] = acc[i / 16][i % 16];
+  }
+  cm::gemm::lds_barrier();
+  if (pair == 1 || ql >= len) return;
   OT* row = dq + (static_cast<int64_t>(h) * rows.start[rows.n] + rows.start[r] + ql) * kD;
-  (void)H;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      row[dt * 32 + (e / 4) * 8 + hh * 4 + e % 4] = cm::from_f32<OT>(acc[dt][e] * scale);
+      row[dt * 32 + (e / 4) * 8 + hh * 4 + e % 4] =
+          cm::from_f32<OT>((acc[dt][e] + xf[(dt * 16 + e) * cm::kWave]) * scale);
 }
 
 // dK, dV = sum of the partials of the query heads of each group, [G][N][D] in the output dtype.
-// Block (b, g): the 64 padded positions of block b, key/value head g.
+// Thread (position, 4 values of d) of key/value head blockIdx.y.
 template <typename OT>
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
     const float* __restrict__ dk_part, const float* __restrict__ dv_part, Rows rows, int n_pad,
     int hpg, OT* __restrict__ dk, OT* __restrict__ dv) {
-  const int b = blockIdx.x, g = blockIdx.y;
-  const int r = row_of_block(rows, b);
-  const int len = rows.start[r + 1] - rows.start[r];
-  const int local0 = (b - rows.pstart[r] / kBlk) * kBlk;
-  const int n_tok = rows.start[rows.n];
-  for (int i = threadIdx.x; i < kBlk * (kD / 4); i += 256) {
-    const int t = i / (kD / 4), d = (i % (kD / 4)) * 4;
-    if (local0 + t >= len) continue;
-    const int64_t pos = static_cast<int64_t>(b) * kBlk + t;
-    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
-    for (int j = 0; j < hpg; ++j) {
-      const int64_t at = ((static_cast<int64_t>(g) * hpg + j) * n_pad + pos) * kD + d;
-      const float4 a = *reinterpret_cast<const float4*>(dk_part + at);
-      const float4 c = *reinterpret_cast<const float4*>(dv_part + at);
-      sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
-      sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
-    }
-    const int64_t o = (static_cast<int64_t>(g) * n_tok + rows.start[r] + local0 + t) * kD + d;
-    dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
-    dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
-    dv[o] = cm::from_f32<OT>(sv.x); dv[o + 1] = cm::from_f32<OT>(sv.y);
-    dv[o + 2] = cm::from_f32<OT>(sv.z); dv[o + 3] = cm::from_f32<OT>(sv.w);
+  const int g = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int pos = i / (kD / 4), d = (i % (kD / 4)) * 4;
+  if (pos >= n_pad) return;
+  const int r = row_of_block(rows, pos / kBlk);
+  const int local = pos - rows.pstart[r];
+  if (local >= rows.start[r + 1] - rows.start[r]) return;
+  float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+  for (int j = 0; j < hpg; ++j) {
+    const int64_t at = ((static_cast<int64_t>(g) * hpg + j) * n_pad + pos) * kD + d;
+    const float4 a = *reinterpret_cast<const float4*>(dk_part + at);
+    const float4 c = *reinterpret_cast<const float4*>(dv_part + at);
+    sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
+    sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
   }
+  const int64_t o = (static_cast<int64_t>(g) * rows.start[rows.n] + rows.start[r] + local) * kD + d;
+  dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
+  dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
+  dv[o] = cm::from_f32<OT>(sv.x); dv[o + 1] = cm::from_f32<OT>(sv.y);
+  dv[o + 2] = cm::from_f32<OT>(sv.z); dv[o + 3] = cm::from_f32<OT>(sv.w);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -740,11 +820,11 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   }
   if (int st = cm::launch_status()) return st;
   if (dkv_dtype == CM_F32) {
-    hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(n_blocks, G), dim3(256), 0, s,
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(np / 8, G), dim3(256), 0, s,
                        dk_part, dv_part, rows, np, H / G, static_cast<float*>(dk),
                        static_cast<float*>(dv));
   } else {
-    hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(n_blocks, G), dim3(256), 0, s,
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(np / 8, G), dim3(256), 0, s,
                        dk_part, dv_part, rows, np, H / G, static_cast<_Float16*>(dk),
                        static_cast<_Float16*>(dv));
   }
