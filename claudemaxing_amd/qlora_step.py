@@ -13,7 +13,8 @@ This module builds the same step without the network and without bitsandbytes/pe
   linear of the decoder stored as NF4 (`NF4Linear`, blocksize 64 with double-quantized absmax;
   o_proj and down_proj hand their output to the fp32 residual stream in fp32),
   LoRA (`LoRALinear`, fp32 parameters, dropout 0.05) on q_proj and v_proj, everything else
-  frozen, tied fp32 embedding, and the kernel set's patches applied (`apply()`);
+  frozen, tied fp32 embedding (fp16 values, as a checkpoint loaded in fp16 and upcast; the fused
+  head then stores it in fp16), and the kernel set's patches applied (`apply()`);
 * `make_batch`: 4 rows with token lengths uniform in [64, 512], right-padded, labels = ids with
   -100 at the pads;
 * `train_step`: the fused-head request TRL's compute_loss makes, the forward under fp16 autocast,
@@ -30,6 +31,7 @@ import torch
 
 from . import apply
 from .attention import packed_rows
+from .embedding import shrink_tied_embedding
 from .lm_head_loss import _REQUEST_ATTR, _pack_batch, _packed_forward
 from .lora import LoRALinear
 from .nf4_linear import NF4Linear
@@ -67,6 +69,11 @@ def build_model(device, seed=0, r=16, alpha=32, dropout=0.05, patch=True, **over
     with torch.device(device):
         model = Qwen2ForCausalLM(cfg)
     model.requires_grad_(False)
+    # as a checkpoint loaded in fp16 and upcast for k-bit training: fp32 values that are fp16
+    # numbers (the tied embedding is then stored back in fp16 by the fused head, losslessly)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(p.to(torch.float16))
     for layer in model.model.layers:
         for block_name, names in NF4_TARGETS:
             block = getattr(layer, block_name)
@@ -142,6 +149,8 @@ class GraphedStep:
     def __init__(self, model, opt, scaler, batch, warmup=3):
         self.model, self.opt, self.scaler = model, opt, scaler
         self.params = lora_parameters(model)
+        with torch.autocast("cuda", dtype=torch.float16):
+            shrink_tied_embedding(model)  # as the fused head's forward does
         kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
                       use_cache=False)
         self.packed = _pack_batch(model, kwargs, batch["labels"])

@@ -62,9 +62,15 @@ def test_fused_step_matches_stock(dev):
         nf4 = [m for m in model.modules() if isinstance(m, NF4Linear)]
         for m in nf4:
             m.compute_dtype = torch.float32
+        # the fused step stored the tied weight in fp16 (lossless); fp32 products need fp32
+        emb = model.get_input_embeddings()
+        assert emb.weight.dtype == torch.float16
+        w16 = emb.weight.data
+        emb.weight.data = w16.float()
         try:
             loss_r, grads_r = _loss_and_grads(model, batch, False, autocast=False)
         finally:
+            emb.weight.data = w16
             for m in nf4:
                 m.compute_dtype = torch.float16
     report = [f"loss: fp32 {loss_r:.6f}, stock fp16 {loss_s:.6f}, fused fp16 {loss_f:.6f}"]

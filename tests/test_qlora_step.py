@@ -97,3 +97,25 @@ def test_unpatched_restores_and_reapplies():
     assert (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
             mq.apply_rotary_pos_emb, lora._branch_applies) == patched
     assert AttentionInterface._global_mapping["sdpa"] is sdpa
+
+
+def test_shrink_needs_cuda_autocast():
+    """Without CUDA fp16 autocast nothing is decided and the weight is left alone."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from claudemaxing_amd.embedding import shrink_tied_embedding
+
+    cfg = Qwen2Config(vocab_size=100, hidden_size=32, intermediate_size=64, num_hidden_layers=1,
+                      num_attention_heads=2, num_key_value_heads=1, tie_word_embeddings=True)
+    model = Qwen2ForCausalLM(cfg)
+    assert shrink_tied_embedding(model) is False
+    assert model.get_input_embeddings().weight.dtype == torch.float32
+    assert not hasattr(model, "_fp16_tied_embedding")
+
+
+def test_build_model_weights_are_fp16_values():
+    model = qlora_step.build_model("cpu", seed=0, patch=False, num_hidden_layers=1,
+                                   vocab_size=512, hidden_size=128, intermediate_size=256,
+                                   num_attention_heads=2, num_key_value_heads=1)
+    w = model.get_input_embeddings().weight
+    assert w.dtype == torch.float32 and torch.equal(w.half().float(), w)
