@@ -206,6 +206,16 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
 #pragma unroll
     for (int j = 0; j < TN; ++j) bf[buf][j] = L::frag(Bs, brow + j * 32, ch);
   };
+  // Scheduling of a group "fragment reads of the next substep + first half of the MFMAs":
+  // one LDS read, one MFMA, alternately (measured 1.5% faster on the LM head than all reads
+  // first).
+  auto interleave_reads = [] {
+#pragma unroll
+    for (int i = 0; i < (TM + TN > kHalf ? TM + TN : kHalf); ++i) {
+      if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (i < kHalf) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    }
+  };
   auto mfma = [&](int b, int g0, int g1) {
 #pragma unroll
     for (int g = g0; g < g1; ++g) {
@@ -245,8 +255,10 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
     const bool load = kl < n_kt;
     const bool ia = load && inside_a(kl), ib = load && inside_b(kl);
     read(kt, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt > 0) mfma(1, 0, kHalf);
+    if (kt > 0) {
+      mfma(1, 0, kHalf);
+      interleave_reads();
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (load) {
 #pragma unroll
@@ -260,8 +272,8 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
     for (int ks = 0; ks + 1 < KS; ++ks) {
       const int b = ks & 1;
       read(kt, ks + 1, b ^ 1);
-      __builtin_amdgcn_sched_barrier(0);
       mfma(b, 0, kHalf);
+      interleave_reads();
       __builtin_amdgcn_sched_barrier(0);
       if (load) {
 #pragma unroll
