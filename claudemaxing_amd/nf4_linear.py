@@ -12,7 +12,7 @@ input's dtype, as Linear4bit does).
 
 import torch
 
-from .nf4 import dequantize_nf4, quantize_nf4
+from .nf4 import QuantState, dequantize_nf4, quantize_nf4
 from .rmsnorm import fp16_copy_of
 
 
@@ -77,6 +77,57 @@ class NF4Linear(torch.nn.Module):
         if self.quant_state.absmax.device != dev:
             self.quant_state = self.quant_state.to(dev)
         return self
+
+    # State dict in bitsandbytes Linear4bit's form: "weight" = the packed bytes [numel/2, 1]
+    # uint8, "weight.<field>" = the serialized QuantState (QuantState.as_dict(packed=True)),
+    # "bias" when there is one.
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        destination[prefix + "weight"] = self.packed.reshape(-1, 1)
+        for k, v in self.quant_state.as_dict(packed=True).items():
+            destination[prefix + "weight." + k] = v
+        if self.bias is not None:
+            destination[prefix + "bias"] = self.bias
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        key = prefix + "weight"
+        if key not in state_dict:
+            missing_keys.append(key)
+            return
+        dev = self.packed.device
+        fields = {k[len(key) + 1:]: v for k, v in state_dict.items() if k.startswith(key + ".")}
+        state = QuantState.from_dict(fields, dev)
+        if tuple(state.shape) != (self.out_features, self.in_features):
+            error_msgs.append(f"{key}: shape {tuple(state.shape)} against "
+                              f"{(self.out_features, self.in_features)}")
+            return
+        self.packed = state_dict[key].to(dev, torch.uint8).reshape(-1, 1).contiguous()
+        self.quant_state = state
+        if prefix + "bias" in state_dict:
+            self.bias = state_dict[prefix + "bias"].detach().to(dev).clone()
+            self._bias_c = None
+        elif self.bias is not None:
+            missing_keys.append(prefix + "bias")
+        for k in state_dict:
+            if k.startswith(prefix) and k != key and not k.startswith(key + ".") \
+                    and k != prefix + "bias" and "." not in k[len(prefix):]:
+                unexpected_keys.append(k)
+
+    @classmethod
+    def from_state_dict(cls, state_dict, prefix="", compute_dtype=torch.float16, out_dtype=None,
+                        device=None):
+        """An NF4Linear from a bitsandbytes Linear4bit state dict (keys "<prefix>weight",
+        "<prefix>weight.<quant_state fields>", optionally "<prefix>bias")."""
+        key = prefix + "weight"
+        fields = {k[len(key) + 1:]: v for k, v in state_dict.items() if k.startswith(key + ".")}
+        state = QuantState.from_dict(fields, device)
+        packed = state_dict[key].to(torch.uint8).reshape(-1, 1).contiguous()
+        if device is not None:
+            packed = packed.to(device)
+        bias = state_dict.get(prefix + "bias")
+        if bias is not None and device is not None:
+            bias = bias.to(device)
+        return cls(packed, state, compute_dtype, bias, out_dtype)
 
     def _bias_in(self, dtype):
         """The frozen bias in `dtype`, converted once per bias version."""
