@@ -24,6 +24,7 @@ host cores (a baseline, not the target), plus every kernel's numbers under "kern
 """
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -497,6 +498,11 @@ def main():
               f"({100 * achieved / peak:.1f}% of peak)", file=sys.stderr, flush=True)
     if not results:
         sys.exit("bench.py: --only must name at least one kernel")
+    # the kernel benches' inputs (rotated copies beyond 512 MiB) must not count in the step's
+    # peak memory
+    del kernels, kern
+    gc.collect()
+    torch.cuda.empty_cache()
     headline = "lmhead_ce" if "lmhead_ce" in results else next(iter(results))
     hr = results[headline]
     line = {

@@ -24,7 +24,7 @@
 //   K4 final    (after the last chunk) lse, loss, entropy, correct; G = scale (sum_s G_s / 1024
 //               - W_t).
 //
-// The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 256 MiB) lives in the
+// The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 1 GiB) lives in the
 // workspace. The chunk and the transposed weight are stored in 64-column panels
 // ([C/64][tokens][64], [V/64][H][64]) so that every K3 operand tile is one contiguous 16 KiB
 // read.
@@ -421,11 +421,12 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 constexpr int64_t kChunkAlign = kBM1 > 256 ? kBM1 : 256;
 
 int64_t default_chunk(int64_t n_rows, int64_t vocab) {
-  // E chunk of at most 256 MiB (fp16, n_rows x C), whatever the vocabulary, split into equal
-  // chunks. Fewer, larger chunks pay the per-chunk costs (launch ramps, the read-modify-write of
-  // the split-K gradient accumulators) fewer times; measured at N = 2048, V = 151936: 16384
-  // columns 2.82 ms, 50688 (3 chunks) 2.57 ms, one chunk 2.47 ms (a 622 MB E buffer).
-  const int64_t budget = (int64_t{128} << 20) / (n_rows > 0 ? n_rows : 1);  // columns
+  // E chunk of at most 1 GiB (fp16, n_rows x C), whatever the vocabulary, split into equal
+  // chunks. Fewer, larger chunks pay the per-chunk costs (launch ramps, each launch's partly
+  // filled last wave of workgroups, the read-modify-write of the split-K gradient accumulators)
+  // fewer times; measured at N = 2048, V = 151936: 38016 columns (4 chunks) 2.51 ms, 50688
+  // (3) 2.51 ms, 75968 (2) 2.40 ms, one chunk 2.31 ms (a 622 MB E buffer, 0.2% of the HBM).
+  const int64_t budget = (int64_t{512} << 20) / (n_rows > 0 ? n_rows : 1);  // columns
   int64_t c = budget / kChunkAlign * kChunkAlign;
   if (c < 4096) c = 4096;
   if (c >= vocab) return round_up(vocab, kChunkAlign);
