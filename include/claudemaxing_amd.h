@@ -229,6 +229,46 @@ int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows);
  * are unsupported. */
 int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim, int backward);
 
+/* ------------------------------------------------------------------------------------------ */
+/* A rank-16 LoRA adapter on a frozen base projection, fused per token row: forward. Replaces,
+ * for one adapter of the training step, LoRABranch.forward (solution/lora.py:78-94: the pack
+ * kernel 30-42, the fp16 casts of the adapter weights, lora_B(lora_A(xd)) as two GEMMs, the
+ * scaling) and the widening add onto the base output done by its caller (the patched peft
+ * forward, lora.py:136-186). Row t of T, K inputs, N outputs, R = rank = 16:
+ *   xd = fp16(keep ? x * scale_p : 0)    (bits: the mask LSB-first, T*K/8 bytes)
+ *   a16[t][r] = fp16(sum_k xd[k] * fp16(weight_a[r][k]))
+ *   out[t][n] = fp32(base16[t][n]) + fp32(fp16(fp16(sum_r a16[t][r] * fp16(weight_b[n][r]))
+ *                                          * scaling))
+ * x fp32 [T, K], keep bool/uint8 [T, K] (8-byte aligned), weight_a fp32 [R, K], weight_b fp32
+ * [N, R], base16 fp16 [T, N] (the base projection's output), out fp32 [T, N], a16 fp16 [T, R].
+ * K a multiple of 8 and <= 2048, N <= 2048. The sums are in fp32 (order differs from a GEMM).
+ */
+int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a,
+                      const float* weight_b, const void* base16, float* out, uint8_t* bits,
+                      void* a16, int64_t T, int K, int N, int rank, float scale_p,
+                      float scaling, void* stream);
+
+/* Backward, part 1 (LoRABranch.backward, solution/lora.py:96-107, up to lora_A's output):
+ *   gbase16 = fp16(grad)                    (the gradient of the base projection's output)
+ *   g16 = fp16(gbase16 * scaling)           (the gradient of lora_B's output)
+ *   ga16[t][r] = fp16(sum_n g16[t][n] * fp16(weight_b[n][r]))
+ * grad fp32 [T, N]; outputs fp16 [T, N], [T, N], [T, R].
+ */
+int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16, void* g16,
+                       void* ga16, int64_t T, int N, int rank, float scaling, void* stream);
+
+/* Backward, part 2, after the caller's base input gradient dxb16 = gbase16 @ W (fp16 [T, K]):
+ *   gxd = fp16(sum_r ga16[t][r] * fp16(weight_a[r][k]))
+ *   dx[t][k] = fp32(dxb16[t][k]) + (keep ? gxd * scale_p : 0)     (dx may be NULL: then
+ *                                                                   dxb16 is not read)
+ *   xd16[t][k] = fp16(keep ? x16[t][k] * scale_p : 0)   (lora_A's input rebuilt, the unpack
+ *                                                         kernel solution/lora.py:45-57)
+ * keep = the bits of the forward. All fp16/fp32 arrays 16-byte aligned.
+ */
+int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const float* weight_a,
+                       const void* x16, const uint8_t* bits, float* dx, void* xd16, int64_t T,
+                       int K, int rank, float scale_p, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
