@@ -60,6 +60,15 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_rmsnorm_fwd(None, 1, 4, None, 0, None, 1, None, None, None, None, 1, 2, 8,
                               1e-6, None) == INVALID  # row stride < n_cols
     assert lib.cm_xent_rows(None, 1, 4, None, None, None, None, 1, 8, 0, 1.0, None) == INVALID
+    # fused LoRA adapter: rank must be 16, K a multiple of 8 and <= 2048, N <= 2048
+    assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1536, 1536,
+                                 8, 1.05, 2.0, None) == INVALID
+    assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1532, 1536,
+                                 16, 1.05, 2.0, None) == INVALID
+    assert lib.cm_lora_fused_bwd1(None, None, None, None, None, 4, 4096, 16, 2.0,
+                                  None) == INVALID
+    assert lib.cm_lora_fused_bwd2(None, None, None, None, None, None, None, 4, 4096, 16, 1.05,
+                                  None) == INVALID
 
 
 def test_empty_inputs_are_no_ops(lib):
@@ -69,6 +78,10 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, 0, 1, None) == 0
     assert lib.cm_rmsnorm_bwd_partials(0) == 0
     assert lib.cm_rmsnorm_bwd_partials(10) == 12
+    assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 0, 1536, 256,
+                                 16, 1.05, 2.0, None) == 0
+    assert lib.cm_lora_fused_bwd2(None, None, None, None, None, None, None, 0, 1536, 16, 1.05,
+                                  None) == 0
 
 
 def test_call_raises_with_the_library_message():
