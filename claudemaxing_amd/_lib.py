@@ -28,6 +28,29 @@ _DTYPE_CODES = {
 
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
+
+class NF4Weight(ctypes.Structure):
+    """cm_nf4_weight: one NF4 weight's device pointers and sizes."""
+
+    _fields_ = [
+        ("packed", ctypes.c_void_p),
+        ("absmax", ctypes.c_void_p),
+        ("nested", ctypes.c_int),
+        ("code", ctypes.c_void_p),
+        ("code2", ctypes.c_void_p),
+        ("absmax2", ctypes.c_void_p),
+        ("offset", ctypes.c_void_p),
+        ("blocksize", ctypes.c_int),
+        ("blocksize2", ctypes.c_int),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+    ]
+
+
+_PW = ctypes.POINTER(NF4Weight)
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_PL = ctypes.POINTER(ctypes.c_int64)
+
 # name -> (restype, argtypes); mirrors include/claudemaxing_amd.h
 SIGNATURES = {
     "cm_abi_version": (_I, []),
@@ -54,6 +77,8 @@ SIGNATURES = {
     "cm_lora_fused_bwd1": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
     "cm_lora_fused_bwd2": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
     "cm_attn_workspace_bytes": (_L, [_L, _I, _I, _I, _I]),
+    "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P]),
+    "cm_nf4_linear_bwd": (_I, [_PP, _PL, _L, _PW, _I, _P, _L, _I, _P]),
 }
 
 _lock = threading.Lock()

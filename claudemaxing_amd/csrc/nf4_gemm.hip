@@ -1,0 +1,587 @@
+// NF4 weights expanded inside an fp16 GEMM on the gfx950 matrix cores: the dequantization
+// (nested absmax included) happens on the way into the LDS, so the fp16 weight never exists
+// in HBM.
+//
+// Replaces, for the frozen 4-bit layers of the training step, the pair "dequantize_nf4 (the
+// reference's nf4_dequant_kernel, solution/nf4.py:26-46) -> fp16 GEMM" that the reference's
+// patched bitsandbytes matmul runs per linear (solution/nf4.py:102-130, and the recompute in
+// solution/swiglu_recompute.py:165-166, 198-199):
+//
+//   forward   Y_i = X W_i^T (+ b_i)       X fp16 [M, K], W_i NF4 [N_i, K], up to 3 weights that
+//                                         share X in one launch (gate + up)
+//   backward  dX = sum_i G_i W_i          G_i fp16 [M, N_i], the weights' rows concatenated
+//                                         along the contraction (dgate Wg + dup Wu)
+//
+// Each weight element is expanded exactly as the standalone dequant kernel expands it: scale
+// s = code2[absmax8[b]] * absmax2[b / blocksize2] + offset (multiply, then add), value =
+// fp16(code[nibble] * s). So a fused product equals the dequant kernel's fp16 weight fed to a
+// GEMM, up to the order of the fp32 sums. Outputs are rounded once to fp16 (after the bias, as
+// a GEMM with a bias epilogue does) and optionally widened to fp32, which is what "fp16 linear,
+// then .to(float32)" gives.
+//
+// Tiling: C = A B^T on v_mfma_f32_32x32x16_f16 with A = the weight side (BM rows: weight rows
+// forward, weight columns backward) and B = the token side (BN tokens). 4 wavefronts in a 2 x 2
+// grid; stages of 64 contraction elements, double-buffered in the LDS, one barrier per stage.
+// Per stage each lane
+//   - issues the direct-to-LDS loads (global_load_lds_dwordx4) of the next token tile,
+//   - multiplies the current stage,
+//   - expands the next weight tile from the packed bytes it loaded one stage earlier into
+//     registers, writing fp16 16-byte (forward) or 8-byte (backward, transposed) LDS chunks,
+//   - loads the packed bytes and block scales of the stage after that.
+// The forward weight tile is a plain row-major tile; the backward one is the transpose (rows =
+// weight columns, contraction = weight rows), assembled from 8 x RPT blocks: each lane loads one
+// 4-byte word (8 columns) from RPT consecutive weight rows and writes 8 LDS pieces of RPT
+// values. The token side is read as it lies (K-contiguous rows).
+#include <type_traits>
+
+#include "common.h"
+#include "gemm_lds.h"
+
+namespace {
+
+// The block scale is a multiply then an add, never fused (the dequant kernel's arithmetic).
+#pragma clang fp contract(off)
+
+using cm::gemm::DmaTile;
+using cm::gemm::floatx16;
+using cm::gemm::half8;
+using cm::gemm::LdsRows;
+using cm::gemm::RowMajor;
+
+constexpr int kThreads = 256;  // 4 wavefronts, 2 x 2
+constexpr int kBK = 64;        // contraction elements per stage
+constexpr int kMaxW = 3;
+
+struct WeightDev {
+  const uint32_t* packed;  // 4-byte words of the packed weight
+  const void* absmax;      // uint8 (nested) or fp32 block scales
+  const float* absmax2;
+  const float* offset;
+  const float* code;       // [16]
+  const float* code2;      // [256] (nested)
+  int rows;                // N_i
+  int bs_shift;            // log2(blocksize)
+  int bs2_shift;           // log2(blocksize2), or -1: divide by bs2
+  uint32_t bs2;
+  int first;               // forward: first A tile; backward: first stage of this weight
+  const _Float16* bias;    // forward, may be null
+  void* out;               // forward output [M, N_i] (fp16 or fp32)
+  int64_t ldo;
+  const _Float16* g;       // backward input [M, N_i]
+  int64_t ldg;
+};
+
+struct Args {
+  WeightDev w[kMaxW];
+  int n_w;
+  int nested;
+  int cols;         // K: elements per weight row
+  int m;            // tokens
+  int tiles_b;      // token tiles
+  int remap;        // XCD-aware tile order (grid a multiple of 8)
+  int out32;        // outputs widened to fp32
+  const _Float16* x;  // forward token operand [M, K]
+  int64_t ldx;
+  void* dx;         // backward output [M, K]
+  int64_t lddx;
+  int n_stages;     // backward: total stages over all weights
+};
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const _Float16 ha = cm::from_f32<_Float16>(a), hb = cm::from_f32<_Float16>(b);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+}
+
+// Block scale of absmax block blk of weight w (the dequant kernel's formula).
+__device__ __forceinline__ float block_scale(int nested, float q8code, float a2, float off,
+                                             float plain) {
+  if (nested) {
+    const float prod = q8code * a2;
+    return prod + off;
+  }
+  return plain;
+}
+
+// Raw scale inputs of one block, loaded a stage ahead: the u8 code index and absmax2 (nested),
+// or the fp32 scale.
+struct ScaleRaw {
+  uint32_t q8;
+  float a2;  // absmax2 (nested) or the fp32 scale
+};
+
+__device__ __forceinline__ ScaleRaw load_scale(const WeightDev& w, int nested, int64_t elem) {
+  const uint32_t blk = static_cast<uint32_t>(elem >> w.bs_shift);
+  ScaleRaw r;
+  if (nested) {
+    r.q8 = static_cast<const uint8_t*>(w.absmax)[blk];
+    const uint32_t b2 = w.bs2_shift >= 0 ? (blk >> w.bs2_shift) : (blk / w.bs2);
+    r.a2 = w.absmax2[b2];
+  } else {
+    r.q8 = 0;
+    r.a2 = static_cast<const float*>(w.absmax)[blk];
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Weight-side tile loaders. A stage's tile is BM rows x 64 contraction elements in the LDS
+// (row-major rows of 8 16-byte chunks, chunk XOR-swizzled by LdsRows<64>::swz(row)).
+
+// Forward: tile rows = weight rows r0 .. r0 + BM, columns kc .. kc + 64. A lane expands EPT =
+// BM / 4 consecutive elements of one row (one block scale: blocksize >= 32 >= EPT).
+template <int BM>
+struct FwdLoader {
+  static constexpr int kEPT = BM / 4;           // elements per lane per stage
+  static constexpr int kWords = kEPT / 8;       // 4-byte packed words per lane
+  static constexpr int kTPR = kBK / kEPT;       // lanes per tile row
+  static_assert(kWords == 2 || kWords == 4, "BM of 64 or 128");
+  uint32_t word[kWords];
+  ScaleRaw sc;
+  int row, part;
+
+  __device__ __forceinline__ void init(int tid) {
+    row = tid / kTPR;
+    part = tid % kTPR;
+  }
+  __device__ __forceinline__ void load(const WeightDev& w, int nested, int cols, int r0, int kc) {
+    const int64_t e0 = static_cast<int64_t>(r0 + row) * cols + kc + part * kEPT;
+    const uint32_t* p = w.packed + (e0 >> 3);
+    if constexpr (kWords == 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      word[0] = v.x; word[1] = v.y; word[2] = v.z; word[3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      word[0] = v.x; word[1] = v.y;
+    }
+    sc = load_scale(w, nested, e0);
+  }
+  __device__ __forceinline__ void store(uint4* tile, const float* s_code, const float* s_code2,
+                                        float off, int nested) const {
+    using L = LdsRows<kBK>;
+    const float s = block_scale(nested, s_code2[nested ? sc.q8 : 0], sc.a2, off, sc.a2);
+#pragma unroll
+    for (int q = 0; q < kWords; ++q) {
+      uint32_t h[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (word[q] >> (8 * b)) & 0xffu;
+        h[b] = pack2(s_code[byte >> 4] * s, s_code[byte & 0xfu] * s);
+      }
+      const int lc = part * kWords + q;
+      tile[row * L::kRC + (lc ^ L::swz(row))] = make_uint4(h[0], h[1], h[2], h[3]);
+    }
+  }
+};
+
+// Backward: tile rows = weight columns k0 .. k0 + BM, contraction = weight rows n0 .. n0 + 64.
+// A lane takes RPT = BM / 32 consecutive weight rows x 8 consecutive columns (one 4-byte word
+// per row, one block scale per row) and writes, for each of its 8 columns, RPT values into one
+// piece of an LDS chunk.
+template <int BM>
+struct BwdLoader {
+  static constexpr int kRPT = BM / 32;     // weight rows per lane
+  static constexpr int kNG = kBK / kRPT;   // lanes along the contraction
+  static_assert(kRPT == 2 || kRPT == 4, "BM of 64 or 128");
+  uint32_t word[kRPT];
+  ScaleRaw sc[kRPT];
+  int kw, ng;
+
+  __device__ __forceinline__ void init(int tid) {
+    ng = tid % kNG;
+    kw = tid / kNG;
+  }
+  __device__ __forceinline__ void load(const WeightDev& w, int nested, int cols, int n0, int k0) {
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) {
+      const int64_t e0 = static_cast<int64_t>(n0 + ng * kRPT + r) * cols + k0 + kw * 8;
+      word[r] = w.packed[e0 >> 3];
+      sc[r] = load_scale(w, nested, e0);
+    }
+  }
+  __device__ __forceinline__ void store(uint4* tile, const float* s_code, const float* s_code2,
+                                        float off, int nested) const {
+    using L = LdsRows<kBK>;
+    float s[kRPT];
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r)
+      s[r] = block_scale(nested, s_code2[nested ? sc[r].q8 : 0], sc[r].a2, off, sc[r].a2);
+    const int ncol = ng * kRPT;  // first contraction column of the lane's piece
+    const int lc = ncol / 8;
+    char* base = reinterpret_cast<char*>(tile);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // element j of each row's word: byte j / 2, high nibble for even j
+      float v[kRPT];
+#pragma unroll
+      for (int r = 0; r < kRPT; ++r) {
+        const uint32_t byte = (word[r] >> (8 * (j / 2))) & 0xffu;
+        const uint32_t nib = (j % 2 == 0) ? (byte >> 4) : (byte & 0xfu);
+        v[r] = s_code[nib] * s[r];
+      }
+      const int kk = kw * 8 + j;
+      char* dst = base + (kk * L::kRC + (lc ^ L::swz(kk))) * 16 + (ncol % 8) * 2;
+      if constexpr (kRPT == 4) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = pack2(v[0], v[1]);
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+template <int BM, int BN, bool TRANS>
+__global__ __launch_bounds__(kThreads, 2) void nf4_gemm_kernel(const Args args) {
+  using L = LdsRows<kBK>;
+  constexpr int kRC = L::kRC;
+  constexpr int kStage = (BM + BN) * kRC;  // uint4 per stage
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  using TB = DmaTile<BN, 4, kBK>;
+  using Loader = typename std::conditional<TRANS, BwdLoader<BM>, FwdLoader<BM>>::type;
+
+  __shared__ uint4 ring[2 * kStage];
+  __shared__ float s_code[kMaxW][16];
+  __shared__ float s_code2[kMaxW][256];
+  __shared__ float s_off[kMaxW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % cm::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / cm::kWave);
+  const int wm = wave / 2, wn = wave % 2;
+  const int nested = args.nested;
+
+  for (int i = 0; i < args.n_w; ++i) {
+    if (tid < 16) s_code[i][tid] = args.w[i].code[tid];
+    if (nested) {
+      s_code2[i][tid] = args.w[i].code2[tid];
+      if (tid == 0) s_off[i] = *args.w[i].offset;
+    } else if (tid == 0) {
+      s_off[i] = 0.0f;
+    }
+  }
+
+  // tile of this workgroup: a (weight side) and b (tokens), consecutive ids share the a tile
+  int bid = blockIdx.x;
+  if (args.remap) {
+    const int per = gridDim.x / 8;
+    bid = (bid % 8) * per + bid / 8;
+  }
+  const int ta = bid / args.tiles_b, tb = bid % args.tiles_b;
+  const int m0 = tb * BN;
+
+  // forward: the weight holding tile ta, its first row; backward: the weight columns
+  int wf = 0;
+  if constexpr (!TRANS) {
+    while (wf + 1 < args.n_w && ta >= args.w[wf + 1].first) ++wf;
+  }
+  const int a0 = TRANS ? ta * BM : (ta - args.w[wf].first) * BM;
+  const int n_kt = TRANS ? args.n_stages : args.cols / kBK;
+
+  // stage kt -> weight index and contraction offset within it
+  auto stage_w = [&](int kt) {
+    if constexpr (!TRANS) {
+      return wf;
+    } else {
+      int i = 0;
+      while (i + 1 < args.n_w && kt >= args.w[i + 1].first) ++i;
+      return i;
+    }
+  };
+  auto stage_k = [&](int kt, int wi) { return TRANS ? (kt - args.w[wi].first) * kBK : kt * kBK; };
+  auto token_src = [&](int wi) {
+    RowMajor s;
+    if constexpr (TRANS) {
+      s.p = args.w[wi].g;
+      s.ld = args.w[wi].ldg;
+      s.k_len = args.w[wi].rows;
+    } else {
+      s.p = args.x;
+      s.ld = args.ldx;
+      s.k_len = args.cols;
+    }
+    s.rows = args.m;
+    return s;
+  };
+
+  Loader ld;
+  ld.init(tid);
+  TB lb;
+  auto load_a = [&](int kt) {
+    const int wi = stage_w(kt), kc = stage_k(kt, wi);
+    if constexpr (TRANS) {
+      ld.load(args.w[wi], nested, args.cols, kc, a0);
+    } else {
+      ld.load(args.w[wi], nested, args.cols, a0, kc);
+    }
+  };
+  auto store_a = [&](int kt, uint4* st) {
+    const int wi = stage_w(kt);
+    ld.store(st, s_code[wi], s_code2[wi], s_off[wi], nested);
+  };
+  auto issue_b = [&](int kt, uint4* st) {
+    const int wi = stage_w(kt), kc = stage_k(kt, wi);
+    const RowMajor src = token_src(wi);
+    lb.init(src, wave, lane);
+    const bool inside = src.tile_inside(m0, BN, kc);
+#pragma unroll
+    for (int q = 0; q < TB::kPer; ++q) lb.issue(src, m0, kc, st + BM * kRC, wave, q, inside);
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // prologue: stage 0 in buffer 0, the packed bytes of stage 1 in registers
+  load_a(0);
+  issue_b(0, ring);
+  __syncthreads();  // the code tables
+  store_a(0, ring);
+  cm::gemm::wait_vmcnt<0>();  // the token tile of stage 0
+  if (n_kt > 1) load_a(1);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  cm::gemm::lds_barrier();
+
+  const int arow = wm * WTM + lane % 32, brow = wn * WTN + lane % 32;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    uint4* cur = ring + (kt & 1) * kStage;
+    uint4* nxt = ring + ((kt + 1) & 1) * kStage;
+    const bool more = kt + 1 < n_kt;
+    if (more) issue_b(kt + 1, nxt);
+    const uint4* As = cur;
+    const uint4* Bs = cur + BM * kRC;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int ch = ks * 2 + lane / 32;
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = L::frag(As, arow + i * 32, ch);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = L::frag(Bs, brow + j * 32, ch);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_a(kt + 1, nxt);
+    // the token tile of stage kt + 1 has landed; the packed bytes of stage kt + 2 are loaded
+    // after this wait and stay in flight through the barrier and the next stage's products
+    cm::gemm::wait_vmcnt<0>();
+    if (kt + 2 < n_kt) load_a(kt + 2);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this lane's LDS writes have landed
+    cm::gemm::lds_barrier();
+  }
+
+  // epilogue: lane holds C[a][t] for tokens t = m0 + wn * WTN + j * 32 + lane % 32 and weight-side
+  // rows a = a0 + wm * WTM + i * 32 + (e / 4) * 8 + (lane / 32) * 4 + e % 4: 4 consecutive
+  // outputs of one token row per (i, j, e / 4)
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int t = m0 + wn * WTN + j * 32 + lane % 32;
+    if (t >= args.m) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int a = a0 + wm * WTM + i * 32 + g * 8 + (lane / 32) * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
+        void* out;
+        int64_t off;
+        if constexpr (TRANS) {
+          out = args.dx;
+          off = static_cast<int64_t>(t) * args.lddx + a;
+        } else {
+          const WeightDev& w = args.w[wf];
+          if (w.bias) {
+            const uint2 bb = *reinterpret_cast<const uint2*>(w.bias + a);
+            const _Float16* bh = reinterpret_cast<const _Float16*>(&bb);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += static_cast<float>(bh[e]);
+          }
+          out = w.out;
+          off = static_cast<int64_t>(t) * w.ldo + a;
+        }
+        if (args.out32) {
+          float4 o;
+          o.x = cm::round_to<_Float16>(v[0]);
+          o.y = cm::round_to<_Float16>(v[1]);
+          o.z = cm::round_to<_Float16>(v[2]);
+          o.w = cm::round_to<_Float16>(v[3]);
+          *reinterpret_cast<float4*>(static_cast<float*>(out) + off) = o;
+        } else {
+          *reinterpret_cast<uint2*>(static_cast<_Float16*>(out) + off) =
+              make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t{1} << s) < v) ++s;
+  return s;
+}
+
+constexpr int kCUs = 256;
+
+template <int BM, int BN, bool TRANS>
+int launch_cfg(const Args& a, int n_tiles, hipStream_t stream) {
+  hipLaunchKernelGGL((nf4_gemm_kernel<BM, BN, TRANS>), dim3(static_cast<uint32_t>(n_tiles)),
+                     dim3(kThreads), 0, stream, a);
+  return cm::launch_status();
+}
+
+// Common checks and device views of the weights; 0 or an error code.
+int setup(const cm_nf4_weight* w, int n_w, int64_t m, Args& a) {
+  CM_CHECK_ARG(w != nullptr && n_w >= 1 && n_w <= kMaxW);
+  CM_CHECK_ARG(m >= 0 && m < (int64_t{1} << 31));
+  const int64_t cols = w[0].cols;
+  CM_CHECK_ARG(cols > 0 && cols % kBK == 0 && cols < (int64_t{1} << 30));
+  a = Args{};
+  a.n_w = n_w;
+  a.nested = w[0].nested ? 1 : 0;
+  a.cols = static_cast<int>(cols);
+  a.m = static_cast<int>(m);
+  for (int i = 0; i < n_w; ++i) {
+    const cm_nf4_weight& s = w[i];
+    CM_CHECK_ARG(s.packed && s.absmax && s.code);
+    CM_CHECK_ARG(s.cols == cols && s.rows > 0 && s.rows % kBK == 0 &&
+                 s.rows < (int64_t{1} << 30));
+    // 32-bit block indices; 4-byte aligned packed rows (cols a multiple of 64)
+    CM_CHECK_ARG(s.rows * cols / 32 < (int64_t{1} << 31));
+    CM_CHECK_ARG(cm::aligned(s.packed, 16));
+    CM_CHECK_ARG((s.nested ? 1 : 0) == a.nested);
+    const int bs_shift = log2_exact(s.blocksize);
+    CM_CHECK_ARG(bs_shift >= 5);  // blocksize >= 32, a power of two
+    if (a.nested) CM_CHECK_ARG(s.code2 && s.absmax2 && s.offset && s.blocksize2 >= 1);
+    WeightDev& d = a.w[i];
+    d.packed = reinterpret_cast<const uint32_t*>(s.packed);
+    d.absmax = s.absmax;
+    d.absmax2 = s.absmax2;
+    d.offset = s.offset;
+    d.code = s.code;
+    d.code2 = s.code2;
+    d.rows = static_cast<int>(s.rows);
+    d.bs_shift = bs_shift;
+    d.bs2_shift = a.nested ? log2_exact(s.blocksize2) : 0;
+    d.bs2 = a.nested ? static_cast<uint32_t>(s.blocksize2) : 1u;
+  }
+  return 0;
+}
+
+// Tile shape per call: the largest tiles that still give every CU a workgroup; the smallest
+// when none does.
+template <class TilesFn>
+int pick_tiles(TilesFn tiles, bool allow128, int& bm, int& bn) {
+  const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+  for (const auto& c : cand) {
+    if (c[0] == 128 && !allow128) continue;
+    if (tiles(c[0], c[1]) >= kCUs) {
+      bm = c[0];
+      bn = c[1];
+      return 0;
+    }
+  }
+  bm = 64;
+  bn = 64;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int cm_nf4_linear_fwd(const void* x, int64_t ldx, int64_t m, const cm_nf4_weight* w,
+                                 int n_w, const void* const* bias, void* const* out,
+                                 const int64_t* ldo, int out_dtype, void* stream) {
+  Args a;
+  if (int st = setup(w, n_w, m, a)) return st;
+  CM_CHECK_ARG(out_dtype == CM_F16 || out_dtype == CM_F32);
+  CM_CHECK_ARG(out != nullptr && ldo != nullptr);
+  if (m == 0) return 0;
+  CM_CHECK_ARG(x && cm::aligned(x, 16) && ldx >= a.cols && ldx % 8 == 0);
+  a.x = static_cast<const _Float16*>(x);
+  a.ldx = ldx;
+  a.out32 = out_dtype == CM_F32;
+  bool all128 = true;
+  for (int i = 0; i < n_w; ++i) {
+    WeightDev& d = a.w[i];
+    CM_CHECK_ARG(out[i] && ldo[i] >= d.rows && ldo[i] % 4 == 0);
+    CM_CHECK_ARG(cm::aligned(out[i], a.out32 ? 16 : 8));
+    d.out = out[i];
+    d.ldo = ldo[i];
+    d.bias = bias ? static_cast<const _Float16*>(bias[i]) : nullptr;
+    if (d.bias) CM_CHECK_ARG(cm::aligned(d.bias, 8));
+    all128 = all128 && d.rows % 128 == 0;
+  }
+  auto tiles = [&](int bm, int bn) {
+    int64_t ta = 0;
+    for (int i = 0; i < n_w; ++i) ta += a.w[i].rows / bm;
+    return ta * ((m + bn - 1) / bn);
+  };
+  int bm, bn;
+  pick_tiles(tiles, all128, bm, bn);
+  int first = 0;
+  for (int i = 0; i < n_w; ++i) {
+    a.w[i].first = first;
+    first += a.w[i].rows / bm;
+  }
+  a.tiles_b = static_cast<int>((m + bn - 1) / bn);
+  const int64_t n_tiles = tiles(bm, bn);
+  CM_CHECK_ARG(n_tiles < 0x7fffffff);
+  a.remap = n_tiles % 8 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nt = static_cast<int>(n_tiles);
+  if (bm == 128 && bn == 128) return launch_cfg<128, 128, false>(a, nt, s);
+  if (bm == 128) return launch_cfg<128, 64, false>(a, nt, s);
+  if (bn == 128) return launch_cfg<64, 128, false>(a, nt, s);
+  return launch_cfg<64, 64, false>(a, nt, s);
+}
+
+extern "C" int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
+                                 const cm_nf4_weight* w, int n_w, void* dx, int64_t lddx,
+                                 int dx_dtype, void* stream) {
+  Args a;
+  if (int st = setup(w, n_w, m, a)) return st;
+  CM_CHECK_ARG(dx_dtype == CM_F16 || dx_dtype == CM_F32);
+  CM_CHECK_ARG(g != nullptr && ldg != nullptr);
+  if (m == 0) return 0;
+  a.out32 = dx_dtype == CM_F32;
+  CM_CHECK_ARG(dx && lddx >= a.cols && lddx % 4 == 0 && cm::aligned(dx, a.out32 ? 16 : 8));
+  a.dx = dx;
+  a.lddx = lddx;
+  int stages = 0;
+  for (int i = 0; i < n_w; ++i) {
+    WeightDev& d = a.w[i];
+    CM_CHECK_ARG(g[i] && cm::aligned(g[i], 16) && ldg[i] >= d.rows && ldg[i] % 8 == 0);
+    d.g = static_cast<const _Float16*>(g[i]);
+    d.ldg = ldg[i];
+    d.first = stages;
+    stages += d.rows / kBK;
+  }
+  a.n_stages = stages;
+  auto tiles = [&](int bm, int bn) {
+    return static_cast<int64_t>(a.cols / bm) * ((m + bn - 1) / bn);
+  };
+  int bm, bn;
+  pick_tiles(tiles, a.cols % 128 == 0, bm, bn);
+  a.tiles_b = static_cast<int>((m + bn - 1) / bn);
+  const int64_t n_tiles = tiles(bm, bn);
+  CM_CHECK_ARG(n_tiles < 0x7fffffff);
+  a.remap = n_tiles % 8 == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nt = static_cast<int>(n_tiles);
+  if (bm == 128 && bn == 128) return launch_cfg<128, 128, true>(a, nt, s);
+  if (bm == 128) return launch_cfg<128, 64, true>(a, nt, s);
+  if (bn == 128) return launch_cfg<64, 128, true>(a, nt, s);
+  return launch_cfg<64, 64, true>(a, nt, s);
+}

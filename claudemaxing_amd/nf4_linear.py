@@ -10,40 +10,165 @@ Linear4bit equivalent that casts its input to `compute_dtype` and its output bac
 input's dtype, as Linear4bit does).
 """
 
+import ctypes
+
 import torch
 
-from .nf4 import QuantState, dequantize_nf4, quantize_nf4
+from . import _lib
+from .nf4 import _BLOCKSIZES, QuantState, _nf4_code, _offset_tensor, dequantize_nf4, quantize_nf4
 from .rmsnorm import fp16_copy_of
+
+# ---------------------------------------------------------------------------------------------
+# The fused path: NF4 weights expanded inside the GEMM (csrc/nf4_gemm.hip), fp16 compute.
+
+
+def fused_supported(packed, state):
+    """Whether cm_nf4_linear_* takes this weight: an fp16-compute NF4 QuantState on the GPU
+    whose rows and columns are multiples of 64 (every Qwen2.5 projection)."""
+    if state is None or getattr(state, "quant_type", None) != "nf4" or not packed.is_cuda:
+        return False
+    shape = getattr(state, "shape", None)
+    if shape is None or len(shape) != 2 or shape[0] % 64 or shape[1] % 64:
+        return False
+    if packed.dtype != torch.uint8 or not packed.is_contiguous() or packed.data_ptr() % 16:
+        return False
+    if state.blocksize not in _BLOCKSIZES or not state.absmax.is_cuda:
+        return False
+    if state.code is not None and (state.code.numel() != 16 or state.code.dtype != torch.float32):
+        return False
+    if state.nested:
+        s2 = state.state2
+        return (state.absmax.dtype == torch.uint8 and s2.code.dtype == torch.float32
+                and s2.absmax.dtype == torch.float32 and s2.blocksize > 0)
+    return state.absmax.dtype == torch.float32
+
+
+def _descriptor(packed, state):
+    """(cm_nf4_weight, tensors it points into that must stay alive for the call)."""
+    nested = bool(state.nested)
+    s2 = state.state2 if nested else None
+    code = _nf4_code(packed.device) if state.code is None else state.code
+    offset = _offset_tensor(state.offset, packed.device) if nested else None
+    d = _lib.NF4Weight(packed.data_ptr(), state.absmax.data_ptr(), int(nested), code.data_ptr(),
+                       _lib.ptr(s2.code if nested else None),
+                       _lib.ptr(s2.absmax if nested else None), _lib.ptr(offset),
+                       int(state.blocksize), int(s2.blocksize) if nested else 1,
+                       int(state.shape[0]), int(state.shape[1]))
+    return d, (code, offset)
+
+
+def _weights(pairs):
+    descs, keep = [], []
+    for packed, state in pairs:
+        d, k = _descriptor(packed, state)
+        descs.append(d)
+        keep.append(k)
+    return (_lib.NF4Weight * len(descs))(*descs), keep
+
+
+# Products below this many FLOPs take the fused kernel; larger ones expand the weight with the
+# dequant kernel and multiply with torch's GEMM, which is faster there (measured on MI355X at
+# 1276 tokens: k/v projections 22.6 vs 30.0 us forward, 14.9 vs 29.2 us backward; q 30.9 vs
+# 30.3 us; gate+up 173 vs 103 us).
+FUSED_MAX_FLOPS = 2.0e9
+
+
+def fused_pays(m, n, k):
+    """Whether the fused kernel is the faster way to multiply m tokens by an [n, k] weight."""
+    return 2.0 * m * n * k < FUSED_MAX_FLOPS
+
+
+def _rows16(t, k):
+    """t as fp16 rows [M, k] with a row stride the kernel takes (unit column stride, a multiple
+    of 8 elements, 16-byte aligned); copies only when it has to."""
+    t2 = t.reshape(-1, k)
+    if (t2.dtype != torch.float16 or t2.stride(1) != 1 or t2.stride(0) % 8
+            or t2.data_ptr() % 16 or t2.stride(0) < k):
+        t2 = t2.to(torch.float16).contiguous()
+    return t2
+
+
+def nf4_linear_fwd(x16, pairs, biases=None, out_dtype=torch.float16):
+    """[x16 @ W_i.T (+ b_i) for (packed_i, state_i) in pairs] in one launch of the fused kernel;
+    x16 fp16 [..., K], biases fp16 [N_i] or None, outputs [..., N_i] in out_dtype (fp16, or fp32
+    = the fp16 result widened)."""
+    k = pairs[0][1].shape[1]
+    x2 = _rows16(x16, k)
+    m = x2.shape[0]
+    outs = [torch.empty(m, st.shape[0], dtype=out_dtype, device=x2.device) for _, st in pairs]
+    w, keep = _weights(pairs)
+    n = len(pairs)
+    bias_arr = None
+    if biases is not None and any(b is not None for b in biases):
+        biases = [None if b is None else b.to(torch.float16).contiguous() for b in biases]
+        bias_arr = (ctypes.c_void_p * n)(*[_lib.ptr(b) for b in biases])
+    out_arr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    ldo = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    _lib.call("cm_nf4_linear_fwd", x2.data_ptr(), x2.stride(0), m, w, n, bias_arr, out_arr, ldo,
+              _lib.dtype_code(out_dtype), _lib.stream(x2.device))
+    del keep
+    lead = x16.shape[:-1]
+    return [o.view(*lead, o.shape[1]) for o in outs]
+
+
+def nf4_linear_bwd(grads, pairs, dx_dtype=torch.float16):
+    """sum_i grads_i @ W_i in one launch of the fused kernel, rounded once to fp16 (widened to
+    fp32 when dx_dtype is fp32); grads_i [..., N_i] (cast to fp16 when they are not)."""
+    k = pairs[0][1].shape[1]
+    g2 = [_rows16(g, st.shape[0]) for g, (_, st) in zip(grads, pairs)]
+    m = g2[0].shape[0]
+    dx = torch.empty(m, k, dtype=dx_dtype, device=g2[0].device)
+    w, keep = _weights(pairs)
+    n = len(pairs)
+    g_arr = (ctypes.c_void_p * n)(*[g.data_ptr() for g in g2])
+    ldg = (ctypes.c_int64 * n)(*[g.stride(0) for g in g2])
+    _lib.call("cm_nf4_linear_bwd", g_arr, ldg, m, w, n, dx.data_ptr(), dx.stride(0),
+              _lib.dtype_code(dx_dtype), _lib.stream(dx.device))
+    del keep
+    return dx.view(*grads[0].shape[:-1], k)
 
 
 class MatMulNF4(torch.autograd.Function):
     """x @ W.T (+ bias) for a frozen NF4 weight W [out, in], computed in `compute` dtype (x's
-    own when None) with W expanded in that dtype each way; an optional frozen bias in that
-    dtype. An fp32 x is taken through the fp16 copy the preceding norm wrote of it when there
-    is one (rmsnorm.fp16_copy_of: the same values as x.to(fp16)), else cast. The output is in
-    the compute dtype; the input gradient is returned in x's dtype."""
+    own when None); an optional frozen bias in that dtype. An fp32 x is taken through the fp16
+    copy the preceding norm wrote of it when there is one (rmsnorm.fp16_copy_of: the same values
+    as x.to(fp16)), else cast. The output is the compute-dtype result, widened to `out_dtype`
+    when that is given; the input gradient is returned in x's dtype.
+
+    In fp16 the weight is expanded inside the GEMM each way (cm_nf4_linear_fwd/bwd); otherwise
+    it is expanded by the dequant kernel and multiplied by torch."""
 
     @staticmethod
-    def forward(ctx, x, packed, state, bias=None, compute=None):
+    def forward(ctx, x, packed, state, bias=None, compute=None, out_dtype=None):
         compute = compute or x.dtype
+        out_dtype = out_dtype or compute
         xc = x
         if x.dtype != compute:
             low = fp16_copy_of(x) if compute == torch.float16 else None
             xc = low if low is not None else x.to(compute)
+        ctx.packed, ctx.state, ctx.x_dtype, ctx.compute = packed, state, x.dtype, compute
+        ctx.fused = (compute == torch.float16 and out_dtype in (torch.float16, torch.float32)
+                     and fused_supported(packed, state)
+                     and fused_pays(xc.numel() // max(xc.shape[-1], 1), *state.shape))
+        if ctx.fused:
+            return nf4_linear_fwd(xc, [(packed, state)], [bias], out_dtype)[0]
         w = dequantize_nf4(packed, state, compute)
-        ctx.packed, ctx.state, ctx.x_dtype = packed, state, x.dtype
-        return torch.nn.functional.linear(xc, w, bias)
+        return torch.nn.functional.linear(xc, w, bias).to(out_dtype)
 
     @staticmethod
     def backward(ctx, grad):
         if not ctx.needs_input_grad[0]:
-            return None, None, None, None, None
+            return None, None, None, None, None, None
+        grad = grad.to(ctx.compute)
+        if ctx.fused and ctx.x_dtype in (torch.float16, torch.float32):
+            dx = nf4_linear_bwd([grad], [(ctx.packed, ctx.state)], ctx.x_dtype)
+            return dx, None, None, None, None, None
         w = dequantize_nf4(ctx.packed, ctx.state, grad.dtype)
-        return torch.matmul(grad, w).to(ctx.x_dtype), None, None, None, None
+        return torch.matmul(grad, w).to(ctx.x_dtype), None, None, None, None, None
 
 
-def matmul_nf4(x, packed, state, bias=None, compute=None):
-    return MatMulNF4.apply(x, packed, state, bias, compute)
+def matmul_nf4(x, packed, state, bias=None, compute=None, out_dtype=None):
+    return MatMulNF4.apply(x, packed, state, bias, compute, out_dtype)
 
 
 class NF4Linear(torch.nn.Module):
@@ -141,9 +266,8 @@ class NF4Linear(torch.nn.Module):
         return cached[1]
 
     def forward(self, x):
-        out = matmul_nf4(x, self.packed, self.quant_state, self._bias_in(self.compute_dtype),
-                         self.compute_dtype)
-        return out.to(self.out_dtype or x.dtype)
+        return matmul_nf4(x, self.packed, self.quant_state, self._bias_in(self.compute_dtype),
+                          self.compute_dtype, self.out_dtype or x.dtype)
 
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

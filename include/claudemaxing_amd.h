@@ -269,6 +269,54 @@ int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const float* weight_
                        const void* x16, const uint8_t* bits, float* dx, void* xd16, int64_t T,
                        int K, int rank, float scale_p, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* NF4 weights expanded inside an fp16 matrix-core GEMM (the fp16 weight is never written to
+ * memory). Replaces, per frozen 4-bit linear of the training step, the pair "dequantize_nf4
+ * (solution/nf4.py:64-82, kernel 26-46) -> fp16 GEMM" that the reference's patched bitsandbytes
+ * matmul runs (solution/nf4.py:102-130: forward F.linear(x, W) and the input gradient
+ * grad @ W) and the MLP recompute's two 4-bit matmuls (solution/swiglu_recompute.py:165-166,
+ * 198-199).
+ *
+ * One weight: bitsandbytes' NF4 storage of W [rows, cols] (row-major, element j = flat index),
+ * the same fields cm_nf4_dequant takes. Every element is expanded exactly as cm_nf4_dequant
+ * expands it to fp16. Requirements: packed 16-byte aligned; rows and cols multiples of 64;
+ * blocksize a power of two >= 32; every weight of one call has the same cols and nested flag.
+ */
+typedef struct cm_nf4_weight {
+  const uint8_t* packed;   /* [rows * cols / 2] */
+  const void* absmax;      /* uint8 [blocks] (nested) or fp32 [blocks] */
+  int nested;
+  const float* code;       /* [16] */
+  const float* code2;      /* [256] (nested) */
+  const float* absmax2;    /* (nested) */
+  const float* offset;     /* [1] (nested) */
+  int blocksize;
+  int blocksize2;
+  int64_t rows;            /* out_features */
+  int64_t cols;            /* in_features */
+} cm_nf4_weight;
+
+/* Forward, for n_w (1..3) weights sharing the input:
+ *   out_i[t][n] = round(sum_k x[t][k] * fp16(W_i[n][k]) + bias_i[n])     (fp32 sums)
+ * x fp16 [m, cols] with row stride ldx (a multiple of 8, 16-byte aligned); bias NULL or an
+ * array of n_w fp16 pointers (entries may be NULL); out_i [m, rows_i] with row stride ldo[i] (a
+ * multiple of 4). out_dtype CM_F16 (round = to fp16) or CM_F32 (round = to fp16, then widened:
+ * the fp16 linear followed by .to(float32)).
+ */
+int cm_nf4_linear_fwd(const void* x, int64_t ldx, int64_t m, const cm_nf4_weight* w, int n_w,
+                      const void* const* bias, void* const* out, const int64_t* ldo,
+                      int out_dtype, void* stream);
+
+/* Input gradient, summed over n_w (1..3) weights:
+ *   dx[t][k] = round(sum_i sum_n g_i[t][n] * fp16(W_i[n][k]))             (fp32 sums)
+ * g_i fp16 [m, rows_i] with row stride ldg[i] (a multiple of 8, 16-byte aligned); dx [m, cols]
+ * with row stride lddx (a multiple of 4), dx_dtype CM_F16 or CM_F32 (rounded to fp16, then
+ * widened). With two weights this is the MLP's dgate Wg + dup Wu rounded once.
+ */
+int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
+                      const cm_nf4_weight* w, int n_w, void* dx, int64_t lddx, int dx_dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,3 +103,50 @@ def test_dtype_codes():
     with pytest.raises(TypeError):
         _lib.dtype_code(torch.complex64)
     assert ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def _nf4_weight(rows, cols, blocksize=64, nested=1):
+    # host-side descriptor with fake, 16-byte aligned addresses: only the argument checks read it
+    return _lib.NF4Weight(0x1000, 0x2000, nested, 0x3000, 0x4000, 0x5000, 0x6000, blocksize, 256,
+                          rows, cols)
+
+
+def test_nf4_linear_argument_checks(lib):
+    Arr = _lib.NF4Weight * 3
+    ptrs = (ctypes.c_void_p * 3)(0x10000, 0x20000, 0x30000)
+    lds = (ctypes.c_int64 * 3)(1536, 1536, 1536)
+    fwd, bwd = lib.cm_nf4_linear_fwd, lib.cm_nf4_linear_bwd
+    ok = Arr(_nf4_weight(1536, 1536), _nf4_weight(256, 1536), _nf4_weight(256, 1536))
+    # empty token batch with valid weights: nothing to do
+    assert fwd(0x40000, 1536, 0, ok, 3, None, ptrs, lds, 1, None) == 0
+    assert bwd(ptrs, lds, 0, ok, 3, 0x40000, 1536, 0, None) == 0
+    # no weights, too many weights, NULL descriptors
+    assert fwd(0x40000, 1536, 4, ok, 0, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40000, 1536, 4, ok, 4, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40000, 1536, 4, None, 1, None, ptrs, lds, 1, None) == INVALID
+    # columns or rows not a multiple of 64, mixed column counts
+    assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(1536, 1500)), 1, None, ptrs, lds, 1,
+               None) == INVALID
+    assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(100, 1536)), 1, None, ptrs, lds, 1,
+               None) == INVALID
+    assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536), _nf4_weight(256, 1472)), 2, None,
+               ptrs, lds, 1, None) == INVALID
+    # blocksize below 32 or not a power of two
+    assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536, 16)), 1, None, ptrs, lds, 1,
+               None) == INVALID
+    assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536, 96)), 1, None, ptrs, lds, 1,
+               None) == INVALID
+    # output dtype other than fp16/fp32, input row stride not a multiple of 8 or below K
+    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, lds, 2, None) == INVALID
+    assert fwd(0x40000, 1532, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40000, 1540, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
+    # misaligned input, output stride below the weight's rows
+    assert fwd(0x40008, 1536, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
+    small = (ctypes.c_int64 * 3)(1024, 1536, 1536)
+    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, small, 1, None) == INVALID
+    # backward: gradient row stride below the weight's rows, dx stride below K
+    assert bwd(ptrs, small, 4, ok, 1, 0x40000, 1536, 1, None) == INVALID
+    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1024, 1, None) == INVALID
+    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1536, 3, None) == INVALID
+    # the C layout of cm_nf4_weight on x86-64: 4 pointers, int + padding, 3 pointers, 2 ints, 2 int64
+    assert _lib.NF4Weight.rows.offset == 64 and ctypes.sizeof(_lib.NF4Weight) == 80
