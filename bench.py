@@ -298,6 +298,68 @@ def k_bandwidth_scale(dev, names):
     return out
 
 
+def k_nf4_linear(dev, names):
+    """The NF4-fused GEMM at the training step's MLP shapes (1276 packed tokens, Qwen2.5-1.5B
+    gate/up [8960,1536]): the gate+up forward (also the backward's recompute) and the input
+    gradient dgate Wg + dup Wu, each beside the unfused path it replaces (the dequant kernel +
+    torch's fp16 GEMM)."""
+    import ctypes
+
+    import torch
+
+    from claudemaxing_amd import _lib, nf4
+    from claudemaxing_amd.nf4_linear import _weights
+
+    m, f, h = 1276, 8960, 1536
+    gen = torch.Generator().manual_seed(0)
+    qs = [nf4.quantize_nf4(torch.randn(f, h, generator=gen) * 0.02, 64, True) for _ in range(2)]
+    x = torch.randn(m, h, generator=gen).half()
+    g = torch.randn(m, f, generator=gen).half()
+    flops = 2 * 2 * m * f * h
+    in_bytes = sum(p.numel() for p, _ in qs) + x.numel() * 2
+    out = []
+    fwd, fwd_ref, bwd, bwd_ref = [], [], [], []
+    for _ in range(copies_for(in_bytes + 2 * g.numel() * 2)):
+        pairs = [(p.to(dev), st.to(dev)) for p, st in qs]
+        xd, gd = x.to(dev), g.to(dev)
+        ys = [torch.empty(m, f, dtype=torch.float16, device=dev) for _ in range(2)]
+        dx = torch.empty(m, h, dtype=torch.float16, device=dev)
+        w_arr, keep = _weights(pairs)
+        out_arr = (ctypes.c_void_p * 2)(*[y.data_ptr() for y in ys])
+        ldo = (ctypes.c_int64 * 2)(f, f)
+        g_arr = (ctypes.c_void_p * 2)(gd.data_ptr(), gd.data_ptr())
+        ldg = (ctypes.c_int64 * 2)(f, f)
+        assert xd.shape == (m, h) and all(y.shape == (m, f) for y in ys) and dx.shape == (m, h)
+        hold = (pairs, xd, gd, ys, dx, w_arr, keep, out_arr, ldo, g_arr, ldg)
+        fwd.append((bound("cm_nf4_linear_fwd", xd.data_ptr(), h, m, w_arr, 2, None, out_arr, ldo,
+                          _lib.F16, None, 0, _stream(dev)), hold))
+        ws_bytes = _lib.load().cm_nf4_linear_workspace_bytes(m, w_arr, 2, 1)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        bwd.append((bound("cm_nf4_linear_bwd", g_arr, ldg, m, w_arr, 2, dx.data_ptr(), h,
+                          _lib.F16, ws.data_ptr(), ws_bytes, _stream(dev)), hold + (ws,)))
+
+        def ref_f(pairs=pairs, xd=xd):
+            for p, st in pairs:
+                torch.nn.functional.linear(xd, nf4.dequantize_nf4(p, st, torch.float16))
+
+        def ref_b(pairs=pairs, gd=gd):
+            wg, wu = (nf4.dequantize_nf4(p, st, torch.float16) for p, st in pairs)
+            torch.addmm(torch.mm(gd, wg), gd, wu)
+
+        fwd_ref.append((ref_f, hold))
+        bwd_ref.append((ref_b, hold))
+    if "nf4_linear_fwd" in names:
+        out.append(Kernel("nf4_linear_fwd", f"gate+up {m} tokens x 2 x [{f},{h}] nf4", "mfma",
+                          flops, fwd))
+        out.append(Kernel("nf4_linear_fwd_unfused", "the same: dequant + torch fp16 GEMM x 2",
+                          "mfma", flops, fwd_ref, step=False))
+    if "nf4_linear_bwd" in names:
+        out.append(Kernel("nf4_linear_bwd", f"dgate Wg + dup Wu, {m} tokens", "mfma", flops, bwd))
+        out.append(Kernel("nf4_linear_bwd_unfused", "the same: dequant x 2 + mm + addmm", "mfma",
+                          flops, bwd_ref, step=False))
+    return out
+
+
 def k_lmhead(dev):
     import torch
 
@@ -320,7 +382,7 @@ def k_lmhead(dev):
 
 ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd", "swiglu_fwd",
        "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "rmsnorm_fwd_bw", "rope_fwd_bw",
-       "lmhead_ce"]
+       "nf4_linear_fwd", "nf4_linear_bwd", "lmhead_ce"]
 
 
 def build_kernels(dev, only):
@@ -343,6 +405,8 @@ def build_kernels(dev, only):
         kernels += k_copy_ref(dev)
     if names & {"rmsnorm_fwd_bw", "rope_fwd_bw"}:
         kernels += k_bandwidth_scale(dev, names)
+    if names & {"nf4_linear_fwd", "nf4_linear_bwd"}:
+        kernels += k_nf4_linear(dev, names)
     if "lmhead_ce" in names:
         kernels += k_lmhead(dev)
     return kernels

@@ -77,8 +77,9 @@ SIGNATURES = {
     "cm_lora_fused_bwd1": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
     "cm_lora_fused_bwd2": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
     "cm_attn_workspace_bytes": (_L, [_L, _I, _I, _I, _I]),
-    "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P]),
-    "cm_nf4_linear_bwd": (_I, [_PP, _PL, _L, _PW, _I, _P, _L, _I, _P]),
+    "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P, _L, _P]),
+    "cm_nf4_linear_bwd": (_I, [_PP, _PL, _L, _PW, _I, _P, _L, _I, _P, _L, _P]),
+    "cm_nf4_linear_workspace_bytes": (_L, [_L, _PW, _I, _I]),
 }
 
 _lock = threading.Lock()

@@ -85,6 +85,10 @@ struct Args {
   void* dx;         // backward output [M, K]
   int64_t lddx;
   int n_stages;     // backward: total stages over all weights
+  // split over the contraction (ws kernel): slices write fp32 partials [split][m][n_out]
+  int split;
+  float* ws;
+  int n_out;        // output columns of the partials
 };
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -129,15 +133,17 @@ __device__ __forceinline__ ScaleRaw load_scale(const WeightDev& w, int nested, i
 // (row-major rows of 8 16-byte chunks, chunk XOR-swizzled by LdsRows<64>::swz(row)).
 
 // Forward: tile rows = weight rows r0 .. r0 + BM, columns kc .. kc + 64. A lane expands EPT =
-// BM / 4 consecutive elements of one row (one block scale: blocksize >= 32 >= EPT).
+// BM / 4 consecutive elements of one row (256 lanes), with one block scale per run of up to 32
+// elements (blocksize >= 32).
 template <int BM>
 struct FwdLoader {
-  static constexpr int kEPT = BM / 4;           // elements per lane per stage
-  static constexpr int kWords = kEPT / 8;       // 4-byte packed words per lane
-  static constexpr int kTPR = kBK / kEPT;       // lanes per tile row
-  static_assert(kWords == 2 || kWords == 4, "BM of 64 or 128");
+  static constexpr int kEPT = BM / 4;             // elements per lane per stage
+  static constexpr int kWords = kEPT / 8;         // 4-byte packed words per lane
+  static constexpr int kTPR = kBK / kEPT;         // lanes per tile row
+  static constexpr int kRuns = kEPT > 32 ? kEPT / 32 : 1;  // block-scale runs per lane
+  static_assert(kWords == 2 || kWords == 4 || kWords == 8, "BM of 64, 128 or 256");
   uint32_t word[kWords];
-  ScaleRaw sc;
+  ScaleRaw sc[kRuns];
   int row, part;
 
   __device__ __forceinline__ void init(int tid) {
@@ -147,26 +153,34 @@ struct FwdLoader {
   __device__ __forceinline__ void load(const WeightDev& w, int nested, int cols, int r0, int kc) {
     const int64_t e0 = static_cast<int64_t>(r0 + row) * cols + kc + part * kEPT;
     const uint32_t* p = w.packed + (e0 >> 3);
-    if constexpr (kWords == 4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(p);
-      word[0] = v.x; word[1] = v.y; word[2] = v.z; word[3] = v.w;
-    } else {
+    if constexpr (kWords == 2) {
       const uint2 v = *reinterpret_cast<const uint2*>(p);
       word[0] = v.x; word[1] = v.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < kWords / 4; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(p)[q];
+        word[4 * q] = v.x; word[4 * q + 1] = v.y; word[4 * q + 2] = v.z; word[4 * q + 3] = v.w;
+      }
     }
-    sc = load_scale(w, nested, e0);
+#pragma unroll
+    for (int r = 0; r < kRuns; ++r) sc[r] = load_scale(w, nested, e0 + 32 * r);
   }
   __device__ __forceinline__ void store(uint4* tile, const float* s_code, const float* s_code2,
                                         float off, int nested) const {
     using L = LdsRows<kBK>;
-    const float s = block_scale(nested, s_code2[nested ? sc.q8 : 0], sc.a2, off, sc.a2);
+    float s[kRuns];
+#pragma unroll
+    for (int r = 0; r < kRuns; ++r)
+      s[r] = block_scale(nested, s_code2[nested ? sc[r].q8 : 0], sc[r].a2, off, sc[r].a2);
 #pragma unroll
     for (int q = 0; q < kWords; ++q) {
+      const float sq = s[(q * 8) / 32 < kRuns ? (q * 8) / 32 : kRuns - 1];
       uint32_t h[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const uint32_t byte = (word[q] >> (8 * b)) & 0xffu;
-        h[b] = pack2(s_code[byte >> 4] * s, s_code[byte & 0xfu] * s);
+        h[b] = pack2(s_code[byte >> 4] * sq, s_code[byte & 0xfu] * sq);
       }
       const int lc = part * kWords + q;
       tile[row * L::kRC + (lc ^ L::swz(row))] = make_uint4(h[0], h[1], h[2], h[3]);
@@ -182,7 +196,7 @@ template <int BM>
 struct BwdLoader {
   static constexpr int kRPT = BM / 32;     // weight rows per lane
   static constexpr int kNG = kBK / kRPT;   // lanes along the contraction
-  static_assert(kRPT == 2 || kRPT == 4, "BM of 64 or 128");
+  static_assert(kRPT == 2 || kRPT == 4 || kRPT == 8, "BM of 64, 128 or 256");
   uint32_t word[kRPT];
   ScaleRaw sc[kRPT];
   int kw, ng;
@@ -221,7 +235,10 @@ struct BwdLoader {
       }
       const int kk = kw * 8 + j;
       char* dst = base + (kk * L::kRC + (lc ^ L::swz(kk))) * 16 + (ncol % 8) * 2;
-      if constexpr (kRPT == 4) {
+      if constexpr (kRPT == 8) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]),
+                                                    pack2(v[4], v[5]), pack2(v[6], v[7]));
+      } else if constexpr (kRPT == 4) {
         *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
       } else {
         *reinterpret_cast<uint32_t*>(dst) = pack2(v[0], v[1]);
@@ -426,6 +443,275 @@ __global__ __launch_bounds__(kThreads, 2) void nf4_gemm_kernel(const Args args) 
 }
 
 // ---------------------------------------------------------------------------------------------
+// Wavefront-specialized version for tiles of BM = 128 or 256 weight-side rows x 128 tokens: one
+// workgroup of 8 wavefronts per CU. Wavefronts 0-3 (the consumers, a 2 x 2 grid) only read LDS
+// fragments and issue MFMAs; wavefronts 4-7 (the producers) fill a ring of 3 LDS stages two
+// stages ahead: the token tile by direct-to-LDS loads, the weight tile expanded from the packed
+// bytes and block scales they loaded one stage earlier. Each SIMD holds one consumer and one
+// producer, so the expansion's VALU and LDS work issues beside the matrix core instead of between
+// its products. One barrier per stage: after the barrier that ends stage kt - 1, stage kt is
+// complete in its slot and the slot of stage kt - 1 is free for stage kt + 2.
+//
+// The contraction may be split over gridDim: slice s of S covers stages [s n / S, (s + 1) n / S)
+// and writes fp32 partial sums; nf4_gemm_reduce adds the slices in order (deterministic), adds
+// the bias and rounds.
+constexpr int kWsThreads = 512;
+constexpr int kRing = 3;
+constexpr int kWsBN = 128;
+
+template <int BM, bool TRANS>
+__global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
+  constexpr int BN = kWsBN;
+  using L = LdsRows<kBK>;
+  constexpr int kRC = L::kRC;
+  constexpr int kSlot = (BM + BN) * kRC;  // uint4 per ring slot
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int KS = kBK / 16;  // MFMA substeps per stage
+  using TB = DmaTile<BN, 4, kBK>;
+  using Loader = typename std::conditional<TRANS, BwdLoader<BM>, FwdLoader<BM>>::type;
+
+  __shared__ uint4 ring[kRing * kSlot];
+  __shared__ float s_code[kMaxW][16];
+  __shared__ float s_code2[kMaxW][256];
+  __shared__ float s_off[kMaxW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % cm::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / cm::kWave);
+  const bool producer = wave >= 4;
+  const int ptid = tid - 4 * cm::kWave;  // producer lane index 0..255
+  const int nested = args.nested;
+
+  if (producer) {
+    for (int i = 0; i < args.n_w; ++i) {
+      if (ptid < 16) s_code[i][ptid] = args.w[i].code[ptid];
+      if (nested) {
+        s_code2[i][ptid] = args.w[i].code2[ptid];
+        if (ptid == 0) s_off[i] = *args.w[i].offset;
+      } else if (ptid == 0) {
+        s_off[i] = 0.0f;
+      }
+    }
+  }
+
+  // workgroup -> (slice, weight-side tile, token tile); consecutive ids share the slice and the
+  // weight tile (XCD-aware when the grid is a multiple of 8)
+  int bid = blockIdx.x;
+  if (args.remap) {
+    const int per = gridDim.x / 8;
+    bid = (bid % 8) * per + bid / 8;
+  }
+  const int n_tiles = gridDim.x / args.split;
+  const int slice = bid / n_tiles;
+  const int tile = bid % n_tiles;
+  const int ta = tile / args.tiles_b, tb = tile % args.tiles_b;
+  const int m0 = tb * BN;
+  int wf = 0;
+  if constexpr (!TRANS) {
+    while (wf + 1 < args.n_w && ta >= args.w[wf + 1].first) ++wf;
+  }
+  const int a0 = TRANS ? ta * BM : (ta - args.w[wf].first) * BM;
+  const int n_all = TRANS ? args.n_stages : args.cols / kBK;
+  const int kb = static_cast<int>(static_cast<int64_t>(slice) * n_all / args.split);
+  const int ke = static_cast<int>(static_cast<int64_t>(slice + 1) * n_all / args.split);
+  const int n_loc = ke - kb;
+
+  auto stage_w = [&](int kt) {
+    if constexpr (!TRANS) {
+      return wf;
+    } else {
+      int i = 0;
+      while (i + 1 < args.n_w && kt >= args.w[i + 1].first) ++i;
+      return i;
+    }
+  };
+  auto stage_k = [&](int kt, int wi) { return TRANS ? (kt - args.w[wi].first) * kBK : kt * kBK; };
+
+  __syncthreads();  // the code tables
+
+  if (producer) {
+    const int pwave = wave - 4;
+    Loader ld;
+    ld.init(ptid);
+    TB lb;
+    auto load_a = [&](int kt) {
+      const int wi = stage_w(kt), kc = stage_k(kt, wi);
+      if constexpr (TRANS) {
+        ld.load(args.w[wi], nested, args.cols, kc, a0);
+      } else {
+        ld.load(args.w[wi], nested, args.cols, a0, kc);
+      }
+    };
+    auto produce = [&](int kt, uint4* slot) {
+      const int wi = stage_w(kt), kc = stage_k(kt, wi);
+      ld.store(slot, s_code[wi], s_code2[wi], s_off[wi], nested);
+      RowMajor src;
+      if constexpr (TRANS) {
+        src.p = args.w[wi].g;
+        src.ld = args.w[wi].ldg;
+        src.k_len = args.w[wi].rows;
+      } else {
+        src.p = args.x;
+        src.ld = args.ldx;
+        src.k_len = args.cols;
+      }
+      src.rows = args.m;
+      lb.init(src, pwave, lane);
+      const bool inside = src.tile_inside(m0, BN, kc);
+#pragma unroll
+      for (int q = 0; q < TB::kPer; ++q) lb.issue(src, m0, kc, slot + BM * kRC, pwave, q, inside);
+    };
+    // prologue: stages 0 .. kRing - 2, and the packed bytes of stage kRing - 1 in registers
+#pragma unroll
+    for (int j = 0; j < kRing - 1; ++j) {
+      if (j < n_loc) {
+        load_a(kb + j);
+        cm::gemm::wait_vmcnt<0>();
+        produce(kb + j, ring + j * kSlot);
+      }
+    }
+    if (kRing - 1 < n_loc) load_a(kb + kRing - 1);
+    cm::gemm::wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    cm::gemm::lds_barrier();
+    for (int kt = 0; kt < n_loc; ++kt) {
+      const int j = kt + kRing - 1;
+      // the token tile of stage kt + 1 (issued one iteration ago) and the packed bytes of stage
+      // j have landed
+      cm::gemm::wait_vmcnt<0>();
+      if (j < n_loc) {
+        produce(kb + j, ring + (j % kRing) * kSlot);
+        if (j + 1 < n_loc) load_a(kb + j + 1);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // this lane's LDS writes have landed
+      cm::gemm::lds_barrier();
+    }
+    return;
+  }
+
+  // consumers
+  const int wm = wave / 2, wn = wave % 2;
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  cm::gemm::lds_barrier();  // the prologue's stages are in the ring
+  const int arow = wm * WTM + lane % 32, brow = wn * WTN + lane % 32;
+  for (int kt = 0; kt < n_loc; ++kt) {
+    const uint4* As = ring + (kt % kRing) * kSlot;
+    const uint4* Bs = As + BM * kRC;
+    half8 af[2][TM], bf[2][TN];
+    auto read = [&](int ks, int b) {
+      const int ch = ks * 2 + lane / 32;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[b][i] = L::frag(As, arow + i * 32, ch);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[b][j] = L::frag(Bs, brow + j * 32, ch);
+    };
+    read(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read(ks + 1, (ks + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][i], bf[ks & 1][j],
+                                                             acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    cm::gemm::lds_barrier();
+  }
+
+  // epilogue: as nf4_gemm_kernel's, or fp32 partials of this slice
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int t = m0 + wn * WTN + j * 32 + lane % 32;
+    if (t >= args.m) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int a = a0 + wm * WTM + i * 32 + g * 8 + (lane / 32) * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
+        if (args.split > 1) {
+          float* dst = args.ws + (static_cast<int64_t>(slice) * args.m + t) * args.n_out + a;
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          continue;
+        }
+        void* out;
+        int64_t off;
+        if constexpr (TRANS) {
+          out = args.dx;
+          off = static_cast<int64_t>(t) * args.lddx + a;
+        } else {
+          const WeightDev& w = args.w[wf];
+          if (w.bias) {
+            const uint2 bb = *reinterpret_cast<const uint2*>(w.bias + a);
+            const _Float16* bh = reinterpret_cast<const _Float16*>(&bb);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += static_cast<float>(bh[e]);
+          }
+          out = w.out;
+          off = static_cast<int64_t>(t) * w.ldo + a;
+        }
+        if (args.out32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(out) + off) =
+              make_float4(cm::round_to<_Float16>(v[0]), cm::round_to<_Float16>(v[1]),
+                          cm::round_to<_Float16>(v[2]), cm::round_to<_Float16>(v[3]));
+        } else {
+          *reinterpret_cast<uint2*>(static_cast<_Float16*>(out) + off) =
+              make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+        }
+      }
+    }
+  }
+}
+
+// Sum of the split's fp32 partials in slice order, plus the bias, rounded to fp16 (and widened
+// with out32). One lane per 4 consecutive outputs.
+__global__ __launch_bounds__(256) void nf4_gemm_reduce(const float* __restrict__ ws, int split,
+                                                        int m, int n_out,
+                                                        const _Float16* __restrict__ bias,
+                                                        void* out, int64_t ldo, int out32) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int quads = n_out / 4;
+  if (q >= static_cast<int64_t>(m) * quads) return;
+  const int t = static_cast<int>(q / quads), a = static_cast<int>(q % quads) * 4;
+  const int64_t slice_stride = static_cast<int64_t>(m) * n_out;
+  const float* src = ws + static_cast<int64_t>(t) * n_out + a;
+  float4 acc = *reinterpret_cast<const float4*>(src);
+  for (int s = 1; s < split; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(src + s * slice_stride);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  if (bias) {
+    acc.x += static_cast<float>(bias[a]);
+    acc.y += static_cast<float>(bias[a + 1]);
+    acc.z += static_cast<float>(bias[a + 2]);
+    acc.w += static_cast<float>(bias[a + 3]);
+  }
+  const int64_t off = static_cast<int64_t>(t) * ldo + a;
+  if (out32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + off) =
+        make_float4(cm::round_to<_Float16>(acc.x), cm::round_to<_Float16>(acc.y),
+                    cm::round_to<_Float16>(acc.z), cm::round_to<_Float16>(acc.w));
+  } else {
+    *reinterpret_cast<uint2*>(static_cast<_Float16*>(out) + off) =
+        make_uint2(pack2(acc.x, acc.y), pack2(acc.z, acc.w));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 int log2_exact(int64_t v) {
   if (v <= 0 || (v & (v - 1))) return -1;
   int s = 0;
@@ -480,39 +766,179 @@ int setup(const cm_nf4_weight* w, int n_w, int64_t m, Args& a) {
   return 0;
 }
 
-// Tile shape per call: the largest tiles that still give every CU a workgroup; the smallest
-// when none does.
+// Tile shape per call for the general kernel: the largest tiles that still give every CU a
+// workgroup; the smallest when none does.
 template <class TilesFn>
-int pick_tiles(TilesFn tiles, bool allow128, int& bm, int& bn) {
+void pick_tiles(TilesFn tiles, bool allow128, int& bm, int& bn) {
   const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
   for (const auto& c : cand) {
     if (c[0] == 128 && !allow128) continue;
     if (tiles(c[0], c[1]) >= kCUs) {
       bm = c[0];
       bn = c[1];
-      return 0;
+      return;
     }
   }
   bm = 64;
   bn = 64;
+}
+
+// How one call runs: the wavefront-specialized kernel (ws) when the weight-side extent is a
+// multiple of 128, with the contraction split when the tiles alone leave CUs idle; the general
+// kernel otherwise.
+struct Plan {
+  bool ws;
+  int bm, bn, split;
+  int64_t tiles;     // output tiles (workgroups = tiles * split)
+  int n_out;         // output columns (weight rows forward, weight columns backward)
+  int64_t ws_bytes;  // fp32 partials of a split
+};
+
+Plan plan_for(const Args& a, bool trans) {
+  Plan p{};
+  const int64_t tb = (static_cast<int64_t>(a.m) + kWsBN - 1) / kWsBN;
+  int64_t rows_total = 0;
+  bool all128 = true, all256 = true;
+  for (int i = 0; i < a.n_w; ++i) {
+    rows_total += a.w[i].rows;
+    all128 = all128 && a.w[i].rows % 128 == 0;
+    all256 = all256 && a.w[i].rows % 256 == 0;
+  }
+  const int extent = trans ? a.cols : static_cast<int>(rows_total);
+  const bool e128 = trans ? a.cols % 128 == 0 : all128;
+  const bool e256 = trans ? a.cols % 256 == 0 : all256;
+  p.n_out = trans ? a.cols : (a.n_w == 1 ? a.w[0].rows : 0);
+  if (e128) {
+    p.ws = true;
+    p.bn = kWsBN;
+    p.bm = e256 ? 256 : 128;
+    p.tiles = extent / p.bm * tb;
+    if (p.bm == 256 && p.tiles < kCUs / 2) {
+      p.bm = 128;
+      p.tiles = extent / p.bm * tb;
+    }
+    const int n_all = trans ? a.n_stages : a.cols / kBK;
+    p.split = 1;
+    if (p.tiles < 3 * kCUs / 4 && (trans || a.n_w == 1)) {
+      int64_t sp = kCUs / (p.tiles > 0 ? p.tiles : 1);
+      if (sp > 8) sp = 8;
+      if (sp > n_all / 8) sp = n_all / 8;
+      if (sp > 1) p.split = static_cast<int>(sp);
+    }
+    p.ws_bytes = p.split > 1 ? int64_t{4} * p.split * a.m * p.n_out : 0;
+    return p;
+  }
+  p.ws = false;
+  p.split = 1;
+  auto tiles = [&](int bm, int bn) {
+    return static_cast<int64_t>(extent / bm) * ((a.m + bn - 1) / bn);
+  };
+  pick_tiles(tiles, trans ? a.cols % 128 == 0 : all128, p.bm, p.bn);
+  p.tiles = tiles(p.bm, p.bn);
+  return p;
+}
+
+template <int BM, bool TRANS>
+int launch_ws(const Args& a, int64_t blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((nf4_gemm_ws<BM, TRANS>), dim3(static_cast<uint32_t>(blocks)),
+                     dim3(kWsThreads), 0, stream, a);
+  return cm::launch_status();
+}
+
+// Launch per plan (first fields of `first` already set: the forward's tile offsets are filled
+// here). out/ldo/bias of the reduce: the one output of the call.
+int run(Args& a, Plan p, bool trans, void* workspace, int64_t ws_bytes, void* out, int64_t ldo,
+        const _Float16* bias, hipStream_t s) {
+  if (p.ws && p.split > 1 &&
+      (workspace == nullptr || ws_bytes < p.ws_bytes || !cm::aligned(workspace, 16))) {
+    p.split = 1;  // no room for the partials: one slice (same results, fewer workgroups)
+  }
+  if (!trans) {
+    int first = 0;
+    for (int i = 0; i < a.n_w; ++i) {
+      a.w[i].first = first;
+      first += a.w[i].rows / p.bm;
+    }
+  }
+  a.tiles_b = static_cast<int>((a.m + p.bn - 1) / p.bn);
+  const int64_t blocks = p.tiles * p.split;
+  CM_CHECK_ARG(blocks > 0 && blocks < 0x7fffffff);
+  a.remap = blocks % 8 == 0;
+  a.split = p.split;
+  a.ws = p.split > 1 ? static_cast<float*>(workspace) : nullptr;
+  a.n_out = p.n_out;
+  int st;
+  if (p.ws) {
+    if (trans) {
+      st = p.bm == 256 ? launch_ws<256, true>(a, blocks, s) : launch_ws<128, true>(a, blocks, s);
+    } else {
+      st = p.bm == 256 ? launch_ws<256, false>(a, blocks, s)
+                       : launch_ws<128, false>(a, blocks, s);
+    }
+  } else {
+    const int nt = static_cast<int>(blocks);
+    if (trans) {
+      if (p.bm == 128 && p.bn == 128) st = launch_cfg<128, 128, true>(a, nt, s);
+      else if (p.bm == 128) st = launch_cfg<128, 64, true>(a, nt, s);
+      else if (p.bn == 128) st = launch_cfg<64, 128, true>(a, nt, s);
+      else st = launch_cfg<64, 64, true>(a, nt, s);
+    } else {
+      if (p.bm == 128 && p.bn == 128) st = launch_cfg<128, 128, false>(a, nt, s);
+      else if (p.bm == 128) st = launch_cfg<128, 64, false>(a, nt, s);
+      else if (p.bn == 128) st = launch_cfg<64, 128, false>(a, nt, s);
+      else st = launch_cfg<64, 64, false>(a, nt, s);
+    }
+  }
+  if (st || p.split == 1) return st;
+  const int64_t quads = static_cast<int64_t>(a.m) * (p.n_out / 4);
+  hipLaunchKernelGGL(nf4_gemm_reduce, dim3(static_cast<uint32_t>((quads + 255) / 256)), dim3(256),
+                     0, s, a.ws, p.split, a.m, p.n_out, bias, out, ldo, a.out32);
+  return cm::launch_status();
+}
+
+int fwd_args(const void* x, int64_t ldx, int64_t m, const cm_nf4_weight* w, int n_w, Args& a) {
+  if (int st = setup(w, n_w, m, a)) return st;
+  if (m > 0) CM_CHECK_ARG(x && cm::aligned(x, 16) && ldx >= a.cols && ldx % 8 == 0);
+  a.x = static_cast<const _Float16*>(x);
+  a.ldx = ldx;
+  return 0;
+}
+
+int bwd_args(const cm_nf4_weight* w, int n_w, int64_t m, Args& a) {
+  if (int st = setup(w, n_w, m, a)) return st;
+  int stages = 0;
+  for (int i = 0; i < n_w; ++i) {
+    a.w[i].first = stages;
+    stages += a.w[i].rows / kBK;
+  }
+  a.n_stages = stages;
   return 0;
 }
 
 }  // namespace
 
+extern "C" int64_t cm_nf4_linear_workspace_bytes(int64_t m, const cm_nf4_weight* w, int n_w,
+                                                 int backward) {
+  Args a;
+  if (setup(w, n_w, m, a)) return -1;
+  if (m == 0) return 0;
+  if (backward) {
+    bwd_args(w, n_w, m, a);
+    return plan_for(a, true).ws_bytes;
+  }
+  return plan_for(a, false).ws_bytes;
+}
+
 extern "C" int cm_nf4_linear_fwd(const void* x, int64_t ldx, int64_t m, const cm_nf4_weight* w,
                                  int n_w, const void* const* bias, void* const* out,
-                                 const int64_t* ldo, int out_dtype, void* stream) {
+                                 const int64_t* ldo, int out_dtype, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
   Args a;
-  if (int st = setup(w, n_w, m, a)) return st;
   CM_CHECK_ARG(out_dtype == CM_F16 || out_dtype == CM_F32);
   CM_CHECK_ARG(out != nullptr && ldo != nullptr);
+  if (int st = fwd_args(x, ldx, m, w, n_w, a)) return st;
   if (m == 0) return 0;
-  CM_CHECK_ARG(x && cm::aligned(x, 16) && ldx >= a.cols && ldx % 8 == 0);
-  a.x = static_cast<const _Float16*>(x);
-  a.ldx = ldx;
   a.out32 = out_dtype == CM_F32;
-  bool all128 = true;
   for (int i = 0; i < n_w; ++i) {
     WeightDev& d = a.w[i];
     CM_CHECK_ARG(out[i] && ldo[i] >= d.rows && ldo[i] % 4 == 0);
@@ -521,67 +947,32 @@ extern "C" int cm_nf4_linear_fwd(const void* x, int64_t ldx, int64_t m, const cm
     d.ldo = ldo[i];
     d.bias = bias ? static_cast<const _Float16*>(bias[i]) : nullptr;
     if (d.bias) CM_CHECK_ARG(cm::aligned(d.bias, 8));
-    all128 = all128 && d.rows % 128 == 0;
   }
-  auto tiles = [&](int bm, int bn) {
-    int64_t ta = 0;
-    for (int i = 0; i < n_w; ++i) ta += a.w[i].rows / bm;
-    return ta * ((m + bn - 1) / bn);
-  };
-  int bm, bn;
-  pick_tiles(tiles, all128, bm, bn);
-  int first = 0;
-  for (int i = 0; i < n_w; ++i) {
-    a.w[i].first = first;
-    first += a.w[i].rows / bm;
-  }
-  a.tiles_b = static_cast<int>((m + bn - 1) / bn);
-  const int64_t n_tiles = tiles(bm, bn);
-  CM_CHECK_ARG(n_tiles < 0x7fffffff);
-  a.remap = n_tiles % 8 == 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nt = static_cast<int>(n_tiles);
-  if (bm == 128 && bn == 128) return launch_cfg<128, 128, false>(a, nt, s);
-  if (bm == 128) return launch_cfg<128, 64, false>(a, nt, s);
-  if (bn == 128) return launch_cfg<64, 128, false>(a, nt, s);
-  return launch_cfg<64, 64, false>(a, nt, s);
+  const Plan p = plan_for(a, false);
+  return run(a, p, false, workspace, workspace_bytes, a.w[0].out, a.w[0].ldo, a.w[0].bias,
+             static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
                                  const cm_nf4_weight* w, int n_w, void* dx, int64_t lddx,
-                                 int dx_dtype, void* stream) {
+                                 int dx_dtype, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
   Args a;
-  if (int st = setup(w, n_w, m, a)) return st;
   CM_CHECK_ARG(dx_dtype == CM_F16 || dx_dtype == CM_F32);
   CM_CHECK_ARG(g != nullptr && ldg != nullptr);
+  if (int st = bwd_args(w, n_w, m, a)) return st;
   if (m == 0) return 0;
   a.out32 = dx_dtype == CM_F32;
   CM_CHECK_ARG(dx && lddx >= a.cols && lddx % 4 == 0 && cm::aligned(dx, a.out32 ? 16 : 8));
   a.dx = dx;
   a.lddx = lddx;
-  int stages = 0;
   for (int i = 0; i < n_w; ++i) {
     WeightDev& d = a.w[i];
     CM_CHECK_ARG(g[i] && cm::aligned(g[i], 16) && ldg[i] >= d.rows && ldg[i] % 8 == 0);
     d.g = static_cast<const _Float16*>(g[i]);
     d.ldg = ldg[i];
-    d.first = stages;
-    stages += d.rows / kBK;
   }
-  a.n_stages = stages;
-  auto tiles = [&](int bm, int bn) {
-    return static_cast<int64_t>(a.cols / bm) * ((m + bn - 1) / bn);
-  };
-  int bm, bn;
-  pick_tiles(tiles, a.cols % 128 == 0, bm, bn);
-  a.tiles_b = static_cast<int>((m + bn - 1) / bn);
-  const int64_t n_tiles = tiles(bm, bn);
-  CM_CHECK_ARG(n_tiles < 0x7fffffff);
-  a.remap = n_tiles % 8 == 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nt = static_cast<int>(n_tiles);
-  if (bm == 128 && bn == 128) return launch_cfg<128, 128, true>(a, nt, s);
-  if (bm == 128) return launch_cfg<128, 64, true>(a, nt, s);
-  if (bn == 128) return launch_cfg<64, 128, true>(a, nt, s);
-  return launch_cfg<64, 64, true>(a, nt, s);
+  const Plan p = plan_for(a, true);
+  return run(a, p, true, workspace, workspace_bytes, dx, lddx, nullptr,
+             static_cast<hipStream_t>(stream));
 }

@@ -88,6 +88,15 @@ def _rows16(t, k):
     return t2
 
 
+def _workspace(m, w, n, backward, device):
+    """The fp32 partial-sum buffer a split contraction needs (None when the call does not split),
+    from torch's caching allocator on the current stream."""
+    nbytes = _lib.load().cm_nf4_linear_workspace_bytes(m, w, n, backward)
+    if nbytes < 0:
+        raise RuntimeError("cm_nf4_linear_workspace_bytes: invalid weights")
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
 def nf4_linear_fwd(x16, pairs, biases=None, out_dtype=torch.float16):
     """[x16 @ W_i.T (+ b_i) for (packed_i, state_i) in pairs] in one launch of the fused kernel;
     x16 fp16 [..., K], biases fp16 [N_i] or None, outputs [..., N_i] in out_dtype (fp16, or fp32
@@ -104,8 +113,10 @@ def nf4_linear_fwd(x16, pairs, biases=None, out_dtype=torch.float16):
         bias_arr = (ctypes.c_void_p * n)(*[_lib.ptr(b) for b in biases])
     out_arr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     ldo = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    ws = _workspace(m, w, n, 0, x2.device)
     _lib.call("cm_nf4_linear_fwd", x2.data_ptr(), x2.stride(0), m, w, n, bias_arr, out_arr, ldo,
-              _lib.dtype_code(out_dtype), _lib.stream(x2.device))
+              _lib.dtype_code(out_dtype), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+              _lib.stream(x2.device))
     del keep
     lead = x16.shape[:-1]
     return [o.view(*lead, o.shape[1]) for o in outs]
@@ -122,8 +133,10 @@ def nf4_linear_bwd(grads, pairs, dx_dtype=torch.float16):
     n = len(pairs)
     g_arr = (ctypes.c_void_p * n)(*[g.data_ptr() for g in g2])
     ldg = (ctypes.c_int64 * n)(*[g.stride(0) for g in g2])
+    ws = _workspace(m, w, n, 1, dx.device)
     _lib.call("cm_nf4_linear_bwd", g_arr, ldg, m, w, n, dx.data_ptr(), dx.stride(0),
-              _lib.dtype_code(dx_dtype), _lib.stream(dx.device))
+              _lib.dtype_code(dx_dtype), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+              _lib.stream(dx.device))
     del keep
     return dx.view(*grads[0].shape[:-1], k)
 

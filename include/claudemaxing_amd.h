@@ -302,20 +302,28 @@ typedef struct cm_nf4_weight {
  * array of n_w fp16 pointers (entries may be NULL); out_i [m, rows_i] with row stride ldo[i] (a
  * multiple of 4). out_dtype CM_F16 (round = to fp16) or CM_F32 (round = to fp16, then widened:
  * the fp16 linear followed by .to(float32)).
+ * workspace: device memory of cm_nf4_linear_workspace_bytes(m, w, n_w, 0) bytes (16-byte
+ * aligned) for the fp32 partial sums of a split contraction; NULL (or fewer bytes) runs the
+ * contraction unsplit: the same results, on fewer workgroups.
  */
 int cm_nf4_linear_fwd(const void* x, int64_t ldx, int64_t m, const cm_nf4_weight* w, int n_w,
                       const void* const* bias, void* const* out, const int64_t* ldo,
-                      int out_dtype, void* stream);
+                      int out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Input gradient, summed over n_w (1..3) weights:
  *   dx[t][k] = round(sum_i sum_n g_i[t][n] * fp16(W_i[n][k]))             (fp32 sums)
  * g_i fp16 [m, rows_i] with row stride ldg[i] (a multiple of 8, 16-byte aligned); dx [m, cols]
  * with row stride lddx (a multiple of 4), dx_dtype CM_F16 or CM_F32 (rounded to fp16, then
- * widened). With two weights this is the MLP's dgate Wg + dup Wu rounded once.
+ * widened). With two weights this is the MLP's dgate Wg + dup Wu rounded once. workspace as for
+ * cm_nf4_linear_fwd (backward = 1).
  */
 int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
                       const cm_nf4_weight* w, int n_w, void* dx, int64_t lddx, int dx_dtype,
-                      void* stream);
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of cm_nf4_linear_fwd (backward = 0) or cm_nf4_linear_bwd (backward = 1) for
+ * these sizes (0: the call does not split its contraction), -1 for invalid weights. */
+int64_t cm_nf4_linear_workspace_bytes(int64_t m, const cm_nf4_weight* w, int n_w, int backward);
 
 #ifdef __cplusplus
 }

@@ -51,9 +51,9 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_lora_pack(None, 0, None, None, None, 7, 1.0, None) == INVALID  # n % 8
     assert lib.cm_lora_unpack(None, None, None, None, None, 0, -8, 1.0, None) == INVALID
     assert lib.cm_nf4_dequant(None, None, 1, None, None, None, None, None, 1, 10, 48, 256,
-                              None) == INVALID  # blocksize not a power of two
+                              None, 0, None) == INVALID  # blocksize not a power of two
     assert lib.cm_nf4_dequant(None, None, 1, None, None, None, None, None, 1, 10, 16, 256,
-                              None) == INVALID  # blocksize below 32
+                              None, 0, None) == INVALID  # blocksize below 32
     assert lib.cm_rope(None, 1, 0, 0, 0, 1, None, 1, None, 1, 0, 0, 0, 0, None, 1, None, None,
                        1, 0, 0, 1, 1, 7, 0, None) == INVALID  # odd head_dim
     assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, -1, 1, None) == INVALID
@@ -66,9 +66,9 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1532, 1536,
                                  16, 1.05, 2.0, None) == INVALID
     assert lib.cm_lora_fused_bwd1(None, None, None, None, None, 4, 4096, 16, 2.0,
-                                  None) == INVALID
+                                  None, 0, None) == INVALID
     assert lib.cm_lora_fused_bwd2(None, None, None, None, None, None, None, 4, 4096, 16, 1.05,
-                                  None) == INVALID
+                                  None, 0, None) == INVALID
 
 
 def test_empty_inputs_are_no_ops(lib):
@@ -118,35 +118,41 @@ def test_nf4_linear_argument_checks(lib):
     fwd, bwd = lib.cm_nf4_linear_fwd, lib.cm_nf4_linear_bwd
     ok = Arr(_nf4_weight(1536, 1536), _nf4_weight(256, 1536), _nf4_weight(256, 1536))
     # empty token batch with valid weights: nothing to do
-    assert fwd(0x40000, 1536, 0, ok, 3, None, ptrs, lds, 1, None) == 0
-    assert bwd(ptrs, lds, 0, ok, 3, 0x40000, 1536, 0, None) == 0
+    assert fwd(0x40000, 1536, 0, ok, 3, None, ptrs, lds, 1, None, 0, None) == 0
+    assert bwd(ptrs, lds, 0, ok, 3, 0x40000, 1536, 0, None, 0, None) == 0
     # no weights, too many weights, NULL descriptors
-    assert fwd(0x40000, 1536, 4, ok, 0, None, ptrs, lds, 1, None) == INVALID
-    assert fwd(0x40000, 1536, 4, ok, 4, None, ptrs, lds, 1, None) == INVALID
-    assert fwd(0x40000, 1536, 4, None, 1, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40000, 1536, 4, ok, 0, None, ptrs, lds, 1, None, 0, None) == INVALID
+    assert fwd(0x40000, 1536, 4, ok, 4, None, ptrs, lds, 1, None, 0, None) == INVALID
+    assert fwd(0x40000, 1536, 4, None, 1, None, ptrs, lds, 1, None, 0, None) == INVALID
     # columns or rows not a multiple of 64, mixed column counts
     assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(1536, 1500)), 1, None, ptrs, lds, 1,
-               None) == INVALID
+               None, 0, None) == INVALID
     assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(100, 1536)), 1, None, ptrs, lds, 1,
-               None) == INVALID
+               None, 0, None) == INVALID
     assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536), _nf4_weight(256, 1472)), 2, None,
-               ptrs, lds, 1, None) == INVALID
+               ptrs, lds, 1, None, 0, None) == INVALID
     # blocksize below 32 or not a power of two
     assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536, 16)), 1, None, ptrs, lds, 1,
-               None) == INVALID
+               None, 0, None) == INVALID
     assert fwd(0x40000, 1536, 4, Arr(_nf4_weight(256, 1536, 96)), 1, None, ptrs, lds, 1,
-               None) == INVALID
+               None, 0, None) == INVALID
     # output dtype other than fp16/fp32, input row stride not a multiple of 8 or below K
-    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, lds, 2, None) == INVALID
-    assert fwd(0x40000, 1532, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
-    assert fwd(0x40000, 1540, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, lds, 2, None, 0, None) == INVALID
+    assert fwd(0x40000, 1532, 4, ok, 1, None, ptrs, lds, 1, None, 0, None) == INVALID
+    assert fwd(0x40000, 1540, 4, ok, 1, None, ptrs, lds, 1, None, 0, None) == INVALID
     # misaligned input, output stride below the weight's rows
-    assert fwd(0x40008, 1536, 4, ok, 1, None, ptrs, lds, 1, None) == INVALID
+    assert fwd(0x40008, 1536, 4, ok, 1, None, ptrs, lds, 1, None, 0, None) == INVALID
     small = (ctypes.c_int64 * 3)(1024, 1536, 1536)
-    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, small, 1, None) == INVALID
+    assert fwd(0x40000, 1536, 4, ok, 1, None, ptrs, small, 1, None, 0, None) == INVALID
     # backward: gradient row stride below the weight's rows, dx stride below K
-    assert bwd(ptrs, small, 4, ok, 1, 0x40000, 1536, 1, None) == INVALID
-    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1024, 1, None) == INVALID
-    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1536, 3, None) == INVALID
+    assert bwd(ptrs, small, 4, ok, 1, 0x40000, 1536, 1, None, 0, None) == INVALID
+    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1024, 1, None, 0, None) == INVALID
+    assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1536, 3, None, 0, None) == INVALID
+    # workspace sizes: split contractions need fp32 partials, the gate+up launch does not
+    ws = lib.cm_nf4_linear_workspace_bytes
+    assert ws(1276, Arr(_nf4_weight(8960, 1536), _nf4_weight(8960, 1536)), 2, 0) == 0
+    down = Arr(_nf4_weight(1536, 8960))
+    assert ws(1276, down, 1, 0) == 4 * 2 * 1276 * 1536  # 2 slices of [1276, 1536] fp32
+    assert ws(0, down, 1, 0) == 0 and ws(4, Arr(_nf4_weight(100, 64)), 1, 0) == -1
     # the C layout of cm_nf4_weight on x86-64: 4 pointers, int + padding, 3 pointers, 2 ints, 2 int64
     assert _lib.NF4Weight.rows.offset == 64 and ctypes.sizeof(_lib.NF4Weight) == 80

@@ -66,6 +66,29 @@ def ranges(args_by_name):
         x16, bits, g16, xd, dx, dxdt, n, _, _ = a
         out += [(x16, 2 * n, "x16"), (bits, n // 8, "bits"), (g16, 2 * n, "g16"),
                 (xd, 2 * n, "xd"), (dx, n * NBYTES[dxdt], "dx")]
+    elif name in ("cm_nf4_linear_fwd", "cm_nf4_linear_bwd"):
+        if name == "cm_nf4_linear_fwd":
+            x, ldx, m, w, n_w, bias, outs, ldo, odt, ws, ws_bytes, _ = a
+        else:
+            gs, ldg, m, w, n_w, dx, lddx, odt, ws, ws_bytes, _ = a
+        for i in range(n_w):
+            wi = w[i]
+            n_el = wi.rows * wi.cols
+            n_blk = n_el // wi.blocksize
+            out += [(wi.packed, n_el // 2, "packed"), (wi.absmax, n_blk, "absmax"),
+                    (wi.code, 64, "code"), (wi.code2, 1024, "code2"),
+                    (wi.absmax2, 4 * math.ceil(n_blk / wi.blocksize2), "absmax2"),
+                    (wi.offset, 4, "offset")]
+            if name == "cm_nf4_linear_fwd":
+                out.append((outs[i], ((m - 1) * ldo[i] + wi.rows) * NBYTES[odt], "out"))
+            else:
+                out.append((gs[i], ((m - 1) * ldg[i] + wi.rows) * 2, "g"))
+        if name == "cm_nf4_linear_fwd":
+            out.append((x, ((m - 1) * ldx + w[0].cols) * 2, "x"))
+        else:
+            out.append((dx, ((m - 1) * lddx + w[0].cols) * NBYTES[odt], "dx"))
+        if ws:
+            out.append((ws, ws_bytes, "workspace"))
     else:
         raise AssertionError(f"no range rule for {name}")
     return out
@@ -104,10 +127,13 @@ def test_every_bench_launch_stays_inside_its_tensors(recorded):
     dev = torch.device("cpu")
     names = set(bench.ALL) - {"lmhead_ce", "hbm_copy_ref"}
     kernels = bench.build_kernels(dev, sorted(names))
-    assert {k.name for k in kernels} == names
+    assert {k.name for k in kernels if not k.name.endswith("_unfused")} == names
     checked = 0
     for kern in kernels:
         for fn, keep in kern.launches:
+            if not hasattr(fn, "record"):  # a torch reference path, not a C-ABI launch
+                assert kern.name.endswith("_unfused"), kern.name
+                continue
             owned = storages(keep, [])
             for ptr, nbytes, what in ranges(fn.record):
                 if ptr is None or nbytes <= 0:

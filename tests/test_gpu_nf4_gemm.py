@@ -62,8 +62,13 @@ def check_product(out, x16, ws, what, bias=None, trans=False, grads=None):
     assert torch.equal(got.to(torch.float16).double(), got), f"{what}: not fp16-valued"
 
 
+# (256, 1536): 256-row tiles with a split contraction; (1536, 128): unsplit; (192, 640): the
+# general kernel forward; (384, 576): 128-row tiles forward, the general kernel backward
+IDENTITY_SHAPES = [(256, 1536), (1536, 128), (192, 640), (384, 576)]
+
+
 @pytest.mark.parametrize("nested", [True, False])
-@pytest.mark.parametrize("n,k", [(256, 1536), (1536, 128), (192, 640)])
+@pytest.mark.parametrize("n,k", IDENTITY_SHAPES)
 def test_forward_expansion_is_bitexact(n, k, nested, dev):
     banner(f"nf4_gemm fwd identity n={n} k={k} nested={nested}")
     packed, state, w16 = make_weight(n, k, 1, nested)
@@ -74,7 +79,7 @@ def test_forward_expansion_is_bitexact(n, k, nested, dev):
 
 
 @pytest.mark.parametrize("nested", [True, False])
-@pytest.mark.parametrize("n,k", [(256, 1536), (1536, 128), (192, 640)])
+@pytest.mark.parametrize("n,k", IDENTITY_SHAPES)
 def test_backward_expansion_is_bitexact(n, k, nested, dev):
     banner(f"nf4_gemm bwd identity n={n} k={k} nested={nested}")
     packed, state, w16 = make_weight(n, k, 2, nested)
@@ -159,8 +164,10 @@ def test_mlp_shapes_two_weights(dev):
     check_product(dx, None, [wg, wu], "dgate Wg + dup Wu", trans=True, grads=[dg, du])
 
 
-def test_three_weights_with_biases_and_strided_input(dev):
+def test_three_weights_with_biases_and_strided_input(dev, monkeypatch):
     banner("nf4_gemm q/k/v in one launch, strided x")
+    import claudemaxing_amd.nf4_linear as NL
+
     m, h = 517, 1536
     ws = [make_weight(n, h, 20 + i) for i, n in enumerate((1536, 256, 256))]
     pairs = [to_dev(p, s, dev) for p, s, _ in ws]
@@ -169,10 +176,30 @@ def test_three_weights_with_biases_and_strided_input(dev):
     big = torch.randn(m, h + 64, generator=torch.Generator().manual_seed(31)).half().to(dev)
     x = big[:, 32:32 + h]  # row stride 1600 elements, 64-byte aligned start
     outs = nf4_linear_fwd(x, pairs, [b.to(dev) for b in biases])
+    # single launches without a split contraction sum every output in the same order (stages in
+    # sequence, the same MFMA substeps), whatever the tile shape: the same bits
+    monkeypatch.setattr(NL, "_workspace", lambda *a: None)
     for i, ((p, s, w16), b, o) in enumerate(zip(ws, biases, outs)):
         (single,) = nf4_linear_fwd(x.contiguous(), [pairs[i]], [b.to(dev)])
         assert_bits_equal(o, single, f"weight {i} of three")
         check_product(o, x.cpu(), w16, f"weight {i}", b)
+
+
+def test_unsplit_without_workspace(dev, monkeypatch):
+    banner("nf4_gemm split contraction vs no workspace")
+    import claudemaxing_amd.nf4_linear as NL
+
+    m, n, k = 1276, 1536, 8960  # down_proj: split in two slices when the workspace is there
+    packed, state, w16 = make_weight(n, k, 60)
+    pd = to_dev(packed, state, dev)
+    x16 = torch.randn(m, k, generator=torch.Generator().manual_seed(61)).half()
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(62)) * 0.1).half()
+    (split,) = nf4_linear_fwd(x16.to(dev), [pd], [bias.to(dev)])
+    monkeypatch.setattr(NL, "_workspace", lambda *a: None)
+    (whole,) = nf4_linear_fwd(x16.to(dev), [pd], [bias.to(dev)])
+    torch.cuda.synchronize()
+    check_product(split, x16, w16, "split", bias)
+    check_product(whole, x16, w16, "unsplit", bias)
 
 
 def test_supported_predicate(dev):
