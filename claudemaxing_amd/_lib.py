@@ -44,6 +44,7 @@ class NF4Weight(ctypes.Structure):
         ("blocksize2", ctypes.c_int),
         ("rows", ctypes.c_int64),
         ("cols", ctypes.c_int64),
+        ("scale_map", ctypes.c_void_p),
     ]
 
 
@@ -80,6 +81,7 @@ SIGNATURES = {
     "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P, _L, _P]),
     "cm_nf4_linear_bwd": (_I, [_PP, _PL, _L, _PW, _I, _P, _L, _I, _P, _L, _P]),
     "cm_nf4_linear_workspace_bytes": (_L, [_L, _PW, _I, _I]),
+    "cm_nf4_scale_map": (_I, [_PW, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -54,6 +54,7 @@ constexpr int kMaxW = 3;
 
 struct WeightDev {
   const uint32_t* packed;  // 4-byte words of the packed weight
+  const float* smap;       // fp32 block scales [cols / blocksize][rows], or null
   const void* absmax;      // uint8 (nested) or fp32 block scales
   const float* absmax2;
   const float* offset;
@@ -443,60 +444,137 @@ __global__ __launch_bounds__(kThreads, 2) void nf4_gemm_kernel(const Args args) 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wavefront-specialized version for tiles of BM = 128 or 256 weight-side rows x 128 tokens: one
-// workgroup of 8 wavefronts per CU. Wavefronts 0-3 (the consumers, a 2 x 2 grid) only read LDS
-// fragments and issue MFMAs; wavefronts 4-7 (the producers) fill a ring of 3 LDS stages two
-// stages ahead: the token tile by direct-to-LDS loads, the weight tile expanded from the packed
-// bytes and block scales they loaded one stage earlier. Each SIMD holds one consumer and one
-// producer, so the expansion's VALU and LDS work issues beside the matrix core instead of between
-// its products. One barrier per stage: after the barrier that ends stage kt - 1, stage kt is
-// complete in its slot and the slot of stage kt - 1 is free for stage kt + 2.
+// Wavefront-specialized version for weights with a scale map (fp32 block scales decoded once per
+// weight, cm_nf4_scale_map), tiles of BM = 128 or 256 weight-side rows x 128 tokens, one
+// workgroup of 8 wavefronts per CU.
+//
+// Wavefronts 0-3 (consumers, a 2 x 2 grid) only read LDS fragments and issue MFMAs. Wavefronts
+// 4-7 (producers) move every byte from HBM/L2 by direct-to-LDS loads (global_load_lds), so the
+// only memory waits in the loop are the producers' explicit vmcnt waits:
+//   - raw stage data in a ring of 3 slots, issued two stages ahead: the token tile (read by the
+//     consumers), and the packed weight bytes and block scales, each into the slot of the lane
+//     that expands them (lane-private, so a lane's own vmcnt wait makes them visible to it);
+//   - the expanded fp16 weight tile in a double buffer, written one stage ahead.
+// Per stage kt a producer lane issues the raw loads of stage kt + 2, waits for those of stage
+// kt + 1 and expands stage kt + 1; the consumers multiply stage kt. One barrier per stage.
+//
+// Expansion, forward: a lane owns EPT = BM / 4 consecutive elements of one weight row, all in one
+// block (blocksize >= 64), so it builds the block's 16 products fp16(code[i] * s) once and maps
+// nibbles to them with byte permutes (v_perm_b32 over the products' low- and high-byte planes):
+// no per-element multiply and no LDS lookups. Backward: a lane owns RPT = BM / 32 weight rows x
+// 8 columns, one scale per row; each value is fp16(code[nibble] * s_row) with the 16-entry code
+// table in LDS. Both give exactly the dequant kernel's fp16 values.
 //
 // The contraction may be split over gridDim: slice s of S covers stages [s n / S, (s + 1) n / S)
 // and writes fp32 partial sums; nf4_gemm_reduce adds the slices in order (deterministic), adds
 // the bias and rounds.
-constexpr int kWsThreads = 512;
+#ifndef CM_NF4_CONSUMERS
+#define CM_NF4_CONSUMERS 8
+#endif
+constexpr int kConsumers = CM_NF4_CONSUMERS;  // MFMA wavefronts: 2 x 2 or 4 x 2
+constexpr int kProducers = 4;
+constexpr int kWsThreads = (kConsumers + kProducers) * 64;
 constexpr int kRing = 3;
 constexpr int kWsBN = 128;
 
+// One global_load_lds_dword: lane l's 4 bytes from g land at lds_lane0 + 4 l (wave-uniform base in
+// M0); issued like gemm::dma16.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma4(const void* g, void* lds_lane0) {
+  const uint32_t m0v = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((cm::gemm::lds_ptr_t)lds_lane0));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(m0v), "v"(g)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// The 16 products fp16(code[i] * s) as byte planes: lo[q] holds the low bytes of products
+// 4q .. 4q + 3, hi[q] their high bytes.
+struct ProductPlanes {
+  uint32_t lo[4], hi[4];
+  __device__ __forceinline__ void build(const float (&code)[16], float s) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t d0 = pack2(code[4 * q] * s, code[4 * q + 1] * s);
+      const uint32_t d1 = pack2(code[4 * q + 2] * s, code[4 * q + 3] * s);
+      lo[q] = __builtin_amdgcn_perm(d1, d0, 0x06040200u);
+      hi[q] = __builtin_amdgcn_perm(d1, d0, 0x07050301u);
+    }
+  }
+  // x: four nibble values, one per byte -> (low bytes, high bytes) of their products
+  __device__ __forceinline__ void lookup(uint32_t x, uint32_t& l, uint32_t& h) const {
+    const uint32_t sel = x & 0x07070707u;
+    // 0xff in the bytes whose nibble is >= 8 (selector 0x0d gives 0xff, 0x0c gives 0x00)
+    const uint32_t msk = __builtin_amdgcn_perm(0u, 0u, ((x >> 3) & 0x01010101u) | 0x0c0c0c0cu);
+    const uint32_t l0 = __builtin_amdgcn_perm(lo[1], lo[0], sel);
+    const uint32_t l1 = __builtin_amdgcn_perm(lo[3], lo[2], sel);
+    const uint32_t h0 = __builtin_amdgcn_perm(hi[1], hi[0], sel);
+    const uint32_t h1 = __builtin_amdgcn_perm(hi[3], hi[2], sel);
+    l = (l1 & msk) | (l0 & ~msk);
+    h = (h1 & msk) | (h0 & ~msk);
+  }
+  // one packed word (elements 2b in the high nibble, 2b + 1 in the low nibble of byte b) ->
+  // its 8 fp16 values in element order, as 4 dwords
+  __device__ __forceinline__ uint4 expand(uint32_t w) const {
+    uint32_t le, he, lo_, ho;
+    lookup((w >> 4) & 0x0f0f0f0fu, le, he);  // elements 0, 2, 4, 6
+    lookup(w & 0x0f0f0f0fu, lo_, ho);        // elements 1, 3, 5, 7
+    const uint32_t e02 = __builtin_amdgcn_perm(he, le, 0x05010400u);  // e0 | e2 << 16
+    const uint32_t e46 = __builtin_amdgcn_perm(he, le, 0x07030602u);
+    const uint32_t o13 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e1 | e3 << 16
+    const uint32_t o57 = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);
+    return make_uint4(__builtin_amdgcn_perm(o13, e02, 0x05040100u),   // e0 | e1 << 16
+                      __builtin_amdgcn_perm(o13, e02, 0x07060302u),   // e2 | e3 << 16
+                      __builtin_amdgcn_perm(o57, e46, 0x05040100u),
+                      __builtin_amdgcn_perm(o57, e46, 0x07060302u));
+  }
+};
+
 template <int BM, bool TRANS>
-__global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
+struct V3Layout {
+  static constexpr int kEPT = BM / 4;                 // forward: elements per lane
+  static constexpr int kTPR = kBK / kEPT;             // forward: lanes per weight row
+  static constexpr int kRPT = BM / 32;                // backward: weight rows per lane
+  static constexpr int kNG = kBK / kRPT;              // backward: lanes along the contraction
+  static constexpr int kA16 = BM * 8;                 // uint4 of an expanded weight tile
+  static constexpr int kBt = kWsBN * 8;               // uint4 of a token tile
+  static constexpr int kPk = TRANS ? kRPT * 64 : (kEPT / 32) * 256;  // uint4 of packed bytes
+  static constexpr int kSc = 64;                      // uint4 of block scales (1 KB)
+  static constexpr int kSlot = kBt + kPk + kSc;
+  // direct-to-LDS instructions a producer lane issues per stage
+  static constexpr int kIssue = 4 + (TRANS ? kRPT : kEPT / 32) + 1;
+};
+
+template <int BM, bool TRANS>
+__global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_v3(const Args args) {
   constexpr int BN = kWsBN;
   using L = LdsRows<kBK>;
+  using Y = V3Layout<BM, TRANS>;
   constexpr int kRC = L::kRC;
-  constexpr int kSlot = (BM + BN) * kRC;  // uint4 per ring slot
-  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int WM = kConsumers / 2, WN = 2;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int KS = kBK / 16;  // MFMA substeps per stage
+  constexpr int KS = kBK / 16;
   using TB = DmaTile<BN, 4, kBK>;
-  using Loader = typename std::conditional<TRANS, BwdLoader<BM>, FwdLoader<BM>>::type;
 
-  __shared__ uint4 ring[kRing * kSlot];
+  __shared__ uint4 a16[2 * Y::kA16];
+  __shared__ uint4 raw[kRing * Y::kSlot];
   __shared__ float s_code[kMaxW][16];
-  __shared__ float s_code2[kMaxW][256];
-  __shared__ float s_off[kMaxW];
 
   const int tid = threadIdx.x;
   const int lane = tid % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / cm::kWave);
-  const bool producer = wave >= 4;
-  const int ptid = tid - 4 * cm::kWave;  // producer lane index 0..255
-  const int nested = args.nested;
+  const bool producer = wave >= kConsumers;
+  const int p = tid - kConsumers * cm::kWave;  // producer lane 0..255
 
   if (producer) {
-    for (int i = 0; i < args.n_w; ++i) {
-      if (ptid < 16) s_code[i][ptid] = args.w[i].code[ptid];
-      if (nested) {
-        s_code2[i][ptid] = args.w[i].code2[ptid];
-        if (ptid == 0) s_off[i] = *args.w[i].offset;
-      } else if (ptid == 0) {
-        s_off[i] = 0.0f;
-      }
-    }
+    for (int i = 0; i < args.n_w; ++i)
+      if (p < 16) s_code[i][p] = args.w[i].code[p];
   }
 
-  // workgroup -> (slice, weight-side tile, token tile); consecutive ids share the slice and the
-  // weight tile (XCD-aware when the grid is a multiple of 8)
   int bid = blockIdx.x;
   if (args.remap) {
     const int per = gridDim.x / 8;
@@ -516,74 +594,141 @@ __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
   const int kb = static_cast<int>(static_cast<int64_t>(slice) * n_all / args.split);
   const int ke = static_cast<int>(static_cast<int64_t>(slice + 1) * n_all / args.split);
   const int n_loc = ke - kb;
-
-  auto stage_w = [&](int kt) {
-    if constexpr (!TRANS) {
-      return wf;
-    } else {
-      int i = 0;
-      while (i + 1 < args.n_w && kt >= args.w[i + 1].first) ++i;
-      return i;
-    }
-  };
-  auto stage_k = [&](int kt, int wi) { return TRANS ? (kt - args.w[wi].first) * kBK : kt * kBK; };
+  const int cols = args.cols;
 
   __syncthreads();  // the code tables
 
   if (producer) {
-    const int pwave = wave - 4;
-    Loader ld;
-    ld.init(ptid);
+    const int pw = wave - kConsumers;
     TB lb;
-    auto load_a = [&](int kt) {
-      const int wi = stage_w(kt), kc = stage_k(kt, wi);
+    float code[16];
+    if constexpr (!TRANS) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) code[i] = s_code[wf][i];
+    }
+    // forward lane: weight row a0 + row, elements part * EPT .. + EPT of the stage
+    const int row = p / Y::kTPR, part = p % Y::kTPR;
+    // backward lane: weight rows ng * RPT .. + RPT of the stage, columns a0 + kw * 8 .. + 8
+    const int ng = p % Y::kNG, kw = p / Y::kNG;
+    auto stage_w = [&](int kt) {
+      int i = 0;
       if constexpr (TRANS) {
-        ld.load(args.w[wi], nested, args.cols, kc, a0);
+        while (i + 1 < args.n_w && kt >= args.w[i + 1].first) ++i;
       } else {
-        ld.load(args.w[wi], nested, args.cols, a0, kc);
+        i = wf;
       }
+      return i;
     };
-    auto produce = [&](int kt, uint4* slot) {
-      const int wi = stage_w(kt), kc = stage_k(kt, wi);
-      ld.store(slot, s_code[wi], s_code2[wi], s_off[wi], nested);
+    auto issue = [&](int kt, uint4* slot) {
+      const int wi = stage_w(kt);
+      const WeightDev& w = args.w[wi];
+      const int kc = TRANS ? (kt - w.first) * kBK : kt * kBK;
       RowMajor src;
       if constexpr (TRANS) {
-        src.p = args.w[wi].g;
-        src.ld = args.w[wi].ldg;
-        src.k_len = args.w[wi].rows;
+        src.p = w.g;
+        src.ld = w.ldg;
+        src.k_len = w.rows;
       } else {
         src.p = args.x;
         src.ld = args.ldx;
-        src.k_len = args.cols;
+        src.k_len = cols;
       }
       src.rows = args.m;
-      lb.init(src, pwave, lane);
+      lb.init(src, pw, lane);
       const bool inside = src.tile_inside(m0, BN, kc);
 #pragma unroll
-      for (int q = 0; q < TB::kPer; ++q) lb.issue(src, m0, kc, slot + BM * kRC, pwave, q, inside);
-    };
-    // prologue: stages 0 .. kRing - 2, and the packed bytes of stage kRing - 1 in registers
+      for (int q = 0; q < TB::kPer; ++q) lb.issue(src, m0, kc, slot, pw, q, inside);
+      const char* pk = reinterpret_cast<const char*>(w.packed);
+      uint4* pk_lds = slot + Y::kBt;
+      uint4* sc_lds = pk_lds + Y::kPk;
+      if constexpr (!TRANS) {
+        const int64_t e0 = static_cast<int64_t>(a0 + row) * cols + kc + part * Y::kEPT;
 #pragma unroll
-    for (int j = 0; j < kRing - 1; ++j) {
-      if (j < n_loc) {
-        load_a(kb + j);
-        cm::gemm::wait_vmcnt<0>();
-        produce(kb + j, ring + j * kSlot);
+        for (int i = 0; i < Y::kEPT / 32; ++i)
+          cm::gemm::dma16(pk + e0 / 2 + 16 * i, pk_lds + i * 256 + pw * 64);
+        const int64_t cb = (kc + part * Y::kEPT) >> w.bs_shift;
+        dma4(w.smap + cb * w.rows + a0 + row, reinterpret_cast<float*>(sc_lds) + pw * 64);
+      } else {
+#pragma unroll
+        for (int r = 0; r < Y::kRPT; ++r) {
+          const int64_t e0 = static_cast<int64_t>(kc + ng * Y::kRPT + r) * cols + a0 + kw * 8;
+          dma4(pk + e0 / 2, reinterpret_cast<uint32_t*>(pk_lds) + r * 256 + pw * 64);
+        }
+        // the wave's 64 weight columns lie in one block: its scales of the stage's 64 rows
+        const int64_t cb = static_cast<int64_t>(a0 + pw * (BM / 4)) >> w.bs_shift;
+        if (lane < 16) cm::gemm::dma16(w.smap + cb * w.rows + kc + lane * 4, sc_lds + pw * 16);
       }
+    };
+    auto expand = [&](int kt, const uint4* slot, uint4* dst) {
+      const uint4* pk_lds = slot + Y::kBt;
+      const uint4* sc_lds = pk_lds + Y::kPk;
+      if constexpr (!TRANS) {
+        const float s = reinterpret_cast<const float*>(sc_lds)[p];
+        ProductPlanes pl;
+        pl.build(code, s);
+#pragma unroll
+        for (int i = 0; i < Y::kEPT / 32; ++i) {
+          const uint4 v = pk_lds[i * 256 + p];
+          const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int lc = part * (Y::kEPT / 8) + i * 4 + q;
+            dst[row * kRC + (lc ^ L::swz(row))] = pl.expand(wd[q]);
+          }
+        }
+      } else {
+        const int wi = stage_w(kt);
+        const float* cd = s_code[wi];
+        const uint32_t* pk32 = reinterpret_cast<const uint32_t*>(pk_lds);
+        const float* scf = reinterpret_cast<const float*>(sc_lds) + pw * 64 + ng * Y::kRPT;
+        uint32_t wd[Y::kRPT];
+        float s[Y::kRPT];
+#pragma unroll
+        for (int r = 0; r < Y::kRPT; ++r) {
+          wd[r] = pk32[r * 256 + p];
+          s[r] = scf[r];
+        }
+        const int ncol = ng * Y::kRPT;
+        char* base = reinterpret_cast<char*>(dst);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float v[Y::kRPT];
+#pragma unroll
+          for (int r = 0; r < Y::kRPT; ++r) {
+            const uint32_t byte = (wd[r] >> (8 * (j / 2))) & 0xffu;
+            v[r] = cd[(j % 2 == 0) ? (byte >> 4) : (byte & 0xfu)] * s[r];
+          }
+          const int kk = kw * 8 + j;
+          char* d = base + (kk * kRC + ((ncol / 8) ^ L::swz(kk))) * 16 + (ncol % 8) * 2;
+          if constexpr (Y::kRPT == 8) {
+            *reinterpret_cast<uint4*>(d) = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]),
+                                                      pack2(v[4], v[5]), pack2(v[6], v[7]));
+          } else {
+            *reinterpret_cast<uint2*>(d) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+          }
+        }
+      }
+    };
+    // prologue: raw stages 0 and 1 in flight, stage 0 expanded
+    issue(kb, raw);
+    if (1 < n_loc) {
+      issue(kb + 1, raw + Y::kSlot);
+      cm::gemm::wait_vmcnt<Y::kIssue>();
+    } else {
+      cm::gemm::wait_vmcnt<0>();
     }
-    if (kRing - 1 < n_loc) load_a(kb + kRing - 1);
-    cm::gemm::wait_vmcnt<0>();
+    expand(kb, raw, a16);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     cm::gemm::lds_barrier();
     for (int kt = 0; kt < n_loc; ++kt) {
-      const int j = kt + kRing - 1;
-      // the token tile of stage kt + 1 (issued one iteration ago) and the packed bytes of stage
-      // j have landed
-      cm::gemm::wait_vmcnt<0>();
-      if (j < n_loc) {
-        produce(kb + j, ring + (j % kRing) * kSlot);
-        if (j + 1 < n_loc) load_a(kb + j + 1);
+      if (kt + 2 < n_loc) {
+        issue(kb + kt + 2, raw + ((kt + 2) % kRing) * Y::kSlot);
+        cm::gemm::wait_vmcnt<Y::kIssue>();  // the raw data of stage kt + 1 has landed
+      } else {
+        cm::gemm::wait_vmcnt<0>();
       }
+      if (kt + 1 < n_loc)
+        expand(kb + kt + 1, raw + ((kt + 1) % kRing) * Y::kSlot, a16 + ((kt + 1) & 1) * Y::kA16);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // this lane's LDS writes have landed
       cm::gemm::lds_barrier();
     }
@@ -591,7 +736,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
   }
 
   // consumers
-  const int wm = wave / 2, wn = wave % 2;
+  const int wm = wave / WN, wn = wave % WN;
   floatx16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -599,11 +744,11 @@ __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  cm::gemm::lds_barrier();  // the prologue's stages are in the ring
+  cm::gemm::lds_barrier();  // stage 0 is in place
   const int arow = wm * WTM + lane % 32, brow = wn * WTN + lane % 32;
   for (int kt = 0; kt < n_loc; ++kt) {
-    const uint4* As = ring + (kt % kRing) * kSlot;
-    const uint4* Bs = As + BM * kRC;
+    const uint4* As = a16 + (kt & 1) * Y::kA16;
+    const uint4* Bs = raw + (kt % kRing) * Y::kSlot;
     half8 af[2][TM], bf[2][TN];
     auto read = [&](int ks, int b) {
       const int ch = ks * 2 + lane / 32;
@@ -627,7 +772,9 @@ __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
     cm::gemm::lds_barrier();
   }
 
-  // epilogue: as nf4_gemm_kernel's, or fp32 partials of this slice
+  // epilogue: lane holds C[a][t] for tokens t = m0 + wn * WTN + j * 32 + lane % 32 and weight-side
+  // rows a = a0 + wm * WTM + i * 32 + (e / 4) * 8 + (lane / 32) * 4 + e % 4; a split writes fp32
+  // partials of its slice
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int t = m0 + wn * WTN + j * 32 + lane % 32;
@@ -672,6 +819,19 @@ __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_ws(const Args args) {
       }
     }
   }
+}
+
+// Block scales as an fp32 map, transposed: smap[c][r] = the scale of the block that holds
+// element (r, c * blocksize) (cols a multiple of the blocksize, so a block never crosses rows).
+__global__ __launch_bounds__(256) void nf4_scale_map_kernel(WeightDev w, int nested, int cols,
+                                                             float* __restrict__ smap) {
+  const int64_t nb_row = cols >> w.bs_shift;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // = c * rows + r
+  if (i >= nb_row * w.rows) return;
+  const int64_t c = i / w.rows, r = i % w.rows;
+  const int64_t blk = r * nb_row + c;
+  const ScaleRaw raw = load_scale(w, nested, blk << w.bs_shift);
+  smap[i] = nested ? block_scale(1, w.code2[raw.q8], raw.a2, *w.offset, 0.0f) : raw.a2;
 }
 
 // Sum of the split's fp32 partials in slice order, plus the bias, rounded to fp16 (and widened
@@ -753,6 +913,8 @@ int setup(const cm_nf4_weight* w, int n_w, int64_t m, Args& a) {
     if (a.nested) CM_CHECK_ARG(s.code2 && s.absmax2 && s.offset && s.blocksize2 >= 1);
     WeightDev& d = a.w[i];
     d.packed = reinterpret_cast<const uint32_t*>(s.packed);
+    d.smap = s.scale_map;
+    if (d.smap) CM_CHECK_ARG(cm::aligned(d.smap, 16));
     d.absmax = s.absmax;
     d.absmax2 = s.absmax2;
     d.offset = s.offset;
@@ -783,9 +945,9 @@ void pick_tiles(TilesFn tiles, bool allow128, int& bm, int& bn) {
   bn = 64;
 }
 
-// How one call runs: the wavefront-specialized kernel (ws) when the weight-side extent is a
-// multiple of 128, with the contraction split when the tiles alone leave CUs idle; the general
-// kernel otherwise.
+// How one call runs: the wavefront-specialized kernel (ws) when the weights have scale maps and
+// the weight-side extent is a multiple of 128, with the contraction split when the tiles alone
+// leave CUs idle; the general kernel otherwise.
 struct Plan {
   bool ws;
   int bm, bn, split;
@@ -805,7 +967,11 @@ Plan plan_for(const Args& a, bool trans) {
     all256 = all256 && a.w[i].rows % 256 == 0;
   }
   const int extent = trans ? a.cols : static_cast<int>(rows_total);
-  const bool e128 = trans ? a.cols % 128 == 0 : all128;
+  bool maps = true;  // every weight has a scale map with blocks of >= 64 that never cross rows
+  for (int i = 0; i < a.n_w; ++i)
+    maps = maps && a.w[i].smap && a.w[i].bs_shift >= 6 && (a.cols >> a.w[i].bs_shift) > 0 &&
+           a.cols % (1 << a.w[i].bs_shift) == 0;
+  const bool e128 = maps && (trans ? a.cols % 128 == 0 : all128);
   const bool e256 = trans ? a.cols % 256 == 0 : all256;
   p.n_out = trans ? a.cols : (a.n_w == 1 ? a.w[0].rows : 0);
   if (e128) {
@@ -840,7 +1006,7 @@ Plan plan_for(const Args& a, bool trans) {
 
 template <int BM, bool TRANS>
 int launch_ws(const Args& a, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((nf4_gemm_ws<BM, TRANS>), dim3(static_cast<uint32_t>(blocks)),
+  hipLaunchKernelGGL((nf4_gemm_v3<BM, TRANS>), dim3(static_cast<uint32_t>(blocks)),
                      dim3(kWsThreads), 0, stream, a);
   return cm::launch_status();
 }
@@ -916,6 +1082,18 @@ int bwd_args(const cm_nf4_weight* w, int n_w, int64_t m, Args& a) {
 }
 
 }  // namespace
+
+extern "C" int cm_nf4_scale_map(const cm_nf4_weight* w, float* smap, void* stream) {
+  Args a;
+  if (int st = setup(w, 1, 0, a)) return st;
+  CM_CHECK_ARG(smap && cm::aligned(smap, 16) && a.cols % w->blocksize == 0);
+  const int64_t n = static_cast<int64_t>(a.cols / w->blocksize) * a.w[0].rows;
+  CM_CHECK_ARG((n + 255) / 256 < 0x7fffffff);
+  hipLaunchKernelGGL(nf4_scale_map_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), a.w[0], a.nested, a.cols,
+                     smap);
+  return cm::launch_status();
+}
 
 extern "C" int64_t cm_nf4_linear_workspace_bytes(int64_t m, const cm_nf4_weight* w, int n_w,
                                                  int backward) {

@@ -43,18 +43,41 @@ def fused_supported(packed, state):
     return state.absmax.dtype == torch.float32
 
 
-def _descriptor(packed, state):
+def _descriptor(packed, state, scale_map=True):
     """(cm_nf4_weight, tensors it points into that must stay alive for the call)."""
     nested = bool(state.nested)
     s2 = state.state2 if nested else None
     code = _nf4_code(packed.device) if state.code is None else state.code
     offset = _offset_tensor(state.offset, packed.device) if nested else None
+    smap = _scale_map(packed, state) if scale_map else None
     d = _lib.NF4Weight(packed.data_ptr(), state.absmax.data_ptr(), int(nested), code.data_ptr(),
                        _lib.ptr(s2.code if nested else None),
                        _lib.ptr(s2.absmax if nested else None), _lib.ptr(offset),
                        int(state.blocksize), int(s2.blocksize) if nested else 1,
-                       int(state.shape[0]), int(state.shape[1]))
-    return d, (code, offset)
+                       int(state.shape[0]), int(state.shape[1]), _lib.ptr(smap))
+    return d, (code, offset, smap)
+
+
+def _scale_map(packed, state):
+    """The fp32 block scales of a frozen NF4 weight, [cols / blocksize, rows]
+    (cm_nf4_scale_map), computed once per weight version and kept on its QuantState; None when
+    the fused kernels take none (blocksize below 64 or not dividing the columns)."""
+    rows, cols = int(state.shape[0]), int(state.shape[1])
+    bs = int(state.blocksize)
+    if bs < 64 or cols % bs or not packed.is_cuda:
+        return None
+    s2 = state.state2 if state.nested else None
+    key = (packed.data_ptr(), state.absmax.data_ptr(), state.absmax._version,
+           None if s2 is None else (s2.absmax.data_ptr(), s2.absmax._version))
+    cached = getattr(state, "_cm_scale_map", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    smap = torch.empty(rows * cols // bs, dtype=torch.float32, device=packed.device)
+    d, keep = _descriptor(packed, state, scale_map=False)
+    _lib.call("cm_nf4_scale_map", ctypes.byref(d), smap.data_ptr(), _lib.stream(packed.device))
+    del keep
+    state._cm_scale_map = (key, smap)
+    return smap
 
 
 def _weights(pairs):
@@ -67,10 +90,13 @@ def _weights(pairs):
 
 
 # Products below this many FLOPs take the fused kernel; larger ones expand the weight with the
-# dequant kernel and multiply with torch's GEMM, which is faster there (measured on MI355X at
-# 1276 tokens: k/v projections 22.6 vs 30.0 us forward, 14.9 vs 29.2 us backward; q 30.9 vs
-# 30.3 us; gate+up 173 vs 103 us).
-FUSED_MAX_FLOPS = 2.0e9
+# dequant kernel and multiply with torch's GEMM. The fused kernel expands every weight element
+# once per 128-token tile, at ~4.6 VALU operations per element, as much SIMD time as the
+# tile's matrix-core products; the dequant kernel expands each element once. Measured on MI355X
+# at 1276 tokens (fused vs dequant + GEMM): k/v projections 21 vs 30 us forward, 16 vs 30 us
+# backward; q/o 26 vs 30 us forward, 29 vs 30 us backward; gate+up 135 vs 101 us; down 78 vs
+# 71 us; the MLP input gradient 193 vs 186 us.
+FUSED_MAX_FLOPS = 8.0e9
 
 
 def fused_pays(m, n, k):

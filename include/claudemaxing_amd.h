@@ -294,7 +294,18 @@ typedef struct cm_nf4_weight {
   int blocksize2;
   int64_t rows;            /* out_features */
   int64_t cols;            /* in_features */
+  const float* scale_map;  /* NULL, or the weight's fp32 block scales from cm_nf4_scale_map */
 } cm_nf4_weight;
+
+/* The block scales of one NF4 weight decoded to fp32 (nested: code2[absmax_u8[b]] *
+ * absmax2[b / blocksize2] + offset, multiply then add; else absmax_f32[b]), stored transposed:
+ * smap[c * rows + r] = the scale of the block holding element (r, c * blocksize), for
+ * c < cols / blocksize. cols must be a multiple of blocksize; smap holds rows * cols / blocksize
+ * floats, 16-byte aligned. A frozen weight's map is computed once; with it in cm_nf4_weight the
+ * fused GEMMs read one scale per block instead of decoding the nested absmax in their loops.
+ * No counterpart in the reference (its dequant kernel decodes the nested absmax per call,
+ * solution/nf4.py:35-38). */
+int cm_nf4_scale_map(const cm_nf4_weight* w, float* smap, void* stream);
 
 /* Forward, for n_w (1..3) weights sharing the input:
  *   out_i[t][n] = round(sum_k x[t][k] * fp16(W_i[n][k]) + bias_i[n])     (fp32 sums)

@@ -105,10 +105,10 @@ def test_dtype_codes():
     assert ctypes.sizeof(ctypes.c_void_p) == 8
 
 
-def _nf4_weight(rows, cols, blocksize=64, nested=1):
+def _nf4_weight(rows, cols, blocksize=64, nested=1, scale_map=None):
     # host-side descriptor with fake, 16-byte aligned addresses: only the argument checks read it
     return _lib.NF4Weight(0x1000, 0x2000, nested, 0x3000, 0x4000, 0x5000, 0x6000, blocksize, 256,
-                          rows, cols)
+                          rows, cols, scale_map)
 
 
 def test_nf4_linear_argument_checks(lib):
@@ -150,9 +150,16 @@ def test_nf4_linear_argument_checks(lib):
     assert bwd(ptrs, lds, 4, ok, 1, 0x40000, 1536, 3, None, 0, None) == INVALID
     # workspace sizes: split contractions need fp32 partials, the gate+up launch does not
     ws = lib.cm_nf4_linear_workspace_bytes
-    assert ws(1276, Arr(_nf4_weight(8960, 1536), _nf4_weight(8960, 1536)), 2, 0) == 0
-    down = Arr(_nf4_weight(1536, 8960))
+    assert ws(1276, Arr(_nf4_weight(8960, 1536, scale_map=0x7000),
+                        _nf4_weight(8960, 1536, scale_map=0x7000)), 2, 0) == 0
+    down = Arr(_nf4_weight(1536, 8960, scale_map=0x7000))
     assert ws(1276, down, 1, 0) == 4 * 2 * 1276 * 1536  # 2 slices of [1276, 1536] fp32
+    assert ws(1276, Arr(_nf4_weight(1536, 8960)), 1, 0) == 0  # no scale map: the general kernel
     assert ws(0, down, 1, 0) == 0 and ws(4, Arr(_nf4_weight(100, 64)), 1, 0) == -1
-    # the C layout of cm_nf4_weight on x86-64: 4 pointers, int + padding, 3 pointers, 2 ints, 2 int64
-    assert _lib.NF4Weight.rows.offset == 64 and ctypes.sizeof(_lib.NF4Weight) == 80
+    # scale map: blocksize must divide the columns; NULL output
+    assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536, 4096)), 0x50000, None) == INVALID
+    assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536)), None, None) == INVALID
+    # the C layout of cm_nf4_weight on x86-64: 4 pointers, int + padding, 3 pointers, 2 ints,
+    # 2 int64, 1 pointer
+    assert _lib.NF4Weight.rows.offset == 64 and _lib.NF4Weight.scale_map.offset == 80
+    assert ctypes.sizeof(_lib.NF4Weight) == 88

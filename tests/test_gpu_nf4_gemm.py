@@ -202,6 +202,24 @@ def test_unsplit_without_workspace(dev, monkeypatch):
     check_product(whole, x16, w16, "unsplit", bias)
 
 
+def test_scale_map_is_the_decoded_absmax(dev):
+    banner("nf4 scale map")
+    from claudemaxing_amd.nf4_linear import _scale_map
+    from oracle import nf4 as O
+
+    for nested in (True, False):
+        packed, state, _ = make_weight(384, 1536, 70, nested)
+        pd, sd = to_dev(packed, state, dev)
+        smap = _scale_map(pd, sd).cpu().view(1536 // 64, 384)
+        kw = {}
+        if nested:
+            kw = dict(code2=state.state2.code.numpy(), absmax2=state.state2.absmax.numpy(),
+                      offset=state.offset.numpy().reshape(()), blocksize2=state.state2.blocksize)
+        ref = O.block_scales(state.absmax.numpy(), nested, **kw).reshape(384, 1536 // 64)
+        assert_bits_equal(smap, torch.from_numpy(ref).t().contiguous(), f"nested={nested}")
+        assert _scale_map(pd, sd) is _scale_map(pd, sd)  # computed once per weight
+
+
 def test_supported_predicate(dev):
     packed, state, _ = make_weight(256, 1536, 40)
     assert fused_supported(*to_dev(packed, state, dev))
