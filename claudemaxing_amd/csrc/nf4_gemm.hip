@@ -476,6 +476,10 @@ constexpr int kProducers = 4;
 constexpr int kWsThreads = (kConsumers + kProducers) * 64;
 constexpr int kRing = 3;
 constexpr int kWsBN = 128;
+#ifndef CM_NF4_WIDE_TOKENS
+#define CM_NF4_WIDE_TOKENS 1
+#endif
+constexpr bool kWideTokens = CM_NF4_WIDE_TOKENS;
 
 // One global_load_lds_dword: lane l's 4 bytes from g land at lds_lane0 + 4 l (wave-uniform base in
 // M0); issued like gemm::dma16.
@@ -533,32 +537,31 @@ struct ProductPlanes {
   }
 };
 
-template <int BM, bool TRANS>
+template <int BM, int BN, bool TRANS>
 struct V3Layout {
   static constexpr int kEPT = BM / 4;                 // forward: elements per lane
   static constexpr int kTPR = kBK / kEPT;             // forward: lanes per weight row
   static constexpr int kRPT = BM / 32;                // backward: weight rows per lane
   static constexpr int kNG = kBK / kRPT;              // backward: lanes along the contraction
   static constexpr int kA16 = BM * 8;                 // uint4 of an expanded weight tile
-  static constexpr int kBt = kWsBN * 8;               // uint4 of a token tile
+  static constexpr int kBt = BN * 8;                  // uint4 of a token tile
   static constexpr int kPk = TRANS ? kRPT * 64 : (kEPT / 32) * 256;  // uint4 of packed bytes
   static constexpr int kSc = 64;                      // uint4 of block scales (1 KB)
   static constexpr int kSlot = kBt + kPk + kSc;
   // direct-to-LDS instructions a producer lane issues per stage
-  static constexpr int kIssue = 4 + (TRANS ? kRPT : kEPT / 32) + 1;
+  static constexpr int kIssue = BN / 32 + (TRANS ? kRPT : kEPT / 32) + 1;
 };
 
-template <int BM, bool TRANS>
+template <int BM, int BN, bool TRANS>
 __global__ __launch_bounds__(kWsThreads, 1) void nf4_gemm_v3(const Args args) {
-  constexpr int BN = kWsBN;
   using L = LdsRows<kBK>;
-  using Y = V3Layout<BM, TRANS>;
+  using Y = V3Layout<BM, BN, TRANS>;
   constexpr int kRC = L::kRC;
-  constexpr int WM = kConsumers / 2, WN = 2;
+  constexpr int WN = BN / 64, WM = kConsumers / WN;  // 64 x 64 wavefront tiles
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int KS = kBK / 16;
-  using TB = DmaTile<BN, 4, kBK>;
+  using TB = DmaTile<BN, kProducers, kBK>;
 
   __shared__ uint4 a16[2 * Y::kA16];
   __shared__ uint4 raw[kRing * Y::kSlot];
@@ -983,6 +986,14 @@ Plan plan_for(const Args& a, bool trans) {
       p.bm = 128;
       p.tiles = extent / p.bm * tb;
     }
+    // 256-token tiles expand each weight element half as often; taken when they still give
+    // most CUs a workgroup
+    const int64_t tb2 = (static_cast<int64_t>(a.m) + 255) / 256;
+    if (kWideTokens && a.m >= 512 && extent / 128 * tb2 >= kCUs * 3 / 4) {
+      p.bm = 128;
+      p.bn = 256;
+      p.tiles = extent / 128 * tb2;
+    }
     const int n_all = trans ? a.n_stages : a.cols / kBK;
     p.split = 1;
     if (p.tiles < 3 * kCUs / 4 && (trans || a.n_w == 1)) {
@@ -1004,9 +1015,9 @@ Plan plan_for(const Args& a, bool trans) {
   return p;
 }
 
-template <int BM, bool TRANS>
+template <int BM, int BN, bool TRANS>
 int launch_ws(const Args& a, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((nf4_gemm_v3<BM, TRANS>), dim3(static_cast<uint32_t>(blocks)),
+  hipLaunchKernelGGL((nf4_gemm_v3<BM, BN, TRANS>), dim3(static_cast<uint32_t>(blocks)),
                      dim3(kWsThreads), 0, stream, a);
   return cm::launch_status();
 }
@@ -1035,11 +1046,14 @@ int run(Args& a, Plan p, bool trans, void* workspace, int64_t ws_bytes, void* ou
   a.n_out = p.n_out;
   int st;
   if (p.ws) {
-    if (trans) {
-      st = p.bm == 256 ? launch_ws<256, true>(a, blocks, s) : launch_ws<128, true>(a, blocks, s);
+    if (p.bn == 256) {
+      st = trans ? launch_ws<128, 256, true>(a, blocks, s) : launch_ws<128, 256, false>(a, blocks, s);
+    } else if (trans) {
+      st = p.bm == 256 ? launch_ws<256, 128, true>(a, blocks, s)
+                       : launch_ws<128, 128, true>(a, blocks, s);
     } else {
-      st = p.bm == 256 ? launch_ws<256, false>(a, blocks, s)
-                       : launch_ws<128, false>(a, blocks, s);
+      st = p.bm == 256 ? launch_ws<256, 128, false>(a, blocks, s)
+                       : launch_ws<128, 128, false>(a, blocks, s);
     }
   } else {
     const int nt = static_cast<int>(blocks);

@@ -91,11 +91,11 @@ def _weights(pairs):
 
 # Products below this many FLOPs take the fused kernel; larger ones expand the weight with the
 # dequant kernel and multiply with torch's GEMM. The fused kernel expands every weight element
-# once per 128-token tile, at ~4.6 VALU operations per element, as much SIMD time as the
-# tile's matrix-core products; the dequant kernel expands each element once. Measured on MI355X
+# once per token tile (256 tokens), at ~4.6 VALU operations per element; the dequant kernel
+# expands each element once, and the GEMM then runs at the library's rate. Measured on MI355X
 # at 1276 tokens (fused vs dequant + GEMM): k/v projections 21 vs 30 us forward, 16 vs 30 us
-# backward; q/o 26 vs 30 us forward, 29 vs 30 us backward; gate+up 135 vs 101 us; down 78 vs
-# 71 us; the MLP input gradient 193 vs 186 us.
+# backward; q/o 26 vs 30 us forward, 30 vs 30 us backward; gate+up 122 vs 101 us; down 78 vs
+# 71 us forward, 90 vs 48 us backward; the MLP input gradient 191 vs 186 us.
 FUSED_MAX_FLOPS = 8.0e9
 
 
