@@ -113,7 +113,11 @@ def make_batch(device, seed=0, batch=4, lo=64, hi=512, vocab=QWEN25_1P5B["vocab_
 
 
 def make_optimizer(model, lr=2e-4):
-    return torch.optim.AdamW(lora_parameters(model), lr=lr)
+    """The optimizer transformers' Trainer builds with its defaults (task/task.yaml sets only the
+    learning rate): `optim="adamw_torch_fused"` (the default for torch >= 2.8), i.e. torch's
+    fused AdamW, betas (0.9, 0.999), eps 1e-8, weight decay 0."""
+    return torch.optim.AdamW(lora_parameters(model), lr=lr, betas=(0.9, 0.999), eps=1e-8,
+                             weight_decay=0.0, fused=True)
 
 
 def train_step(model, opt, scaler, batch, fused=True):
