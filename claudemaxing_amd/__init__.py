@@ -10,6 +10,7 @@ from .attention import patch_qwen2_grouped_sdpa
 from .lm_head_loss import patch_fused_head_loss
 from .lora import patch_peft_lora_4bit
 from .nf4 import patch_bnb_nf4_dequant
+from .qkv import patch_qwen2_fused_qkv
 from .rmsnorm import patch_qwen2_rmsnorm
 from .rope import patch_qwen2_rope
 from .swiglu_recompute import patch_qwen2_mlp_recompute
@@ -28,4 +29,5 @@ def apply():
     patch_qwen2_rope()  # rotary embedding, q and k in one launch
     patch_bnb_nf4_dequant()  # NF4 dequantization (when bitsandbytes is installed)
     patch_peft_lora_4bit()  # LoRA branch with a packed dropout mask (when peft is installed)
+    patch_qwen2_fused_qkv()  # q/k/v of NF4 + LoRA blocks as one fused NF4 GEMM each way
     patch_qwen2_grouped_sdpa()  # causal attention of the packed batch

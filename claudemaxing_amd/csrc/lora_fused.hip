@@ -19,6 +19,7 @@
 // Backward-2, row t, after the caller's base input gradient dxb = gbase @ W (fp16):
 //   gxd = fp16(sum_r ga[r] * fp16(A)[r][k]);
 //   dx  = fp32(dxb[k]) + (keep ? gxd * scale_p : 0)           (the unpack kernel's gradient)
+//   or, without dxb, dx += (keep ? gxd * scale_p : 0)         (a second adapter on the same input)
 //   xd' = fp16(keep ? x16 * scale_p : 0)                       (lora_A's input, rebuilt)
 // The products of two fp16 values are exact in fp32, so the sums differ from a GEMM's only in
 // their order.
@@ -255,13 +256,19 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd2_kernel(
   const int t0 = blockIdx.x * kRows, t_end = min(T, t0 + kRows);
   struct In {
     half8 ga0, ga1, db, xv;
+    float4 d0, d1;  // dx as it is (accumulating)
     uint32_t m;
   };
   auto load = [&](int t, In& in) {
     const int64_t at = static_cast<int64_t>(t) * K + 8 * c;
     in.ga0 = *reinterpret_cast<const half8*>(ga16 + static_cast<int64_t>(t) * kR);
     in.ga1 = *reinterpret_cast<const half8*>(ga16 + static_cast<int64_t>(t) * kR + 8);
-    if (dx) in.db = *reinterpret_cast<const half8*>(dxb + at);
+    if (dx && dxb) {
+      in.db = *reinterpret_cast<const half8*>(dxb + at);
+    } else if (dx) {
+      in.d0 = reinterpret_cast<const float4*>(dx + at)[0];
+      in.d1 = reinterpret_cast<const float4*>(dx + at)[1];
+    }
     in.xv = *reinterpret_cast<const half8*>(x16 + at);
     in.m = bits[static_cast<int64_t>(t) * (K / 8) + c];
   };
@@ -283,11 +290,13 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd2_kernel(
     }
     float o[8];
     half8 xo;
+    const float dold[8] = {cur.d0.x, cur.d0.y, cur.d0.z, cur.d0.w,
+                           cur.d1.x, cur.d1.y, cur.d1.z, cur.d1.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool kept = (cur.m >> i) & 1u;
       const float gl = kept ? static_cast<float>(h16(gxd[i])) * scale_p : 0.0f;
-      o[i] = dx ? static_cast<float>(cur.db[i]) + gl : 0.0f;
+      o[i] = dx ? (dxb ? static_cast<float>(cur.db[i]) : dold[i]) + gl : 0.0f;
       xo[i] = h16(kept ? static_cast<float>(cur.xv[i]) * scale_p : 0.0f);
     }
     if (dx) {
@@ -364,8 +373,8 @@ extern "C" int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const flo
   CM_CHECK_ARG(rank == kR && T >= 0 && K > 0 && K % 8 == 0 && K <= 8 * kThreads);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
-  CM_CHECK_ARG(ga16 && weight_a && x16 && bits && xd16 && (!dx || dxb16));
-  CM_CHECK_ARG((!dx || (aligned16(dxb16) && aligned16(dx))) && aligned16(ga16) &&
+  CM_CHECK_ARG(ga16 && weight_a && x16 && bits && xd16);
+  CM_CHECK_ARG((!dx || ((!dxb16 || aligned16(dxb16)) && aligned16(dx))) && aligned16(ga16) &&
                aligned16(weight_a) && aligned16(x16) && aligned16(xd16));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>((T + kRows - 1) / kRows));

@@ -261,6 +261,8 @@ int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16, 
  *   gxd = fp16(sum_r ga16[t][r] * fp16(weight_a[r][k]))
  *   dx[t][k] = fp32(dxb16[t][k]) + (keep ? gxd * scale_p : 0)     (dx may be NULL: then
  *                                                                   dxb16 is not read)
+ *   with dxb16 NULL and dx given: dx[t][k] += (keep ? gxd * scale_p : 0)   (a second adapter on
+ *                                                                   the same input)
  *   xd16[t][k] = fp16(keep ? x16[t][k] * scale_p : 0)   (lora_A's input rebuilt, the unpack
  *                                                         kernel solution/lora.py:45-57)
  * keep = the bits of the forward. All fp16/fp32 arrays 16-byte aligned.

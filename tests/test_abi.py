@@ -66,9 +66,9 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1532, 1536,
                                  16, 1.05, 2.0, None) == INVALID
     assert lib.cm_lora_fused_bwd1(None, None, None, None, None, 4, 4096, 16, 2.0,
-                                  None, 0, None) == INVALID
+                                  None) == INVALID
     assert lib.cm_lora_fused_bwd2(None, None, None, None, None, None, None, 4, 4096, 16, 1.05,
-                                  None, 0, None) == INVALID
+                                  None) == INVALID
 
 
 def test_empty_inputs_are_no_ops(lib):
