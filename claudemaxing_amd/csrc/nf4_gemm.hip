@@ -986,13 +986,23 @@ Plan plan_for(const Args& a, bool trans) {
       p.bm = 128;
       p.tiles = extent / p.bm * tb;
     }
-    // 256-token tiles expand each weight element half as often; taken when they still give
-    // most CUs a workgroup
+    // 256-token tiles expand each weight element half as often; taken when they, split over the
+    // contraction where that is allowed, still give most CUs a workgroup
     const int64_t tb2 = (static_cast<int64_t>(a.m) + 255) / 256;
-    if (kWideTokens && a.m >= 512 && extent / 128 * tb2 >= kCUs * 3 / 4) {
+    const int64_t tiles2 = extent / 128 * tb2;
+    const bool can_split = trans || a.n_w == 1;
+    const int n_stages_all = trans ? a.n_stages : a.cols / kBK;
+    int64_t sp2 = 1;
+    if (can_split && tiles2 < kCUs * 3 / 4) {
+      sp2 = kCUs / (tiles2 > 0 ? tiles2 : 1);
+      if (sp2 > 8) sp2 = 8;
+      if (sp2 > n_stages_all / 8) sp2 = n_stages_all / 8;
+      if (sp2 < 1) sp2 = 1;
+    }
+    if (kWideTokens && a.m >= 384 && tiles2 * sp2 >= kCUs * 3 / 4) {
       p.bm = 128;
       p.bn = 256;
-      p.tiles = extent / 128 * tb2;
+      p.tiles = tiles2;
     }
     const int n_all = trans ? a.n_stages : a.cols / kBK;
     p.split = 1;

@@ -153,7 +153,7 @@ def test_nf4_linear_argument_checks(lib):
     assert ws(1276, Arr(_nf4_weight(8960, 1536, scale_map=0x7000),
                         _nf4_weight(8960, 1536, scale_map=0x7000)), 2, 0) == 0
     down = Arr(_nf4_weight(1536, 8960, scale_map=0x7000))
-    assert ws(1276, down, 1, 0) == 4 * 2 * 1276 * 1536  # 2 slices of [1276, 1536] fp32
+    assert ws(1276, down, 1, 0) == 4 * 4 * 1276 * 1536  # 4 slices of [1276, 1536] fp32
     assert ws(1276, Arr(_nf4_weight(1536, 8960)), 1, 0) == 0  # no scale map: the general kernel
     assert ws(0, down, 1, 0) == 0 and ws(4, Arr(_nf4_weight(100, 64)), 1, 0) == -1
     # scale map: blocksize must divide the columns; NULL output
