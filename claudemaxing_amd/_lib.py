@@ -72,7 +72,7 @@ SIGNATURES = {
     "cm_attn_fwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _I, _I, _I, _F,
                          _P, _P, _P, _L, _P]),
     "cm_attn_bwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _P, _P, _I, _I,
-                         _I, _I, _F, _P, _I, _P, _P, _I, _P, _L, _P]),
+                         _I, _I, _F, _P, _I, _P, _P, _I, _I, _P, _L, _P]),
     "cm_attn_padded_tokens": (_L, [_P, _I]),
     "cm_lora_fused_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _F, _F, _P]),
     "cm_lora_fused_bwd1": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),

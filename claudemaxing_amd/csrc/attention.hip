@@ -534,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
     const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
     const float* __restrict__ delta, Rows rows, int n_pad, int hpg, float c_log2, float scale,
-    OT* __restrict__ dq) {
+    OT* __restrict__ dq, int tok_major) {
   constexpr int kStage = 2 * kKVTile + kKTTile;
   __shared__ uint4 lds[2][2][kStage];
   const int h = blockIdx.y, g = h / hpg;
@@ -614,7 +614,10 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   }
   cm::gemm::lds_barrier();
   if (pair == 1 || ql >= len) return;
-  OT* row = dq + (static_cast<int64_t>(h) * rows.start[rows.n] + rows.start[r] + ql) * kD;
+  // dq is [H][N][D], or [N][H][D] with tok_major
+  const int64_t tok = rows.start[r] + ql;
+  OT* row = dq + (tok_major ? tok * gridDim.y + h
+                            : static_cast<int64_t>(h) * rows.start[rows.n] + tok) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -623,12 +626,13 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
           cm::from_f32<OT>((acc[dt][e] + xf[(dt * 16 + e) * cm::kWave]) * scale);
 }
 
-// dK, dV = sum of the partials of the query heads of each group, [G][N][D] in the output dtype.
+// dK, dV = sum of the partials of the query heads of each group, [G][N][D] (or [N][G][D]) in the
+// output dtype.
 // Thread (position, 4 values of d) of key/value head blockIdx.y.
 template <typename OT>
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
     const float* __restrict__ dk_part, const float* __restrict__ dv_part, Rows rows, int n_pad,
-    int hpg, OT* __restrict__ dk, OT* __restrict__ dv) {
+    int hpg, OT* __restrict__ dk, OT* __restrict__ dv, int tok_major) {
   const int g = blockIdx.y;
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int pos = i / (kD / 4), d = (i % (kD / 4)) * 4;
@@ -644,7 +648,11 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
     sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
     sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
   }
-  const int64_t o = (static_cast<int64_t>(g) * rows.start[rows.n] + rows.start[r] + local) * kD + d;
+  // dK, dV are [G][N][D], or [N][G][D] with tok_major
+  const int64_t tok = rows.start[r] + local;
+  const int64_t o =
+      (tok_major ? tok * gridDim.y + g : static_cast<int64_t>(g) * rows.start[rows.n] + tok) * kD +
+      d;
   dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
   dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
   dv[o] = cm::from_f32<OT>(sv.x); dv[o + 1] = cm::from_f32<OT>(sv.y);
@@ -755,8 +763,8 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
                            int64_t sv_h, int64_t sv_t, const void* out, const void* dout,
                            const float* lse2, const int64_t* bounds, int n_rows, int H, int G,
                            int head_dim, float scale, void* dq, int dq_dtype, void* dk,
-                           void* dv, int dkv_dtype, void* workspace, int64_t workspace_bytes,
-                           void* stream) {
+                           void* dv, int dkv_dtype, int grads_token_major, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
   Rows rows;
   int64_t n_pad;
   CM_CHECK_ARG(build_rows(bounds, n_rows, rows, n_pad) == 0);
@@ -812,21 +820,21 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   if (dq_dtype == CM_F32) {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(n_blocks, H), dim3(kThreads), 0, s, q16,
                        do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
-                       static_cast<float*>(dq));
+                       static_cast<float*>(dq), grads_token_major ? 1 : 0);
   } else {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(n_blocks, H), dim3(kThreads), 0, s,
                        q16, do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
-                       static_cast<_Float16*>(dq));
+                       static_cast<_Float16*>(dq), grads_token_major ? 1 : 0);
   }
   if (int st = cm::launch_status()) return st;
   if (dkv_dtype == CM_F32) {
     hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(np / 8, G), dim3(256), 0, s,
                        dk_part, dv_part, rows, np, H / G, static_cast<float*>(dk),
-                       static_cast<float*>(dv));
+                       static_cast<float*>(dv), grads_token_major ? 1 : 0);
   } else {
     hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(np / 8, G), dim3(256), 0, s,
                        dk_part, dv_part, rows, np, H / G, static_cast<_Float16*>(dk),
-                       static_cast<_Float16*>(dv));
+                       static_cast<_Float16*>(dv), grads_token_major ? 1 : 0);
   }
   return cm::launch_status();
 }

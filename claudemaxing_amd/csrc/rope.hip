@@ -6,7 +6,8 @@
 //   forward  o1 = x1*c1 - x2*s1,  o2 = x2*c2 + x1*s2
 //   backward o1 = x1*c1 + x2*s2,  o2 = x2*c2 - x1*s1      (the transposed rotation)
 // in fp32, stored in the output dtype. Inputs are strided [B, H, T, D] views (the projection
-// output [B, T, H*D] transposed), outputs contiguous [B, H, T, D].
+// output [B, T, H*D] transposed), outputs contiguous [B, H, T, D] or, for gradients that flow
+// back into the projection, [B, T, H, D] (token-major).
 //
 // One workgroup handles one (batch, token): it stages that token's cos/sin rows in LDS once
 // (fp32), then its lanes walk all heads of q and k in 4-pair groups (16-byte fp32 / 8-byte fp16
@@ -65,7 +66,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(
     const XT* __restrict__ x0, int64_t sb0, int64_t sh0, int64_t st0, int H0,
     OT* __restrict__ out0, const XT* __restrict__ x1, int64_t sb1, int64_t sh1, int64_t st1,
     int H1, OT* __restrict__ out1, const CT* __restrict__ cos, const CT* __restrict__ sin,
-    int64_t cs_b, int64_t cs_t, int T, int D, int backward) {
+    int64_t cs_b, int64_t cs_t, int T, int D, int flags) {
+  const bool backward = flags & 1;
   __shared__ float s_cos[kMaxD];
   __shared__ float s_sin[kMaxD];
   const int t = blockIdx.x;
@@ -97,7 +99,10 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(
       dst = out1;
       H = H1;
     }
-    dst += ((static_cast<int64_t>(b) * H + h) * T + t) * static_cast<int64_t>(D);
+    // outputs [B][H][T][D], or [B][T][H][D] with bit 1 of flags
+    dst += ((flags & 2) ? (static_cast<int64_t>(b) * T + t) * H + h
+                        : (static_cast<int64_t>(b) * H + h) * T + t) *
+           static_cast<int64_t>(D);
     float a[G], c[G], o1[G], o2[G];
     VecN<XT, G>::load(src + p0, a);
     VecN<XT, G>::load(src + half + p0, c);
@@ -122,7 +127,7 @@ template <typename XT, typename OT, typename CT>
 int launch_typed(const void* x0, int64_t sb0, int64_t sh0, int64_t st0, int H0, void* out0,
                  const void* x1, int64_t sb1, int64_t sh1, int64_t st1, int H1, void* out1,
                  const void* cos, const void* sin, int64_t cs_b, int64_t cs_t, int B, int T,
-                 int D, int backward, hipStream_t s) {
+                 int D, int flags, hipStream_t s) {
   dim3 grid(T, B);
   const int half = D / 2;
   // 4-pair groups when each group start is a multiple of 4 elements (strides and D allow it).
@@ -137,7 +142,7 @@ int launch_typed(const void* x0, int64_t sb0, int64_t sh0, int64_t st0, int H0, 
                      static_cast<const XT*>(x0), sb0, sh0, st0, H0, static_cast<OT*>(out0),    \
                      static_cast<const XT*>(x1), sb1, sh1, st1, H1, static_cast<OT*>(out1),    \
                      static_cast<const CT*>(cos), static_cast<const CT*>(sin), cs_b, cs_t, T, D, \
-                     backward)
+                     flags)
   if (g4)
     CM_ROPE_LAUNCH(4);
   else
@@ -152,10 +157,11 @@ extern "C" int cm_rope(const void* x0, int x0_dtype, int64_t sb0, int64_t sh0, i
                        int H0, void* out0, int out0_dtype, const void* x1, int x1_dtype,
                        int64_t sb1, int64_t sh1, int64_t st1, int H1, void* out1,
                        int out1_dtype, const void* cos, const void* sin, int cs_dtype,
-                       int64_t cs_b, int64_t cs_t, int B, int T, int D, int backward,
+                       int64_t cs_b, int64_t cs_t, int B, int T, int D, int flags,
                        void* stream) {
   CM_CHECK_ARG(B >= 0 && T >= 0 && H0 >= 0 && H1 >= 0);
   CM_CHECK_ARG(D > 0 && D % 2 == 0 && D <= kMaxD);
+  CM_CHECK_ARG(flags >= 0 && flags <= 3);
   if (B == 0 || T == 0 || H0 + H1 == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff && B <= 65535);
   CM_CHECK_ARG(cos && sin);
@@ -166,20 +172,20 @@ extern "C" int cm_rope(const void* x0, int x0_dtype, int64_t sb0, int64_t sh0, i
   if (H0 > 0 && H1 > 0 && (x0_dtype != x1_dtype || out0_dtype != out1_dtype)) {
     int st = cm_rope(x0, x0_dtype, sb0, sh0, st0, H0, out0, out0_dtype, nullptr, x0_dtype, 0, 0,
                      0, 0, nullptr, out0_dtype, cos, sin, cs_dtype, cs_b, cs_t, B, T, D,
-                     backward, stream);
+                     flags, stream);
     if (st) return st;
     return cm_rope(x1, x1_dtype, sb1, sh1, st1, H1, out1, out1_dtype, nullptr, x1_dtype, 0, 0, 0,
-                   0, nullptr, out1_dtype, cos, sin, cs_dtype, cs_b, cs_t, B, T, D, backward,
+                   0, nullptr, out1_dtype, cos, sin, cs_dtype, cs_b, cs_t, B, T, D, flags,
                    stream);
   }
   if (H0 == 0) {  // single tensor passed in the second slot: move it to the first
     return cm_rope(x1, x1_dtype, sb1, sh1, st1, H1, out1, out1_dtype, nullptr, x1_dtype, 0, 0, 0,
-                   0, nullptr, out1_dtype, cos, sin, cs_dtype, cs_b, cs_t, B, T, D, backward,
+                   0, nullptr, out1_dtype, cos, sin, cs_dtype, cs_b, cs_t, B, T, D, flags,
                    stream);
   }
   CM_FLOAT_SWITCH(x0_dtype, XT, CM_FLOAT_SWITCH(out0_dtype, OT, CM_FLOAT_SWITCH(cs_dtype, CT, {
     return launch_typed<XT, OT, CT>(x0, sb0, sh0, st0, H0, out0, x1, sb1, sh1, st1, H1, out1,
-                                    cos, sin, cs_b, cs_t, B, T, D, backward, s);
+                                    cos, sin, cs_b, cs_t, B, T, D, flags, s);
   })));
   return 0;
 }

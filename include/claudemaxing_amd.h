@@ -91,7 +91,8 @@ int64_t cm_rmsnorm_bwd_partials(int64_t n_rows);
  * by RoPE.forward / RoPE.backward (solution/rope.py:60-76, _rotate 46-57).
  * x_i is [B, H_i, T, D] with element strides (sb_i, sh_i, st_i, 1); cos/sin are [Bc, T, D] with
  * strides (cs_b, cs_t, 1); cs_b = 0 broadcasts one row of positions over the batch.
- * out_i is contiguous [B, H_i, T, D]. With h = D/2:
+ * out_i is contiguous [B, H_i, T, D], or [B, T, H_i, D] (token-major) with bit 1 of flags. With
+ * h = D/2 and bit 0 of flags selecting the backward rotation:
  *   forward:  o[:h] = x1*c1 - x2*s1;  o[h:] = x2*c2 + x1*s2
  *   backward: o[:h] = x1*c1 + x2*s2;  o[h:] = x2*c2 - x1*s1         (fp32 arithmetic)
  * Pass x1 = NULL (H1 = 0) to rotate one tensor. D must be even and <= 512.
@@ -99,7 +100,7 @@ int64_t cm_rmsnorm_bwd_partials(int64_t n_rows);
 int cm_rope(const void* x0, int x0_dtype, int64_t sb0, int64_t sh0, int64_t st0, int H0,
             void* out0, int out0_dtype, const void* x1, int x1_dtype, int64_t sb1, int64_t sh1,
             int64_t st1, int H1, void* out1, int out1_dtype, const void* cos, const void* sin,
-            int cs_dtype, int64_t cs_b, int64_t cs_t, int B, int T, int D, int backward,
+            int cs_dtype, int64_t cs_b, int64_t cs_t, int B, int T, int D, int flags,
             void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
@@ -210,7 +211,9 @@ int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const vo
 
 /* Backward of cm_attn_fwd (the same q, k, v, bounds and scale; out and lse2 as it wrote them;
  * dout fp16 [N][H][D] contiguous). Writes dq [H][N][D] (dq_dtype), dk and dv [G][N][D]
- * (dkv_dtype), contiguous; f32 or f16. dk and dv sum the contributions of the H/G query heads of
+ * (dkv_dtype), contiguous; f32 or f16; with grads_token_major != 0 they are [N][H][D] and
+ * [N][G][D] instead (the layout of the projections the gradients flow back into). dk and dv
+ * sum the contributions of the H/G query heads of
  * each group in a fixed order (no atomics: the same bits on every run). Workspace:
  * cm_attn_workspace_bytes(n_pad, H, G, head_dim, 1) bytes, 256-byte aligned.
  */
@@ -218,8 +221,8 @@ int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const vo
                 int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
                 int64_t sv_h, int64_t sv_t, const void* out, const void* dout, const float* lse2,
                 const int64_t* bounds, int n_rows, int H, int G, int head_dim, float scale,
-                void* dq, int dq_dtype, void* dk, void* dv, int dkv_dtype, void* workspace,
-                int64_t workspace_bytes, void* stream);
+                void* dq, int dq_dtype, void* dk, void* dv, int dkv_dtype,
+                int grads_token_major, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Padded token count of a packed batch: sum over rows of round_up(length, 64); -1 for invalid
  * bounds (not monotone, bounds[0] != 0, n_rows outside 1..128). */
