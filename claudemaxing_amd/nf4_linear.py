@@ -172,7 +172,8 @@ class MatMulNF4(torch.autograd.Function):
     own when None); an optional frozen bias in that dtype. An fp32 x is taken through the fp16
     copy the preceding norm wrote of it when there is one (rmsnorm.fp16_copy_of: the same values
     as x.to(fp16)), else cast. The output is the compute-dtype result, widened to `out_dtype`
-    when that is given; the input gradient is returned in x's dtype.
+    when that is given (an fp32 output of an fp16 product is written in fp32 by the GEMM, without
+    the fp16 rounding); the input gradient is returned in x's dtype.
 
     In fp16 the weight is expanded inside the GEMM each way (cm_nf4_linear_fwd/bwd); otherwise
     it is expanded by the dequant kernel and multiplied by torch."""
@@ -192,6 +193,12 @@ class MatMulNF4(torch.autograd.Function):
         if ctx.fused:
             return nf4_linear_fwd(xc, [(packed, state)], [bias], out_dtype)[0]
         w = dequantize_nf4(packed, state, compute)
+        if out_dtype == torch.float32 and compute != torch.float32 and xc.is_cuda:
+            # the GEMM writes fp32 itself (fp32 sums, no fp16 rounding and no cast launch)
+            x2 = xc.reshape(-1, xc.shape[-1])
+            y = (torch.mm(x2, w.t(), out_dtype=torch.float32) if bias is None else
+                 torch.addmm(bias.float(), x2, w.t(), out_dtype=torch.float32))
+            return y.view(*xc.shape[:-1], w.shape[0])
         return torch.nn.functional.linear(xc, w, bias).to(out_dtype)
 
     @staticmethod
