@@ -24,345 +24,445 @@
 // The products of two fp16 values are exact in fp32, so the sums differ from a GEMM's only in
 // their order.
 //
-// Work split: a workgroup of 256 lanes handles kRows rows; lane c owns the 8 inputs 8c..8c+7
-// (the fp16 adapter weights of its columns stay in registers for all rows) and the outputs
-// c + 256 j. A row's inputs are loaded while the previous row is computed (the rows of a
-// workgroup would otherwise each wait out a full memory latency). The rank-16 reductions over
-// K (or N) are a halving shuffle butterfly per wavefront and a 4-way LDS sum.
+// Work split: a workgroup of 8 wavefronts takes a tile of up to 16 token rows (the host picks
+// fewer rows per tile when that spreads a small batch over more CUs). The rank-16 products run
+// on the matrix cores with fp16 operands and fp32 accumulation, like the GEMMs they replace:
+// the sums over K (or N) as v_mfma_f32_16x16x32_f16 steps of 32, split over the wavefronts and
+// added in a fixed order through the LDS; the expansions back to N (or K) outputs as one
+// v_mfma_f32_16x16x16_f16 per 16 outputs, split over the wavefronts. Operands are assigned to
+// lanes so that each lane's memory accesses are 8 to 32 contiguous bytes, and a wavefront issues
+// all its loads before its first product: a launch costs about one memory round trip plus its
+// stores, the arithmetic being a few dozen matrix instructions per wavefront.
+//
+// 16x16 MFMA tiles: lane l supplies row l % 16 of the left operand and column l % 16 of the right
+// one, both over the k values of lane group g = l / 16 (8 of 32 for 16x16x32, 4 of 16 for
+// 16x16x16), and receives rows 4 g .. 4 g + 3 of column l % 16 of the result. Which 8 of a step's
+// 32 k values a lane group supplies is free as long as both operands agree: here k = 4 g .. 4 g + 3
+// and 16 + 4 g .. 16 + 4 g + 3, so that the 4 lane groups of a row read 64 contiguous bytes per
+// 16-byte access (a wavefront's access then covers 16 runs of 64 bytes; lanes 32 bytes apart
+// would cost the address units a request per lane).
 #include "common.h"
 
 namespace {
 
 #pragma clang fp contract(off)
 
-constexpr int kThreads = 256;
-constexpr int kR = 16;       // LoRA rank
-constexpr int kMaxNJ = 8;    // outputs per lane: N <= 2048
-#ifndef CM_LORA_ROWS
-#define CM_LORA_ROWS 4
-#endif
-constexpr int kRows = CM_LORA_ROWS;  // token rows per workgroup (4: 31.0 ms graphed step; 2: 31.5, 8: 31.8, 16: 33.5)
+constexpr int kR = 16;         // LoRA rank
+constexpr int kWaves = 8;      // wavefronts per workgroup
+constexpr int kThreads = kWaves * cm::kWave;
+constexpr int kTileRows = 16;  // token rows per tile at most (the MFMA tile height)
+constexpr int kMaxK = 2048, kMaxN = 2048;
+constexpr int kCUs = 256;      // MI355X compute units
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float acc4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ _Float16 h16(float v) { return cm::from_f32<_Float16>(v); }
 
-// 16 per-lane partial sums reduced over the workgroup; thread r < 16 returns sum r. Within a
-// wavefront the reduction halves the values it exchanges at each step (lanes l and l ^ 32 swap
-// the halves they do not keep, then l ^ 16, l ^ 8, l ^ 4): 8 + 4 + 2 + 1 shuffles, after which
-// lane l holds rank ((l >> 5) & 1) * 8 + ((l >> 4) & 1) * 4 + ((l >> 3) & 1) * 2 + ((l >> 2) & 1)
-// summed over 16 lanes; two more shuffles finish the quad. The 4 wavefronts meet in LDS.
-__device__ __forceinline__ float block_sum16(float (&p)[kR], float (*red)[kR], int lane,
-                                             int wave) {
-  float q8[8], q4[4], q2[2];
-  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float mine = b5 ? p[8 + i] : p[i], other = b5 ? p[i] : p[8 + i];
-    q8[i] = mine + __shfl_xor(other, 32, cm::kWave);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float mine = b4 ? q8[4 + i] : q8[i], other = b4 ? q8[i] : q8[4 + i];
-    q4[i] = mine + __shfl_xor(other, 16, cm::kWave);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float mine = b3 ? q4[2 + i] : q4[i], other = b3 ? q4[i] : q4[2 + i];
-    q2[i] = mine + __shfl_xor(other, 8, cm::kWave);
-  }
-  float v;
-  {
-    const float mine = b2 ? q2[1] : q2[0], other = b2 ? q2[0] : q2[1];
-    v = mine + __shfl_xor(other, 4, cm::kWave);
-  }
-  v += __shfl_xor(v, 2, cm::kWave);
-  v += __shfl_xor(v, 1, cm::kWave);
-  if ((lane & 3) == 0) red[wave][(b5 ? 8 : 0) + (b4 ? 4 : 0) + (b3 ? 2 : 0) + (b2 ? 1 : 0)] = v;
-  __syncthreads();
-  float s = 0.0f;
-  if (threadIdx.x < kR) s = (red[0][threadIdx.x] + red[1][threadIdx.x]) +
-                            (red[2][threadIdx.x] + red[3][threadIdx.x]);
-  return s;
+__device__ __forceinline__ half8 to_half8(float4 u, float4 v) {
+  half8 h;
+  h[0] = h16(u.x); h[1] = h16(u.y); h[2] = h16(u.z); h[3] = h16(u.w);
+  h[4] = h16(v.x); h[5] = h16(v.y); h[6] = h16(v.z); h[7] = h16(v.w);
+  return h;
 }
 
-// fp16(A)[r][8c .. 8c+7] for r < 16 (zero past K).
-__device__ __forceinline__ void load_a16(const float* A, int K, int c, half8 (&a)[kR]) {
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    if (8 * c < K) {
-      const float4* p = reinterpret_cast<const float4*>(A + static_cast<int64_t>(r) * K + 8 * c);
-      const float4 u = p[0], v = p[1];
-      a[r][0] = h16(u.x); a[r][1] = h16(u.y); a[r][2] = h16(u.z); a[r][3] = h16(u.w);
-      a[r][4] = h16(v.x); a[r][5] = h16(v.y); a[r][6] = h16(v.z); a[r][7] = h16(v.w);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[r][i] = static_cast<_Float16>(0.0f);
-    }
-  }
+__device__ __forceinline__ acc4 mfma_k32(half8 a, half8 b, acc4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ acc4 mfma_k16(half4 a, half4 b, acc4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-// fp16(B)[n][0 .. 15] for the lane's outputs n = c + 256 j (zero past N).
-template <int NJ>
-__device__ __forceinline__ void load_b16(const float* B, int N, int c, _Float16 (&b)[NJ][kR]) {
+// Value i of lane l of the 16x16 tile, summed over the 8 wavefronts' partial tiles in a fixed
+// order.
+__device__ __forceinline__ float sum_waves(const acc4 (*red)[cm::kWave], int l, int i) {
+  float v[kWaves];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int n = c + kThreads * j;
-#pragma unroll
-    for (int q = 0; q < kR / 4; ++q) {
-      const float4 v = n < N ? reinterpret_cast<const float4*>(B + static_cast<int64_t>(n) * kR)[q]
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-      b[j][4 * q] = h16(v.x); b[j][4 * q + 1] = h16(v.y);
-      b[j][4 * q + 2] = h16(v.z); b[j][4 * q + 3] = h16(v.w);
-    }
-  }
+  for (int w = 0; w < kWaves; ++w) v[w] = red[w][l][i];
+  return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
 }
 
-template <int NJ>
+__device__ __forceinline__ int wave_index() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
+}
+
+// Forward. lora_A: a[rows x 16] = xd . fp16(A)^T, step s (inputs 32 s .. 32 s + 31) on wavefront
+// s % 8; lane l brings row l % 16's xd at inputs 32 s + 4 g .. +3 and 32 s + 16 + 4 g .. +3 and
+// fp16(A)[rank l % 16] at the same inputs; the row's 4 lane groups then assemble its 4 mask bytes
+// for lane group 0 to write. lora_B: out^T[16-output tile j x rows] =
+// fp16(B)[tile] . a^T, tile j on wavefront j % 8; lane l gets row l % 16 and the 4 consecutive
+// outputs 16 j + 4 (l / 16) .. +3 (base read 8 bytes, out written 16 bytes at a time).
+// SK and SN bound the steps and tiles per wavefront.
+template <int SK, int SN>
 __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ keep, const float* __restrict__ A,
     const float* __restrict__ B, const _Float16* __restrict__ base, float* __restrict__ out,
-    uint8_t* __restrict__ bits, _Float16* __restrict__ a16, int T, int K, int N,
+    uint8_t* __restrict__ bits, _Float16* __restrict__ a16, int T, int K, int N, int rows,
     float scale_p, float scaling) {
-  __shared__ float red[kThreads / cm::kWave][kR];
-  __shared__ float arow[kR];
-  const int c = threadIdx.x, lane = c % cm::kWave, wave = c / cm::kWave;
-  const bool kok = 8 * c < K;
-  const int t0 = blockIdx.x * kRows, t_end = min(T, t0 + kRows);
-  // the row's inputs, loaded one row ahead of their use
-  struct In {
-    float4 u, v;
-    uint2 kk;
-    _Float16 b[NJ];
-  };
-  auto load = [&](int t, In& in) {
-    if (kok) {
-      const int64_t at = static_cast<int64_t>(t) * K + 8 * c;
-      in.u = reinterpret_cast<const float4*>(x + at)[0];
-      in.v = reinterpret_cast<const float4*>(x + at)[1];
-      in.kk = *reinterpret_cast<const uint2*>(keep + at);
-    }
+  __shared__ acc4 red[kWaves][cm::kWave];
+  const int lane = threadIdx.x % cm::kWave, wave = wave_index();
+  const int r16 = lane % 16, grp = lane / 16;
+  const int t = blockIdx.x * rows + r16;
+  const bool live = r16 < rows && t < T;
+  const int K8 = K / 8, steps = (K + 31) / 32, tiles = (N + 15) / 16;
+  const bool words = K8 % 4 == 0 && (reinterpret_cast<uintptr_t>(bits) & 3) == 0;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 xv[SK][2], av[SK][2];
+  uint32_t kk[SK][2];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = c + kThreads * j;
-      in.b[j] = n < N ? base[static_cast<int64_t>(t) * N + n] : static_cast<_Float16>(0.0f);
-    }
-  };
-  In cur, nxt;
-  load(t0, cur);
-  half8 ar[kR];
-  load_a16(A, K, c, ar);
-  _Float16 br[NJ][kR];
-  load_b16<NJ>(B, N, c, br);
-  for (int t = t0; t < t_end; ++t) {
-    if (t + 1 < t_end) load(t + 1, nxt);
-    float p[kR];
+  for (int i = 0; i < SK; ++i) {
 #pragma unroll
-    for (int r = 0; r < kR; ++r) p[r] = 0.0f;
-    if (kok) {
-      const float xv[8] = {cur.u.x, cur.u.y, cur.u.z, cur.u.w, cur.v.x, cur.v.y, cur.v.z, cur.v.w};
-      float xd[8];
-      uint32_t byte = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool kept = (((i < 4 ? cur.kk.x : cur.kk.y) >> (8 * (i & 3))) & 0xffu) != 0;
-        byte |= static_cast<uint32_t>(kept) << i;
-        xd[i] = static_cast<float>(h16(kept ? xv[i] * scale_p : 0.0f));
+    for (int h = 0; h < 2; ++h) {
+      const int k = 32 * (wave + kWaves * i) + 16 * h + 4 * grp;
+      xv[i][h] = av[i][h] = zero4;
+      kk[i][h] = 0u;
+      if (k < K && live) {
+        const int64_t at = static_cast<int64_t>(t) * K + k;
+        xv[i][h] = *reinterpret_cast<const float4*>(x + at);
+        kk[i][h] = *reinterpret_cast<const uint32_t*>(keep + at);
       }
-      bits[static_cast<int64_t>(t) * (K / 8) + c] = static_cast<uint8_t>(byte);
+      if (k < K) av[i][h] = *reinterpret_cast<const float4*>(A + static_cast<int64_t>(r16) * K + k);
+    }
+  }
+  uint2 bb[SN];  // fp16 base values of this lane's 4 outputs per tile
 #pragma unroll
-      for (int r = 0; r < kR; ++r) {
-        float s = 0.0f;
+  for (int i = 0; i < SN; ++i) {
+    const int n = 16 * (wave + kWaves * i) + 4 * grp;
+    bb[i] = (live && n < N)
+                ? *reinterpret_cast<const uint2*>(base + static_cast<int64_t>(t) * N + n)
+                : make_uint2(0u, 0u);
+  }
+  acc4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += xd[i] * static_cast<float>(ar[r][i]);
-        p[r] = s;
+  for (int i = 0; i < SK; ++i) {
+    const int s = wave + kWaves * i;
+    if (s >= steps) break;
+    const float xs[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                         xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+    half8 xd;
+    uint32_t nib = 0;  // bits 0-3: inputs 32 s + 4 g .., bits 4-7: 32 s + 16 + 4 g ..
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool kept = ((kk[i][e / 4] >> (8 * (e & 3))) & 0xffu) != 0;
+      nib |= static_cast<uint32_t>(kept) << e;
+      xd[e] = h16(kept ? xs[e] * scale_p : 0.0f);
+    }
+    // mask bytes 4 s .. 4 s + 3 of the row: byte 4 s + b holds lane groups 2 (b % 2) and
+    // 2 (b % 2) + 1 of half b / 2
+    const uint32_t n1 = __shfl_xor(nib, 16, cm::kWave), n2 = __shfl_xor(nib, 32, cm::kWave),
+                   n3 = __shfl_xor(nib, 48, cm::kWave);
+    if (grp == 0 && live) {
+      const uint32_t word = (nib & 0xfu) | (n1 & 0xfu) << 4 | (n2 & 0xfu) << 8 |
+                            (n3 & 0xfu) << 12 | (nib >> 4) << 16 | (n1 >> 4) << 20 |
+                            (n2 >> 4) << 24 | (n3 >> 4) << 28;
+      uint8_t* dst = bits + static_cast<int64_t>(t) * K8 + 4 * s;
+      if (words) {
+        *reinterpret_cast<uint32_t*>(dst) = word;
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (4 * s + b < K8) dst[b] = static_cast<uint8_t>(word >> (8 * b));
       }
     }
-    const float s = block_sum16(p, red, lane, wave);
-    if (c < kR) {
-      const _Float16 h = h16(s);
-      a16[static_cast<int64_t>(t) * kR + c] = h;
-      arow[c] = static_cast<float>(h);
+    acc = mfma_k32(xd, to_half8(av[i][0], av[i][1]), acc);
+  }
+  red[wave][lane] = acc;
+  float4 bq[SN];  // fp32 B[16 j + l % 16][4 (l / 16) .. +3]
+#pragma unroll
+  for (int i = 0; i < SN; ++i) {
+    const int n = 16 * (wave + kWaves * i) + r16;
+    bq[i] = zero4;
+    if (n < N) bq[i] = *reinterpret_cast<const float4*>(B + static_cast<int64_t>(n) * kR + 4 * grp);
+  }
+  __syncthreads();
+  // a[row l % 16][ranks 4 (l / 16) .. +3]: a[m][r] is value m % 4 of lane r + 16 (m / 4)
+  half4 ah;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ah[e] = h16(sum_waves(red, 4 * grp + e + 16 * (r16 / 4), r16 % 4));
+  if (wave == 0 && live)
+    *reinterpret_cast<half4*>(a16 + static_cast<int64_t>(t) * kR + 4 * grp) = ah;
+#pragma unroll
+  for (int i = 0; i < SN; ++i) {
+    const int j = wave + kWaves * i;
+    if (j >= tiles) break;
+    half4 bh;
+    bh[0] = h16(bq[i].x); bh[1] = h16(bq[i].y); bh[2] = h16(bq[i].z); bh[3] = h16(bq[i].w);
+    const acc4 o = mfma_k16(bh, ah, acc4{0.f, 0.f, 0.f, 0.f});
+    const int n = 16 * j + 4 * grp;
+    if (live && n < N) {
+      const half4 b4 = __builtin_bit_cast(half4, bb[i]);
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lora = static_cast<float>(h16(static_cast<float>(h16(o[e])) * scaling));
+        r[e] = static_cast<float>(b4[e]) + lora;
+      }
+      *reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * N + n) =
+          make_float4(r[0], r[1], r[2], r[3]);
     }
-    __syncthreads();
-    float av[kR];
-#pragma unroll
-    for (int r = 0; r < kR; ++r) av[r] = arow[r];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = c + kThreads * j;
-      if (n >= N) break;
-      float o = 0.0f;
-#pragma unroll
-      for (int r = 0; r < kR; ++r) o += av[r] * static_cast<float>(br[j][r]);
-      const float lora = static_cast<float>(h16(static_cast<float>(h16(o)) * scaling));
-      out[static_cast<int64_t>(t) * N + n] = static_cast<float>(cur.b[j]) + lora;
-    }
-    __syncthreads();  // red / arow are rewritten by the next row
-    cur = nxt;
   }
 }
 
-template <int NJ>
+// Backward-1. ga[rows x 16] = g . fp16(B), step s (outputs 32 s .. 32 s + 31) on wavefront s % 8;
+// lane l brings row l % 16's gradient at outputs 32 s + 4 g .. +3 and 32 s + 16 + 4 g .. +3
+// (writing gbase and g there) and fp16(B)[those 8 outputs][rank l % 16]. SN bounds the steps per
+// wavefront.
+template <int SN>
 __global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
     const float* __restrict__ grad, const float* __restrict__ B, _Float16* __restrict__ gbase,
-    _Float16* __restrict__ g16, _Float16* __restrict__ ga16, int T, int N, float scaling) {
-  __shared__ float red[kThreads / cm::kWave][kR];
-  const int c = threadIdx.x, lane = c % cm::kWave, wave = c / cm::kWave;
-  const int t0 = blockIdx.x * kRows, t_end = min(T, t0 + kRows);
-  float cur[NJ], nxt[NJ];
-  auto load = [&](int t, float (&g)[NJ]) {
+    _Float16* __restrict__ g16, _Float16* __restrict__ ga16, int T, int N, int rows,
+    float scaling) {
+  __shared__ acc4 red[kWaves][cm::kWave];
+  const int lane = threadIdx.x % cm::kWave, wave = wave_index();
+  const int r16 = lane % 16, grp = lane / 16;
+  const int t = blockIdx.x * rows + r16;
+  const bool live = r16 < rows && t < T;
+  const int steps = (N + 31) / 32;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 gv[SN][2];
+  float bw[SN][8];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = c + kThreads * j;
-      g[j] = n < N ? grad[static_cast<int64_t>(t) * N + n] : 0.0f;
+  for (int i = 0; i < SN; ++i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int n = 32 * (wave + kWaves * i) + 16 * h + 4 * grp;
+      gv[i][h] = zero4;
+      if (n < N && live) gv[i][h] = *reinterpret_cast<const float4*>(grad + static_cast<int64_t>(t) * N + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        bw[i][4 * h + e] = n < N ? B[static_cast<int64_t>(n + e) * kR + r16] : 0.0f;
     }
-  };
-  load(t0, cur);
-  _Float16 br[NJ][kR];
-  load_b16<NJ>(B, N, c, br);
-  for (int t = t0; t < t_end; ++t) {
-    if (t + 1 < t_end) load(t + 1, nxt);
-    float p[kR];
+  }
+  acc4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < kR; ++r) p[r] = 0.0f;
+  for (int i = 0; i < SN; ++i) {
+    const int s = wave + kWaves * i;
+    if (s >= steps) break;
+    const float gs[8] = {gv[i][0].x, gv[i][0].y, gv[i][0].z, gv[i][0].w,
+                         gv[i][1].x, gv[i][1].y, gv[i][1].z, gv[i][1].w};
+    half8 gb, g, bh;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = c + kThreads * j;
-      if (n >= N) break;
-      const int64_t at = static_cast<int64_t>(t) * N + n;
-      const _Float16 gb = h16(cur[j]);
-      const _Float16 g = h16(static_cast<float>(gb) * scaling);
-      gbase[at] = gb;
-      g16[at] = g;
-      const float gf = static_cast<float>(g);
-#pragma unroll
-      for (int r = 0; r < kR; ++r) p[r] += gf * static_cast<float>(br[j][r]);
+    for (int e = 0; e < 8; ++e) {
+      gb[e] = h16(gs[e]);
+      g[e] = h16(static_cast<float>(gb[e]) * scaling);
+      bh[e] = h16(bw[i][e]);
     }
-    const float s = block_sum16(p, red, lane, wave);
-    if (c < kR) ga16[static_cast<int64_t>(t) * kR + c] = h16(s);
-    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) cur[j] = nxt[j];
+    for (int h = 0; h < 2; ++h) {
+      const int n = 32 * s + 16 * h + 4 * grp;
+      if (live && n < N) {
+        const int64_t at = static_cast<int64_t>(t) * N + n;
+        *reinterpret_cast<half4*>(gbase + at) = half4{gb[4 * h], gb[4 * h + 1], gb[4 * h + 2], gb[4 * h + 3]};
+        *reinterpret_cast<half4*>(g16 + at) = half4{g[4 * h], g[4 * h + 1], g[4 * h + 2], g[4 * h + 3]};
+      }
+    }
+    acc = mfma_k32(g, bh, acc);
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    // lane l holds rank l % 16 of rows 4 (l / 16) .. +3
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * grp + e;
+      const int tm = blockIdx.x * rows + m;
+      if (m < rows && tm < T)
+        ga16[static_cast<int64_t>(tm) * kR + r16] = h16(sum_waves(red, lane, e));
+    }
   }
 }
 
+// Backward-2 needs no sum across lanes (each input's gxd is a rank-16 sum), so it runs as a slab:
+// the workgroup's rows x K elements are split into groups of 4 consecutive inputs, group
+// q = threadIdx.x + 512 j being row q / (K / 4), inputs 4 (q % (K / 4)) .. +3. A wavefront's
+// accesses are then single contiguous runs, and all of a lane's loads go out before the
+// workgroup stages fp16(A) and the rows' ga in the LDS. gxd sums the 16 rank products in rank
+// order. J bounds the groups per lane; MODE is 0 without dx, 1 for dx = dxb + term, 2 for
+// dx += term (a compile-time choice: a branch on it between the loads would make the compiler
+// wait for each group's loads in turn).
+template <int J, int MODE>
 __global__ __launch_bounds__(kThreads) void lora_fused_bwd2_kernel(
     const _Float16* __restrict__ dxb, const _Float16* __restrict__ ga16,
     const float* __restrict__ A, const _Float16* __restrict__ x16,
     const uint8_t* __restrict__ bits, float* __restrict__ dx, _Float16* __restrict__ xd16,
-    int T, int K, float scale_p) {
-  const int c = threadIdx.x;
-  if (8 * c >= K) return;  // no barrier below
-  const int t0 = blockIdx.x * kRows, t_end = min(T, t0 + kRows);
-  struct In {
-    half8 ga0, ga1, db, xv;
-    float4 d0, d1;  // dx as it is (accumulating)
-    uint32_t m;
-  };
-  auto load = [&](int t, In& in) {
-    const int64_t at = static_cast<int64_t>(t) * K + 8 * c;
-    in.ga0 = *reinterpret_cast<const half8*>(ga16 + static_cast<int64_t>(t) * kR);
-    in.ga1 = *reinterpret_cast<const half8*>(ga16 + static_cast<int64_t>(t) * kR + 8);
-    if (dx && dxb) {
-      in.db = *reinterpret_cast<const half8*>(dxb + at);
-    } else if (dx) {
-      in.d0 = reinterpret_cast<const float4*>(dx + at)[0];
-      in.d1 = reinterpret_cast<const float4*>(dx + at)[1];
-    }
-    in.xv = *reinterpret_cast<const half8*>(x16 + at);
-    in.m = bits[static_cast<int64_t>(t) * (K / 8) + c];
-  };
-  In cur, nxt;
-  load(t0, cur);
-  half8 ar[kR];
-  load_a16(A, K, c, ar);
-  for (int t = t0; t < t_end; ++t) {
-    if (t + 1 < t_end) load(t + 1, nxt);
-    const int64_t at = static_cast<int64_t>(t) * K + 8 * c;
-    float gxd[8];
+    int T, int K, int rows, float scale_p) {
+  __shared__ half4 s_a[kR * kMaxK / 4];  // fp16(A)[r][4 q .. 4 q + 3] at r * K / 4 + q
+  __shared__ half8 s_g[kTileRows][2];    // ga of the tile's rows
+  const int K4 = K / 4, K8 = K / 8, t0 = blockIdx.x * rows, total = rows * K4;
+  uint4 prior[J];  // the 4 fp16 of dxb in .x/.y, or the 4 fp32 of dx as it is (accumulating)
+  uint2 xq[J];
+  uint32_t mb[J];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) gxd[i] = 0.0f;
+  for (int j = 0; j < J; ++j) {
+    const int q = threadIdx.x + kThreads * j, row = q / K4, kq = q - row * K4;
+    prior[j] = make_uint4(0u, 0u, 0u, 0u);
+    xq[j] = make_uint2(0u, 0u);
+    mb[j] = 0;
+    if (q < total && t0 + row < T) {
+      const int64_t at = static_cast<int64_t>(t0 + row) * K + 4 * kq;
+      if constexpr (MODE == 1) {
+        const uint2 d = *reinterpret_cast<const uint2*>(dxb + at);
+        prior[j].x = d.x;
+        prior[j].y = d.y;
+      } else if constexpr (MODE == 2) {
+        prior[j] = *reinterpret_cast<const uint4*>(dx + at);
+      }
+      xq[j] = *reinterpret_cast<const uint2*>(x16 + at);
+      mb[j] = bits[static_cast<int64_t>(t0 + row) * K8 + kq / 2];
+    }
+  }
+  // fp16(A): 4 K float4, read in order and converted in batches of 8 per lane
+  {
+    constexpr int kBatch = 8;
+    const int units = kR * K4;
+    for (int e0 = threadIdx.x; e0 < units; e0 += kBatch * kThreads) {
+      float4 f[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int e = e0 + b * kThreads;
+        if (e < units) f[b] = reinterpret_cast<const float4*>(A)[e];
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int e = e0 + b * kThreads;
+        if (e < units) s_a[e] = half4{h16(f[b].x), h16(f[b].y), h16(f[b].z), h16(f[b].w)};
+      }
+    }
+  }
+  if (threadIdx.x < 2 * rows) {
+    const int row = threadIdx.x / 2, h = threadIdx.x % 2;
+    s_g[row][h] = t0 + row < T ? *reinterpret_cast<const half8*>(
+                                     ga16 + static_cast<int64_t>(t0 + row) * kR + 8 * h)
+                               : half8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int q = threadIdx.x + kThreads * j, row = q / K4, kq = q - row * K4;
+    if (q >= total || t0 + row >= T) continue;
+    const half8 g0 = s_g[row][0], g1 = s_g[row][1];
+    float gx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      const float g = static_cast<float>(r < 8 ? cur.ga0[r] : cur.ga1[r - 8]);
+      const float g = static_cast<float>(r < 8 ? g0[r] : g1[r - 8]);
+      const half4 a = s_a[r * K4 + kq];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) gxd[i] += g * static_cast<float>(ar[r][i]);
+      for (int e = 0; e < 4; ++e) gx[e] += g * static_cast<float>(a[e]);
     }
-    float o[8];
-    half8 xo;
-    const float dold[8] = {cur.d0.x, cur.d0.y, cur.d0.z, cur.d0.w,
-                           cur.d1.x, cur.d1.y, cur.d1.z, cur.d1.w};
+    const uint32_t nib = (mb[j] >> (4 * (kq & 1))) & 0xfu;
+    const half4 db = __builtin_bit_cast(half4, make_uint2(prior[j].x, prior[j].y));
+    const half4 xv = __builtin_bit_cast(half4, xq[j]);
+    const uint32_t dold[4] = {prior[j].x, prior[j].y, prior[j].z, prior[j].w};
+    float o[4];
+    half4 xo;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool kept = (cur.m >> i) & 1u;
-      const float gl = kept ? static_cast<float>(h16(gxd[i])) * scale_p : 0.0f;
-      o[i] = dx ? (dxb ? static_cast<float>(cur.db[i]) : dold[i]) + gl : 0.0f;
-      xo[i] = h16(kept ? static_cast<float>(cur.xv[i]) * scale_p : 0.0f);
+    for (int e = 0; e < 4; ++e) {
+      const bool kept = (nib >> e) & 1u;
+      const float gl = kept ? static_cast<float>(h16(gx[e])) * scale_p : 0.0f;
+      o[e] = (MODE == 1 ? static_cast<float>(db[e]) : __uint_as_float(dold[e])) + gl;
+      xo[e] = h16(kept ? static_cast<float>(xv[e]) * scale_p : 0.0f);
     }
-    if (dx) {
-      float4* d = reinterpret_cast<float4*>(dx + at);
-      d[0] = make_float4(o[0], o[1], o[2], o[3]);
-      d[1] = make_float4(o[4], o[5], o[6], o[7]);
-    }
-    *reinterpret_cast<half8*>(xd16 + at) = xo;
-    cur = nxt;
+    const int64_t at = static_cast<int64_t>(t0 + row) * K + 4 * kq;
+    if constexpr (MODE != 0)
+      *reinterpret_cast<float4*>(dx + at) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<half4*>(xd16 + at) = xo;
   }
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Per-wavefront bounds: steps of 32 (tiles of 16) over `len` split 8 ways, rounded up to the
+// instantiated sizes.
+int steps_bound(int len) {
+  const int per = ((len + 31) / 32 + kWaves - 1) / kWaves;
+  return per <= 2 ? 2 : per <= 4 ? 4 : per <= 6 ? 6 : 8;
+}
+int tiles_bound(int len) {
+  const int per = ((len + 15) / 16 + kWaves - 1) / kWaves;
+  return per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 12 ? 12 : 16;
+}
+
+// Groups of 4 inputs per lane for a slab of `rows` x `len`, rounded up to the instantiated sizes.
+int groups_bound(int rows, int len) {
+  const int per = (rows * (len / 4) + kThreads - 1) / kThreads;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+}
+
+#ifndef CM_LORA_TILE_ROWS
+#define CM_LORA_TILE_ROWS 0
+#endif
+// Token rows per tile: 16, or fewer when 16-row tiles would leave CUs idle.
+int tile_rows(int64_t T) {
+  if (CM_LORA_TILE_ROWS > 0) return CM_LORA_TILE_ROWS;
+  const int64_t r = (T + kCUs - 1) / kCUs;
+  return static_cast<int>(std::min<int64_t>(kTileRows, std::max<int64_t>(1, r)));
+}
+dim3 tile_grid(int64_t T, int rows) { return dim3(static_cast<unsigned>((T + rows - 1) / rows)); }
 
 }  // namespace
 
-#define CM_LORA_NJ_SWITCH(nj, NJ, ...)           \
-  switch (nj) {                                  \
-    case 1: { constexpr int NJ = 1; __VA_ARGS__; break; } \
-    case 2: { constexpr int NJ = 2; __VA_ARGS__; break; } \
-    case 4: { constexpr int NJ = 4; __VA_ARGS__; break; } \
-    case 6: { constexpr int NJ = 6; __VA_ARGS__; break; } \
-    default: { constexpr int NJ = 8; __VA_ARGS__; break; } \
+#define CM_LORA_SK_SWITCH(v, SK, ...)                     \
+  switch (v) {                                            \
+    case 2: { constexpr int SK = 2; __VA_ARGS__; break; } \
+    case 4: { constexpr int SK = 4; __VA_ARGS__; break; } \
+    case 6: { constexpr int SK = 6; __VA_ARGS__; break; } \
+    default: { constexpr int SK = 8; __VA_ARGS__; break; } \
+  }
+#define CM_LORA_SN_SWITCH(v, SN, ...)                       \
+  switch (v) {                                              \
+    case 2: { constexpr int SN = 2; __VA_ARGS__; break; }   \
+    case 4: { constexpr int SN = 4; __VA_ARGS__; break; }   \
+    case 8: { constexpr int SN = 8; __VA_ARGS__; break; }   \
+    case 12: { constexpr int SN = 12; __VA_ARGS__; break; } \
+    default: { constexpr int SN = 16; __VA_ARGS__; break; } \
   }
 
-namespace {
-int nj_for(int n) {
-  const int nj = (n + kThreads - 1) / kThreads;
-  return nj <= 1 ? 1 : nj <= 2 ? 2 : nj <= 4 ? 4 : nj <= 6 ? 6 : 8;
-}
-}  // namespace
+#define CM_LORA_J_SWITCH(v, J, ...)                        \
+  switch (v) {                                             \
+    case 1: { constexpr int J = 1; __VA_ARGS__; break; }   \
+    case 2: { constexpr int J = 2; __VA_ARGS__; break; }   \
+    case 4: { constexpr int J = 4; __VA_ARGS__; break; }   \
+    case 8: { constexpr int J = 8; __VA_ARGS__; break; }   \
+    default: { constexpr int J = 16; __VA_ARGS__; break; } \
+  }
 
 extern "C" int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a,
                                  const float* weight_b, const void* base16, float* out,
                                  uint8_t* bits, void* a16, int64_t T, int K, int N, int rank,
                                  float scale_p, float scaling, void* stream) {
   CM_CHECK_ARG(rank == kR && T >= 0 && K > 0 && N > 0);
-  CM_CHECK_ARG(K % 8 == 0 && K <= 8 * kThreads && N <= kMaxNJ * kThreads);
+  CM_CHECK_ARG(K % 8 == 0 && N % 8 == 0 && K <= kMaxK && N <= kMaxN);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
   CM_CHECK_ARG(x && keep && weight_a && weight_b && base16 && out && bits && a16);
-  CM_CHECK_ARG(aligned16(x) && (reinterpret_cast<uintptr_t>(keep) & 7) == 0 &&
-               aligned16(weight_a) && aligned16(weight_b));
+  CM_CHECK_ARG(aligned(x, 16) && aligned(keep, 8) && aligned(weight_a, 16) &&
+               aligned(weight_b, 16) && aligned(base16, 8) && aligned(out, 16) && aligned(a16, 8));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((T + kRows - 1) / kRows));
-  CM_LORA_NJ_SWITCH(nj_for(N), NJ, {
-    hipLaunchKernelGGL(lora_fused_fwd_kernel<NJ>, grid, dim3(kThreads), 0, s, x, keep, weight_a,
-                       weight_b, static_cast<const _Float16*>(base16), out, bits,
-                       static_cast<_Float16*>(a16), static_cast<int>(T), K, N, scale_p, scaling);
-  });
+  const int rows = tile_rows(T);
+  CM_LORA_SK_SWITCH(steps_bound(K), SK, CM_LORA_SN_SWITCH(tiles_bound(N), SN, {
+    hipLaunchKernelGGL((lora_fused_fwd_kernel<SK, SN>), tile_grid(T, rows), dim3(kThreads), 0, s,
+                       x, keep, weight_a, weight_b, static_cast<const _Float16*>(base16), out,
+                       bits, static_cast<_Float16*>(a16), static_cast<int>(T), K, N, rows, scale_p,
+                       scaling);
+  }));
   return cm::launch_status();
 }
 
 extern "C" int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16,
                                   void* g16, void* ga16, int64_t T, int N, int rank,
                                   float scaling, void* stream) {
-  CM_CHECK_ARG(rank == kR && T >= 0 && N > 0 && N <= kMaxNJ * kThreads);
+  CM_CHECK_ARG(rank == kR && T >= 0 && N > 0 && N % 8 == 0 && N <= kMaxN);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
-  CM_CHECK_ARG(grad && weight_b && gbase16 && g16 && ga16 && aligned16(weight_b));
+  CM_CHECK_ARG(grad && weight_b && gbase16 && g16 && ga16);
+  CM_CHECK_ARG(aligned(grad, 16) && aligned(weight_b, 4) && aligned(gbase16, 8) &&
+               aligned(g16, 8) && aligned(ga16, 2));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((T + kRows - 1) / kRows));
-  CM_LORA_NJ_SWITCH(nj_for(N), NJ, {
-    hipLaunchKernelGGL(lora_fused_bwd1_kernel<NJ>, grid, dim3(kThreads), 0, s, grad, weight_b,
-                       static_cast<_Float16*>(gbase16), static_cast<_Float16*>(g16),
-                       static_cast<_Float16*>(ga16), static_cast<int>(T), N, scaling);
+  const int rows = tile_rows(T);
+  CM_LORA_SK_SWITCH(steps_bound(N), SN, {
+    hipLaunchKernelGGL(lora_fused_bwd1_kernel<SN>, tile_grid(T, rows), dim3(kThreads), 0, s, grad,
+                       weight_b, static_cast<_Float16*>(gbase16), static_cast<_Float16*>(g16),
+                       static_cast<_Float16*>(ga16), static_cast<int>(T), N, rows, scaling);
   });
   return cm::launch_status();
 }
@@ -370,17 +470,23 @@ extern "C" int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void
 extern "C" int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const float* weight_a,
                                   const void* x16, const uint8_t* bits, float* dx, void* xd16,
                                   int64_t T, int K, int rank, float scale_p, void* stream) {
-  CM_CHECK_ARG(rank == kR && T >= 0 && K > 0 && K % 8 == 0 && K <= 8 * kThreads);
+  CM_CHECK_ARG(rank == kR && T >= 0 && K > 0 && K % 8 == 0 && K <= kMaxK);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
   CM_CHECK_ARG(ga16 && weight_a && x16 && bits && xd16);
-  CM_CHECK_ARG((!dx || ((!dxb16 || aligned16(dxb16)) && aligned16(dx))) && aligned16(ga16) &&
-               aligned16(weight_a) && aligned16(x16) && aligned16(xd16));
+  CM_CHECK_ARG((!dx || ((!dxb16 || aligned(dxb16, 8)) && aligned(dx, 16))) && aligned(ga16, 16) &&
+               aligned(weight_a, 16) && aligned(x16, 8) && aligned(xd16, 8));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((T + kRows - 1) / kRows));
-  hipLaunchKernelGGL(lora_fused_bwd2_kernel, grid, dim3(kThreads), 0, s,
-                     static_cast<const _Float16*>(dxb16), static_cast<const _Float16*>(ga16),
-                     weight_a, static_cast<const _Float16*>(x16), bits, dx,
-                     static_cast<_Float16*>(xd16), static_cast<int>(T), K, scale_p);
+  const int rows = tile_rows(T);
+  const int mode = !dx ? 0 : dxb16 ? 1 : 2;
+  CM_LORA_J_SWITCH(groups_bound(rows, K), J, {
+    const auto kernel = mode == 0   ? lora_fused_bwd2_kernel<J, 0>
+                        : mode == 1 ? lora_fused_bwd2_kernel<J, 1>
+                                    : lora_fused_bwd2_kernel<J, 2>;
+    hipLaunchKernelGGL(kernel, tile_grid(T, rows), dim3(kThreads), 0, s,
+                       static_cast<const _Float16*>(dxb16), static_cast<const _Float16*>(ga16),
+                       weight_a, static_cast<const _Float16*>(x16), bits, dx,
+                       static_cast<_Float16*>(xd16), static_cast<int>(T), K, rows, scale_p);
+  });
   return cm::launch_status();
 }

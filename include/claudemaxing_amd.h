@@ -244,7 +244,9 @@ int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim, int b
  *                                          * scaling))
  * x fp32 [T, K], keep bool/uint8 [T, K] (8-byte aligned), weight_a fp32 [R, K], weight_b fp32
  * [N, R], base16 fp16 [T, N] (the base projection's output), out fp32 [T, N], a16 fp16 [T, R].
- * K a multiple of 8 and <= 2048, N <= 2048. The sums are in fp32 (order differs from a GEMM).
+ * K and N multiples of 8 and <= 2048; x, weight_a, weight_b, out 16-byte aligned, base16 and
+ * a16 8-byte aligned. The rank-16 products run on the matrix cores (fp16 operands, fp32
+ * accumulation, like the GEMMs they replace; the order of the sums differs from theirs).
  */
 int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a,
                       const float* weight_b, const void* base16, float* out, uint8_t* bits,
@@ -255,7 +257,8 @@ int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a
  *   gbase16 = fp16(grad)                    (the gradient of the base projection's output)
  *   g16 = fp16(gbase16 * scaling)           (the gradient of lora_B's output)
  *   ga16[t][r] = fp16(sum_n g16[t][n] * fp16(weight_b[n][r]))
- * grad fp32 [T, N]; outputs fp16 [T, N], [T, N], [T, R].
+ * grad fp32 [T, N]; outputs fp16 [T, N], [T, N], [T, R]. N a multiple of 8 and <= 2048; grad
+ * 16-byte aligned, gbase16 and g16 8-byte aligned.
  */
 int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16, void* g16,
                        void* ga16, int64_t T, int N, int rank, float scaling, void* stream);
@@ -268,7 +271,8 @@ int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16, 
  *                                                                   the same input)
  *   xd16[t][k] = fp16(keep ? x16[t][k] * scale_p : 0)   (lora_A's input rebuilt, the unpack
  *                                                         kernel solution/lora.py:45-57)
- * keep = the bits of the forward. All fp16/fp32 arrays 16-byte aligned.
+ * keep = the bits of the forward. K a multiple of 8 and <= 2048; ga16, weight_a and dx 16-byte
+ * aligned, dxb16, x16 and xd16 8-byte aligned. The 16 rank products are summed in rank order.
  */
 int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const float* weight_a,
                        const void* x16, const uint8_t* bits, float* dx, void* xd16, int64_t T,

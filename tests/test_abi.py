@@ -60,12 +60,17 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_rmsnorm_fwd(None, 1, 4, None, 0, None, 1, None, None, None, None, 1, 2, 8,
                               1e-6, None) == INVALID  # row stride < n_cols
     assert lib.cm_xent_rows(None, 1, 4, None, None, None, None, 1, 8, 0, 1.0, None) == INVALID
-    # fused LoRA adapter: rank must be 16, K a multiple of 8 and <= 2048, N <= 2048
+    # fused LoRA adapter: rank must be 16, K and N multiples of 8 and <= 2048
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1536, 1536,
                                  8, 1.05, 2.0, None) == INVALID
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1532, 1536,
                                  16, 1.05, 2.0, None) == INVALID
     assert lib.cm_lora_fused_bwd1(None, None, None, None, None, 4, 4096, 16, 2.0,
+                                  None) == INVALID
+    # N a multiple of 8 (each lane's vector accesses are all in range or all out)
+    assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1536, 1500,
+                                 16, 1.05, 2.0, None) == INVALID
+    assert lib.cm_lora_fused_bwd1(None, None, None, None, None, 4, 1500, 16, 2.0,
                                   None) == INVALID
     assert lib.cm_lora_fused_bwd2(None, None, None, None, None, None, None, 4, 4096, 16, 1.05,
                                   None) == INVALID
