@@ -41,6 +41,13 @@
 // and 16 + 4 g .. 16 + 4 g + 3, so that the 4 lane groups of a row read 64 contiguous bytes per
 // 16-byte access (a wavefront's access then covers 16 runs of 64 bytes; lanes 32 bytes apart
 // would cost the address units a request per lane).
+//
+// Loads are unconditional, from addresses clamped into the arrays: rows past T (or past the
+// tile, which repeat its last row) and lanes past K or N read real, finite data whose results
+// are never stored, and inputs
+// past K (or N) inside a sum are zeroed by a select after the loads. A load under a branch with a
+// zero default would make the compiler merge the two values at the join, waiting there for the
+// load, which turns one memory round trip into several.
 #include "common.h"
 
 namespace {
@@ -106,31 +113,25 @@ __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
   const bool live = r16 < rows && t < T;
   const int K8 = K / 8, steps = (K + 31) / 32, tiles = (N + 15) / 16;
   const bool words = K8 % 4 == 0 && (reinterpret_cast<uintptr_t>(bits) & 3) == 0;
-  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // lanes past the tile repeat its last row (the same cache lines, no extra traffic)
+  const int64_t tc = min(blockIdx.x * rows + min(r16, rows - 1), T - 1);
   float4 xv[SK][2], av[SK][2];
   uint32_t kk[SK][2];
 #pragma unroll
   for (int i = 0; i < SK; ++i) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int k = 32 * (wave + kWaves * i) + 16 * h + 4 * grp;
-      xv[i][h] = av[i][h] = zero4;
-      kk[i][h] = 0u;
-      if (k < K && live) {
-        const int64_t at = static_cast<int64_t>(t) * K + k;
-        xv[i][h] = *reinterpret_cast<const float4*>(x + at);
-        kk[i][h] = *reinterpret_cast<const uint32_t*>(keep + at);
-      }
-      if (k < K) av[i][h] = *reinterpret_cast<const float4*>(A + static_cast<int64_t>(r16) * K + k);
+      const int k = min(32 * (wave + kWaves * i) + 16 * h + 4 * grp, K - 4);
+      xv[i][h] = *reinterpret_cast<const float4*>(x + tc * K + k);
+      kk[i][h] = *reinterpret_cast<const uint32_t*>(keep + tc * K + k);
+      av[i][h] = *reinterpret_cast<const float4*>(A + static_cast<int64_t>(r16) * K + k);
     }
   }
   uint2 bb[SN];  // fp16 base values of this lane's 4 outputs per tile
 #pragma unroll
   for (int i = 0; i < SN; ++i) {
-    const int n = 16 * (wave + kWaves * i) + 4 * grp;
-    bb[i] = (live && n < N)
-                ? *reinterpret_cast<const uint2*>(base + static_cast<int64_t>(t) * N + n)
-                : make_uint2(0u, 0u);
+    const int n = min(16 * (wave + kWaves * i) + 4 * grp, N - 4);
+    bb[i] = *reinterpret_cast<const uint2*>(base + tc * N + n);
   }
   acc4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -139,13 +140,18 @@ __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
     if (s >= steps) break;
     const float xs[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                          xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
-    half8 xd;
+    const bool in0 = 32 * s + 4 * grp < K, in1 = 32 * s + 16 + 4 * grp < K;
+    half8 xd, ad;
     uint32_t nib = 0;  // bits 0-3: inputs 32 s + 4 g .., bits 4-7: 32 s + 16 + 4 g ..
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const bool kept = ((kk[i][e / 4] >> (8 * (e & 3))) & 0xffu) != 0;
+      const bool in = e < 4 ? in0 : in1;
+      const bool kept = in && ((kk[i][e / 4] >> (8 * (e & 3))) & 0xffu) != 0;
       nib |= static_cast<uint32_t>(kept) << e;
       xd[e] = h16(kept ? xs[e] * scale_p : 0.0f);
+      const float4 a4 = av[i][e / 4];
+      const float ae = (e & 3) == 0 ? a4.x : (e & 3) == 1 ? a4.y : (e & 3) == 2 ? a4.z : a4.w;
+      ad[e] = h16(in ? ae : 0.0f);
     }
     // mask bytes 4 s .. 4 s + 3 of the row: byte 4 s + b holds lane groups 2 (b % 2) and
     // 2 (b % 2) + 1 of half b / 2
@@ -164,15 +170,15 @@ __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
           if (4 * s + b < K8) dst[b] = static_cast<uint8_t>(word >> (8 * b));
       }
     }
-    acc = mfma_k32(xd, to_half8(av[i][0], av[i][1]), acc);
+    acc = mfma_k32(xd, ad, acc);
   }
   red[wave][lane] = acc;
   float4 bq[SN];  // fp32 B[16 j + l % 16][4 (l / 16) .. +3]
 #pragma unroll
   for (int i = 0; i < SN; ++i) {
-    const int n = 16 * (wave + kWaves * i) + r16;
-    bq[i] = zero4;
-    if (n < N) bq[i] = *reinterpret_cast<const float4*>(B + static_cast<int64_t>(n) * kR + 4 * grp);
+    // rows past N only feed outputs past N, which are not stored
+    const int n = min(16 * (wave + kWaves * i) + r16, N - 1);
+    bq[i] = *reinterpret_cast<const float4*>(B + static_cast<int64_t>(n) * kR + 4 * grp);
   }
   __syncthreads();
   // a[row l % 16][ranks 4 (l / 16) .. +3]: a[m][r] is value m % 4 of lane r + 16 (m / 4)
@@ -218,19 +224,18 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
   const int t = blockIdx.x * rows + r16;
   const bool live = r16 < rows && t < T;
   const int steps = (N + 31) / 32;
-  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // lanes past the tile repeat its last row (the same cache lines, no extra traffic)
+  const int64_t tc = min(blockIdx.x * rows + min(r16, rows - 1), T - 1);
   float4 gv[SN][2];
   float bw[SN][8];
 #pragma unroll
   for (int i = 0; i < SN; ++i) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int n = 32 * (wave + kWaves * i) + 16 * h + 4 * grp;
-      gv[i][h] = zero4;
-      if (n < N && live) gv[i][h] = *reinterpret_cast<const float4*>(grad + static_cast<int64_t>(t) * N + n);
+      const int n = min(32 * (wave + kWaves * i) + 16 * h + 4 * grp, N - 4);
+      gv[i][h] = *reinterpret_cast<const float4*>(grad + tc * N + n);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        bw[i][4 * h + e] = n < N ? B[static_cast<int64_t>(n + e) * kR + r16] : 0.0f;
+      for (int e = 0; e < 4; ++e) bw[i][4 * h + e] = B[static_cast<int64_t>(n + e) * kR + r16];
     }
   }
   acc4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -240,12 +245,15 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
     if (s >= steps) break;
     const float gs[8] = {gv[i][0].x, gv[i][0].y, gv[i][0].z, gv[i][0].w,
                          gv[i][1].x, gv[i][1].y, gv[i][1].z, gv[i][1].w};
-    half8 gb, g, bh;
+    const bool in0 = 32 * s + 4 * grp < N, in1 = 32 * s + 16 + 4 * grp < N;
+    half8 gb, g, gm, bh;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
+      const bool in = e < 4 ? in0 : in1;
       gb[e] = h16(gs[e]);
       g[e] = h16(static_cast<float>(gb[e]) * scaling);
-      bh[e] = h16(bw[i][e]);
+      gm[e] = in ? g[e] : static_cast<_Float16>(0.0f);
+      bh[e] = h16(in ? bw[i][e] : 0.0f);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -256,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
         *reinterpret_cast<half4*>(g16 + at) = half4{g[4 * h], g[4 * h + 1], g[4 * h + 2], g[4 * h + 3]};
       }
     }
-    acc = mfma_k32(g, bh, acc);
+    acc = mfma_k32(gm, bh, acc);
   }
   red[wave][lane] = acc;
   __syncthreads();
@@ -272,87 +280,76 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
   }
 }
 
-// Backward-2 needs no sum across lanes (each input's gxd is a rank-16 sum), so it runs as a slab:
-// the workgroup's rows x K elements are split into groups of 4 consecutive inputs, group
-// q = threadIdx.x + 512 j being row q / (K / 4), inputs 4 (q % (K / 4)) .. +3. A wavefront's
-// accesses are then single contiguous runs, and all of a lane's loads go out before the
-// workgroup stages fp16(A) and the rows' ga in the LDS. gxd sums the 16 rank products in rank
-// order. J bounds the groups per lane; MODE is 0 without dx, 1 for dx = dxb + term, 2 for
-// dx += term (a compile-time choice: a branch on it between the loads would make the compiler
-// wait for each group's loads in turn).
-template <int J, int MODE>
-__global__ __launch_bounds__(kThreads) void lora_fused_bwd2_kernel(
+// Backward-2 needs no sum across lanes (each input's gxd is a rank-16 sum): lane c of the
+// workgroup owns inputs 4 c .. 4 c + 3 of R token rows. Its 16 columns of fp16(A) (one 16-byte
+// read per rank, contiguous across the lanes) serve all R rows, and every row's dxb (or dx), x16
+// and mask nibble are loaded at once, so a workgroup waits for memory once. gxd sums the 16
+// rank products in rank order. MODE is 0 without dx, 1 for dx = dxb + term, 2 for dx += term (a
+// compile-time choice: a branch on it between the loads would make the compiler wait for each
+// row's loads in turn).
+template <int R, int MODE>
+__global__ __launch_bounds__(kMaxK / 4) void lora_fused_bwd2_kernel(
     const _Float16* __restrict__ dxb, const _Float16* __restrict__ ga16,
     const float* __restrict__ A, const _Float16* __restrict__ x16,
     const uint8_t* __restrict__ bits, float* __restrict__ dx, _Float16* __restrict__ xd16,
-    int T, int K, int rows, float scale_p) {
-  __shared__ half4 s_a[kR * kMaxK / 4];  // fp16(A)[r][4 q .. 4 q + 3] at r * K / 4 + q
-  __shared__ half8 s_g[kTileRows][2];    // ga of the tile's rows
-  const int K4 = K / 4, K8 = K / 8, t0 = blockIdx.x * rows, total = rows * K4;
-  uint4 prior[J];  // the 4 fp16 of dxb in .x/.y, or the 4 fp32 of dx as it is (accumulating)
-  uint2 xq[J];
-  uint32_t mb[J];
+    int T, int K, float scale_p) {
+  __shared__ half8 s_g[R][2];  // ga of the workgroup's rows
+  const int c = threadIdx.x, K4 = K / 4, K8 = K / 8, t0 = blockIdx.x * R;
+  const bool kok = c < K4;
+  const int cc = kok ? c : K4 - 1;  // clamped column quad
+  uint4 prior[R];  // the 4 fp16 of dxb in .x/.y, or the 4 fp32 of dx as it is (accumulating)
+  uint2 xq[R];
+  uint32_t mb[R];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int q = threadIdx.x + kThreads * j, row = q / K4, kq = q - row * K4;
-    prior[j] = make_uint4(0u, 0u, 0u, 0u);
-    xq[j] = make_uint2(0u, 0u);
-    mb[j] = 0;
-    if (q < total && t0 + row < T) {
-      const int64_t at = static_cast<int64_t>(t0 + row) * K + 4 * kq;
-      if constexpr (MODE == 1) {
-        const uint2 d = *reinterpret_cast<const uint2*>(dxb + at);
-        prior[j].x = d.x;
-        prior[j].y = d.y;
-      } else if constexpr (MODE == 2) {
-        prior[j] = *reinterpret_cast<const uint4*>(dx + at);
-      }
-      xq[j] = *reinterpret_cast<const uint2*>(x16 + at);
-      mb[j] = bits[static_cast<int64_t>(t0 + row) * K8 + kq / 2];
+  for (int i = 0; i < R; ++i) {
+    const int64_t tc = min(t0 + i, T - 1);
+    const int64_t at = tc * K + 4 * cc;
+    if constexpr (MODE == 1) {
+      const uint2 d = *reinterpret_cast<const uint2*>(dxb + at);
+      prior[i] = make_uint4(d.x, d.y, 0u, 0u);
+    } else if constexpr (MODE == 2) {
+      prior[i] = *reinterpret_cast<const uint4*>(dx + at);
+    } else {
+      prior[i] = make_uint4(0u, 0u, 0u, 0u);
     }
+    xq[i] = *reinterpret_cast<const uint2*>(x16 + at);
+    mb[i] = bits[tc * K8 + cc / 2];
   }
-  // fp16(A): 4 K float4, read in order and converted in batches of 8 per lane
-  {
-    constexpr int kBatch = 8;
-    const int units = kR * K4;
-    for (int e0 = threadIdx.x; e0 < units; e0 += kBatch * kThreads) {
-      float4 f[kBatch];
+  float4 ac[kR];  // fp32 A[r][4 c .. 4 c + 3], then its fp16 values
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const int e = e0 + b * kThreads;
-        if (e < units) f[b] = reinterpret_cast<const float4*>(A)[e];
-      }
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const int e = e0 + b * kThreads;
-        if (e < units) s_a[e] = half4{h16(f[b].x), h16(f[b].y), h16(f[b].z), h16(f[b].w)};
-      }
-    }
-  }
-  if (threadIdx.x < 2 * rows) {
-    const int row = threadIdx.x / 2, h = threadIdx.x % 2;
-    s_g[row][h] = t0 + row < T ? *reinterpret_cast<const half8*>(
-                                     ga16 + static_cast<int64_t>(t0 + row) * kR + 8 * h)
-                               : half8{0, 0, 0, 0, 0, 0, 0, 0};
+  for (int r = 0; r < kR; ++r)
+    ac[r] = *reinterpret_cast<const float4*>(A + static_cast<int64_t>(r) * K + 4 * cc);
+  if (threadIdx.x < 2 * R) {
+    const int i = threadIdx.x / 2, h = threadIdx.x % 2;
+    s_g[i][h] = *reinterpret_cast<const half8*>(
+        ga16 + static_cast<int64_t>(min(t0 + i, T - 1)) * kR + 8 * h);
   }
   __syncthreads();
+  if (!kok) return;  // no barrier below
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int q = threadIdx.x + kThreads * j, row = q / K4, kq = q - row * K4;
-    if (q >= total || t0 + row >= T) continue;
-    const half8 g0 = s_g[row][0], g1 = s_g[row][1];
+  for (int r = 0; r < kR; ++r) {
+    ac[r].x = static_cast<float>(h16(ac[r].x));
+    ac[r].y = static_cast<float>(h16(ac[r].y));
+    ac[r].z = static_cast<float>(h16(ac[r].z));
+    ac[r].w = static_cast<float>(h16(ac[r].w));
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (t0 + i >= T) break;
+    const half8 g0 = s_g[i][0], g1 = s_g[i][1];
     float gx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
       const float g = static_cast<float>(r < 8 ? g0[r] : g1[r - 8]);
-      const half4 a = s_a[r * K4 + kq];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) gx[e] += g * static_cast<float>(a[e]);
+      gx[0] += g * ac[r].x;
+      gx[1] += g * ac[r].y;
+      gx[2] += g * ac[r].z;
+      gx[3] += g * ac[r].w;
     }
-    const uint32_t nib = (mb[j] >> (4 * (kq & 1))) & 0xfu;
-    const half4 db = __builtin_bit_cast(half4, make_uint2(prior[j].x, prior[j].y));
-    const half4 xv = __builtin_bit_cast(half4, xq[j]);
-    const uint32_t dold[4] = {prior[j].x, prior[j].y, prior[j].z, prior[j].w};
+    const uint32_t nib = (mb[i] >> (4 * (c & 1))) & 0xfu;
+    const half4 db = __builtin_bit_cast(half4, make_uint2(prior[i].x, prior[i].y));
+    const half4 xv = __builtin_bit_cast(half4, xq[i]);
+    const uint32_t dold[4] = {prior[i].x, prior[i].y, prior[i].z, prior[i].w};
     float o[4];
     half4 xo;
 #pragma unroll
@@ -362,7 +359,7 @@ __global__ __launch_bounds__(kThreads) void lora_fused_bwd2_kernel(
       o[e] = (MODE == 1 ? static_cast<float>(db[e]) : __uint_as_float(dold[e])) + gl;
       xo[e] = h16(kept ? static_cast<float>(xv[e]) * scale_p : 0.0f);
     }
-    const int64_t at = static_cast<int64_t>(t0 + row) * K + 4 * kq;
+    const int64_t at = static_cast<int64_t>(t0 + i) * K + 4 * c;
     if constexpr (MODE != 0)
       *reinterpret_cast<float4*>(dx + at) = make_float4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<half4*>(xd16 + at) = xo;
@@ -382,10 +379,16 @@ int tiles_bound(int len) {
   return per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 12 ? 12 : 16;
 }
 
-// Groups of 4 inputs per lane for a slab of `rows` x `len`, rounded up to the instantiated sizes.
-int groups_bound(int rows, int len) {
-  const int per = (rows * (len / 4) + kThreads - 1) / kThreads;
-  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+#ifndef CM_LORA_QUAD_ROWS
+#define CM_LORA_QUAD_ROWS 0
+#endif
+// Token rows per workgroup of the column-quad kernels: the most (of 1, 2, 4, 8, 16) that still
+// gives the CUs a workgroup each.
+int quad_rows(int64_t T) {
+  if (CM_LORA_QUAD_ROWS > 0) return CM_LORA_QUAD_ROWS;
+  int r = 16;
+  while (r > 1 && (T + r - 1) / r < kCUs) r /= 2;
+  return r;
 }
 
 #ifndef CM_LORA_TILE_ROWS
@@ -477,16 +480,17 @@ extern "C" int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const flo
   CM_CHECK_ARG((!dx || ((!dxb16 || aligned(dxb16, 8)) && aligned(dx, 16))) && aligned(ga16, 16) &&
                aligned(weight_a, 16) && aligned(x16, 8) && aligned(xd16, 8));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int rows = tile_rows(T);
   const int mode = !dx ? 0 : dxb16 ? 1 : 2;
-  CM_LORA_J_SWITCH(groups_bound(rows, K), J, {
-    const auto kernel = mode == 0   ? lora_fused_bwd2_kernel<J, 0>
-                        : mode == 1 ? lora_fused_bwd2_kernel<J, 1>
-                                    : lora_fused_bwd2_kernel<J, 2>;
-    hipLaunchKernelGGL(kernel, tile_grid(T, rows), dim3(kThreads), 0, s,
-                       static_cast<const _Float16*>(dxb16), static_cast<const _Float16*>(ga16),
-                       weight_a, static_cast<const _Float16*>(x16), bits, dx,
-                       static_cast<_Float16*>(xd16), static_cast<int>(T), K, rows, scale_p);
+  const int R = quad_rows(T);
+  const dim3 grid(static_cast<unsigned>((T + R - 1) / R)), block((K / 4 + 63) / 64 * 64);
+  CM_LORA_J_SWITCH(R, RR, {
+    const auto kernel = mode == 0   ? lora_fused_bwd2_kernel<RR, 0>
+                        : mode == 1 ? lora_fused_bwd2_kernel<RR, 1>
+                                    : lora_fused_bwd2_kernel<RR, 2>;
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, static_cast<const _Float16*>(dxb16),
+                       static_cast<const _Float16*>(ga16), weight_a,
+                       static_cast<const _Float16*>(x16), bits, dx, static_cast<_Float16*>(xd16),
+                       static_cast<int>(T), K, scale_p);
   });
   return cm::launch_status();
 }
