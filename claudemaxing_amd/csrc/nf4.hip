@@ -243,6 +243,116 @@ int launch(const uint8_t* packed, const void* absmax, const float* code, const f
 
 }  // namespace
 
+namespace {
+
+// Transposed expansion, fp16 only: out[c][r] = W[r][c] for W [rows, cols], rows a multiple of
+// 64 and cols of 128. A workgroup of 256 lanes expands a 64 x 128 tile through the LDS:
+//  - lane task p = t + 256 j (j < 2) decodes packed word wc = p % 16 (columns 8 wc .. +7 of the
+//    tile, one absmax block since blocksize >= 32) of the rows 2 rp and 2 rp + 1, rp = p / 16,
+//    so a load instruction covers 4 rows x 64 contiguous bytes;
+//  - each of the 8 columns gets the two rows as one 32-bit LDS write; columns are 66 halves
+//    apart, which spreads a wavefront's writes over 32 banks (16 B-aligned columns of 72
+//    halves put them on 4);
+//  - after the barrier, lane task q = t + 256 i writes rows 8 part .. +7 and 32 + 8 part .. +7 of
+//    column q / 4 (part = q % 4), so each store instruction writes 64 contiguous bytes of 16
+//    columns.
+// The values are those of nf4_dequant_vec, bit for bit.
+template <bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
+    const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
+    const float* __restrict__ code, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
+    _Float16* __restrict__ out, int64_t rows, int64_t cols, int unit_shift, int bs2_shift,
+    uint32_t bs2) {
+  constexpr int kTR = 64, kTC = 128, kCol = (kTR + 2) / 2;  // 32-bit words per LDS column
+  __shared__ float s_code[16];
+  __shared__ uint32_t tile[kTC * kCol];  // [column][row pair]
+  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
+  const float offset = NESTED ? *offset_ptr : 0.0f;
+  const int64_t tiles_c = cols / kTC;
+  const int64_t r0 = (blockIdx.x / tiles_c) * kTR, c0 = (blockIdx.x % tiles_c) * kTC;
+  uint32_t word[2][2];
+  int64_t unit[2][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = threadIdx.x + kThreads * j, rp = p / 16, wc = p % 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      unit[j][h] = ((r0 + 2 * rp + h) * cols + c0) / 8 + wc;  // 8 elements per 4-byte unit
+      word[j][h] = __builtin_nontemporal_load(packed + unit[j][h]);
+    }
+  }
+  __syncthreads();  // s_code
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = threadIdx.x + kThreads * j, rp = p / 16, wc = p % 16;
+    uint32_t lo[8], hi[8];  // fp16 bits of the 8 columns, rows 2 rp and 2 rp + 1
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t blk = static_cast<uint32_t>(unit[j][h] >> unit_shift);
+      const float sc = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t byte = (word[j][h] >> (8 * k)) & 0xffu;
+        const uint32_t a = __builtin_bit_cast(uint16_t, cm::from_f32<_Float16>(s_code[byte >> 4] * sc));
+        const uint32_t b = __builtin_bit_cast(uint16_t, cm::from_f32<_Float16>(s_code[byte & 0xfu] * sc));
+        (h ? hi : lo)[2 * k] = a;
+        (h ? hi : lo)[2 * k + 1] = b;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[(8 * wc + e) * kCol + rp] = lo[e] | (hi[e] << 16);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = threadIdx.x + kThreads * i, col = q / 4, part = q % 4;
+    const uint32_t* src = tile + col * kCol;
+    _Float16* dst = out + (c0 + col) * rows + r0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int w0 = 16 * half + 4 * part;  // row pair of row 32 half + 8 part
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = {src[w0], src[w0 + 1], src[w0 + 2], src[w0 + 3]};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + 32 * half + 8 * part));
+    }
+  }
+}
+
+}  // namespace
+
+// Transposed expansion for the MLP backward (no counterpart in the reference: its input
+// gradient multiplies by the expanded weight as stored).
+extern "C" int cm_nf4_dequant_t(const uint8_t* packed, const void* absmax, int nested,
+                                const float* code, const float* code2, const float* absmax2,
+                                const float* offset, void* out, int64_t rows, int64_t cols,
+                                int blocksize, int blocksize2, void* stream) {
+  CM_CHECK_ARG(rows >= 0 && cols >= 0 && rows % 64 == 0 && cols % 128 == 0);
+  if (rows == 0 || cols == 0) return 0;
+  CM_CHECK_ARG(packed && absmax && code && out);
+  CM_CHECK_ARG((reinterpret_cast<uintptr_t>(packed) & 3) == 0 &&
+               (reinterpret_cast<uintptr_t>(out) & 15) == 0);
+  CM_CHECK_ARG(blocksize >= 32 && log2_exact(blocksize) >= 0);
+  CM_CHECK_ARG(rows * cols / blocksize < (int64_t{1} << 31));
+  CM_CHECK_ARG(rows / 64 * (cols / 128) < (int64_t{1} << 31));
+  if (nested) CM_CHECK_ARG(code2 && absmax2 && offset && blocksize2 >= 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int unit_shift = log2_exact(blocksize) - 3;
+  const int bs2_shift = nested ? log2_exact(blocksize2) : 0;
+  const dim3 grid(static_cast<unsigned>(rows / 64 * (cols / 128)));
+  const auto* words = reinterpret_cast<const uint32_t*>(packed);
+  if (nested) {
+    hipLaunchKernelGGL(nf4_dequant_t_kernel<true>, grid, dim3(kThreads), 0, s, words, absmax,
+                       code, code2, absmax2, offset, static_cast<_Float16*>(out), rows, cols,
+                       unit_shift, bs2_shift, static_cast<uint32_t>(blocksize2));
+  } else {
+    hipLaunchKernelGGL(nf4_dequant_t_kernel<false>, grid, dim3(kThreads), 0, s, words, absmax,
+                       code, nullptr, nullptr, nullptr, static_cast<_Float16*>(out), rows, cols,
+                       unit_shift, 0, 1u);
+  }
+  return cm::launch_status();
+}
+
 extern "C" int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested,
                               const float* code, const float* code2, const float* absmax2,
                               const float* offset, void* out, int out_dtype, int64_t n_bytes,

@@ -55,6 +55,15 @@ int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested, const 
                    const float* code2, const float* absmax2, const float* offset, void* out,
                    int out_dtype, int64_t n_bytes, int blocksize, int blocksize2, void* stream);
 
+/* The same expansion written transposed, fp16 only: out[c][r] = W[r][c] for the weight W
+ * [rows, cols] (rows a multiple of 64, cols of 128; packed 4-byte, out 16-byte aligned), the values
+ * bit-identical to cm_nf4_dequant's. No counterpart in the reference: the MLP backward of the
+ * training step takes the gate/up weights this way, so that its input-gradient products
+ * (dgate Wg, dup Wu) read both operands along the contraction. */
+int cm_nf4_dequant_t(const uint8_t* packed, const void* absmax, int nested, const float* code,
+                     const float* code2, const float* absmax2, const float* offset, void* out,
+                     int64_t rows, int64_t cols, int blocksize, int blocksize2, void* stream);
+
 /* ------------------------------------------------------------------------------------------ */
 /* RMSNorm forward, one row per wavefront. Replaces solution/rmsnorm.py:28-47
  * (qwen_rmsnorm_fwd_kernel) as launched by RMSNorm.forward (solution/rmsnorm.py:147-192).

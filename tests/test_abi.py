@@ -54,6 +54,17 @@ def test_argument_checks_run_on_the_host(lib):
                               None, 0, None) == INVALID  # blocksize not a power of two
     assert lib.cm_nf4_dequant(None, None, 1, None, None, None, None, None, 1, 10, 16, 256,
                               None, 0, None) == INVALID  # blocksize below 32
+    # transposed expansion: rows a multiple of 64, columns of 128, blocksize a power of two >= 32
+    assert lib.cm_nf4_dequant_t(None, None, 0, None, None, None, None, None, 100, 128, 64, 1,
+                                None) == INVALID
+    assert lib.cm_nf4_dequant_t(None, None, 0, None, None, None, None, None, 64, 64, 64, 1,
+                                None) == INVALID
+    assert lib.cm_nf4_dequant_t(0x1000, 0x2000, 0, 0x3000, None, None, None, 0x4000, 64, 128, 48,
+                                1, None) == INVALID
+    assert lib.cm_nf4_dequant_t(0x1000, 0x2000, 0, 0x3000, None, None, None, 0x4008, 64, 128, 64,
+                                1, None) == INVALID  # misaligned output
+    assert lib.cm_nf4_dequant_t(None, None, 0, None, None, None, None, None, 0, 128, 64, 1,
+                                None) == 0  # empty
     assert lib.cm_rope(None, 1, 0, 0, 0, 1, None, 1, None, 1, 0, 0, 0, 0, None, 1, None, None,
                        1, 0, 0, 1, 1, 7, 0, None) == INVALID  # odd head_dim
     assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, -1, 1, None) == INVALID

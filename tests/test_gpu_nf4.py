@@ -104,3 +104,48 @@ def test_misaligned_output_takes_the_byte_path(dev):
               sd.offset.reshape(1).data_ptr(), out.data_ptr(), _lib.F16, 16 * 32, 64, 256,
               _lib.stream(dev))
     assert_bits_equal(out.reshape(16, 64), oracle_of(packed, state, torch.float16), "misaligned")
+
+
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("shape", [(8960, 1536), (1536, 8960), (64, 128), (192, 384)])
+def test_transposed_expansion_matches_oracle_bitwise(nested, shape, dev):
+    """cm_nf4_dequant_t (the MLP backward's [in, out] copy of a weight) against the oracle's
+    expansion transposed, bit for bit."""
+    from claudemaxing_amd.nf4 import dequantize_nf4_t
+
+    banner(f"nf4 transposed shape={shape} nested={nested}")
+    w = torch.randn(*shape, generator=torch.Generator().manual_seed(3)) * 0.05
+    w[0, :5] = torch.tensor([0.0, -0.0, 1e-7, 3.0, -2.5])
+    packed, state = quantize_nf4(w, 64, nested)
+    out = dequantize_nf4_t(packed.to(dev), state.to(dev))
+    torch.cuda.synchronize()
+    assert out.shape == (shape[1], shape[0])
+    assert_bits_equal(out, oracle_of(packed, state, torch.float16).t().contiguous(),
+                      f"transposed {shape}")
+
+
+@pytest.mark.parametrize("blocksize,blocksize2", [(32, 256), (128, 100), (4096, 1)])
+def test_transposed_expansion_random_bytes(blocksize, blocksize2, dev):
+    """Every packed byte value and q8 code through the transposed kernel, with power-of-two and
+    other second-level blocksizes."""
+    banner(f"nf4 transposed random bs={blocksize} bs2={blocksize2}")
+    rows, cols = 128, 4096
+    g = torch.Generator().manual_seed(blocksize + blocksize2)
+    n_bytes = rows * cols // 2
+    n_blk = rows * cols // blocksize
+    packed = torch.randint(0, 256, (n_bytes,), dtype=torch.uint8, generator=g)
+    q8 = torch.randint(0, 256, (n_blk,), dtype=torch.uint8, generator=g)
+    absmax2 = torch.rand((n_blk + blocksize2 - 1) // blocksize2, generator=g) + 0.1
+    code2 = torch.from_numpy(O.dynamic_map())
+    code = torch.tensor(O.NF4_TABLE)
+    offset = torch.tensor([0.03125], dtype=torch.float32)
+    out = torch.empty(cols, rows, dtype=torch.float16, device=dev)
+    d = {k: v.to(dev) for k, v in dict(p=packed, q8=q8, a2=absmax2, c2=code2, c=code,
+                                        off=offset).items()}
+    _lib.call("cm_nf4_dequant_t", d["p"].data_ptr(), d["q8"].data_ptr(), 1, d["c"].data_ptr(),
+              d["c2"].data_ptr(), d["a2"].data_ptr(), d["off"].data_ptr(), out.data_ptr(),
+              rows, cols, blocksize, blocksize2, _lib.stream(dev))
+    ref = O.dequant(packed.numpy(), q8.numpy(), nested=True, code2=code2.numpy(),
+                    absmax2=absmax2.numpy(), offset=np.float32(0.03125), blocksize=blocksize,
+                    blocksize2=blocksize2)
+    assert_bits_equal(out, torch.from_numpy(ref).reshape(rows, cols).t().contiguous(), "random")
