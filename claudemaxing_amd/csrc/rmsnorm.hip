@@ -77,10 +77,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
       for (int k = 0; k < VEC; ++k) ss += xv[0][k] * xv[0][k];
     }
   }
+  // the weight's columns, loaded before the row's sum so that both share one memory round trip
+  float wc[kCache][VEC];
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = i * step + lane * VEC;
+      load_v<WT, VEC>(w + c, wc[i], c < n_cols ? min(VEC, n_cols - c) : 0);
+    }
+  }
   ss = cm::wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
   if (lane == 0) rstd[row] = r;
   const bool save_low = low16 != nullptr;
+  const bool any_small = save_low && n_small > 0;  // else the column map is not read at all
   const int n_iter = NV > 0 ? NV : (n_cols + step - 1) / step;
   for (int i = 0; i < n_iter; ++i) {
     const int c = i * step + lane * VEC;
@@ -89,11 +99,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
     float xi[VEC], wv[VEC], o[VEC], nv[VEC];
     if constexpr (NV > 0) {
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) xi[k] = xv[i][k];
+      for (int k = 0; k < VEC; ++k) {
+        xi[k] = xv[i][k];
+        wv[k] = wc[i][k];
+      }
     } else {
       load_v<XT, VEC>(xr + c, xi, cnt);
+      load_v<WT, VEC>(w + c, wv, cnt);
     }
-    load_v<WT, VEC>(w + c, wv, cnt);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
       nv[k] = cm::round_to<XT>(xi[k] * r);  // rounded to the input dtype before the weight
@@ -104,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
       store_v<_Float16, VEC>(low16 + row * static_cast<int64_t>(n_cols) + c, o, cnt);
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
-        if (k < cnt) {
+        if (any_small && k < cnt) {
           const int sl = slot[c + k];
           if (sl >= 0) small16[row * static_cast<int64_t>(n_small) + sl] =
               cm::from_f32<_Float16>(nv[k]);
@@ -156,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_kernel(
         load_v<_Float16, VEC>(lows + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-          const int sl = k < cnt ? slot[c + k] : -1;
+          const int sl = (n_small > 0 && k < cnt) ? slot[c + k] : -1;  // no map: not read
           nv[k] = sl >= 0 ? static_cast<float>(small16[row * static_cast<int64_t>(n_small) + sl])
                           : (k < cnt ? xv[k] / wv[k] : 0.0f);
           gv[k] = d[k] * wv[k];
@@ -203,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_kernel(
           load_v<_Float16, VEC>(lows + row * static_cast<int64_t>(n_cols) + c, xv, cnt);
 #pragma unroll
           for (int k = 0; k < VEC; ++k) {
-            const int sl = k < cnt ? slot[c + k] : -1;
+            const int sl = (n_small > 0 && k < cnt) ? slot[c + k] : -1;
             nv[k] = sl >= 0
                         ? static_cast<float>(small16[row * static_cast<int64_t>(n_small) + sl])
                         : (k < cnt ? xv[k] / wv[k] : 0.0f);
