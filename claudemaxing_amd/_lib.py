@@ -58,6 +58,8 @@ SIGNATURES = {
     "cm_error_string": (ctypes.c_char_p, [_I]),
     "cm_nf4_dequant": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _I, _L, _I, _I, _P]),
     "cm_nf4_dequant_t": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _L, _L, _I, _I, _P]),
+    "cm_gemm_f32_workspace_bytes": (_L, [_I, _I, _I, _I]),
+    "cm_gemm_f32": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _L, _P]),
     "cm_rmsnorm_fwd": (_I, [_P, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P, _I, _L, _I, _F, _P]),
     "cm_rmsnorm_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _L, _I, _P]),
     "cm_rmsnorm_bwd_partials": (_L, [_L]),

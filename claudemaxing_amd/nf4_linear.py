@@ -15,6 +15,7 @@ import ctypes
 import torch
 
 from . import _lib
+from .gemm import gemm_f32, gemm_f32_supported, split_k_pays
 from .nf4 import _BLOCKSIZES, QuantState, _nf4_code, _offset_tensor, dequantize_nf4, quantize_nf4
 from .rmsnorm import fp16_copy_of
 
@@ -196,8 +197,12 @@ class MatMulNF4(torch.autograd.Function):
         if out_dtype == torch.float32 and compute != torch.float32 and xc.is_cuda:
             # the GEMM writes fp32 itself (fp32 sums, no fp16 rounding and no cast launch)
             x2 = xc.reshape(-1, xc.shape[-1])
-            y = (torch.mm(x2, w.t(), out_dtype=torch.float32) if bias is None else
-                 torch.addmm(bias.float(), x2, w.t(), out_dtype=torch.float32))
+            if bias is None and split_k_pays(x2.shape[0], w.shape[0], x2.shape[1]) and \
+                    gemm_f32_supported(x2.shape[0], w.shape[0], (x2, w)):
+                y = gemm_f32((x2, w))  # narrow output, long contraction: split along k
+            else:
+                y = (torch.mm(x2, w.t(), out_dtype=torch.float32) if bias is None else
+                     torch.addmm(bias.float(), x2, w.t(), out_dtype=torch.float32))
             return y.view(*xc.shape[:-1], w.shape[0])
         return torch.nn.functional.linear(xc, w, bias).to(out_dtype)
 

@@ -55,6 +55,22 @@ int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested, const 
                    const float* code2, const float* absmax2, const float* offset, void* out,
                    int out_dtype, int64_t n_bytes, int blocksize, int blocksize2, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* fp16 products with an fp32 result, split along the contraction: C [M, N] fp32 =
+ * A0 B0^T (+ A1 B1^T), A_q [M, K_q] and B_q [N, K_q] fp16 row-major (row strides lda_q, ldb_q,
+ * multiples of 8; K_q multiples of 8; K1 = 0 for one pair). Replaces, in the training step, the
+ * torch.mm / addmm calls of the MLP whose output is narrow next to their contraction: the down
+ * projection's forward (F.linear of the dequantized weight, solution/nf4.py:102-130, the product
+ * bitsandbytes' gemm_4bit falls back to) and the MLP input gradient dgate Wg + dup Wu (autograd
+ * of the two projections, the reference's MLPInputRecompute backward). Work split into K-slices
+ * whose fp32 partial tiles go to `workspace` (cm_gemm_f32_workspace_bytes bytes) and are added in
+ * slice order: deterministic, sums in fp32 (their order differs from a library GEMM's). All
+ * pointers 16-byte aligned, M * N a multiple of 4. */
+int64_t cm_gemm_f32_workspace_bytes(int M, int N, int K0, int K1);
+int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M, int N,
+                float* out, void* workspace, int64_t ws_bytes, void* stream);
+
 /* The same expansion written transposed, fp16 only: out[c][r] = W[r][c] for the weight W
  * [rows, cols] (rows a multiple of 64, cols of 128; packed 4-byte, out 16-byte aligned), the values
  * bit-identical to cm_nf4_dequant's. No counterpart in the reference: the MLP backward of the

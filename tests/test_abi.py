@@ -172,6 +172,18 @@ def test_nf4_linear_argument_checks(lib):
     assert ws(1276, down, 1, 0) == 4 * 4 * 1276 * 1536  # 4 slices of [1276, 1536] fp32
     assert ws(1276, Arr(_nf4_weight(1536, 8960)), 1, 0) == 0  # no scale map: the general kernel
     assert ws(0, down, 1, 0) == 0 and ws(4, Arr(_nf4_weight(100, 64)), 1, 0) == -1
+    # split-K fp32 GEMM: K multiples of 8, strides >= K and multiples of 8, aligned operands,
+    # a workspace of the stated size
+    gf, gws = lib.cm_gemm_f32, lib.cm_gemm_f32_workspace_bytes
+    assert gws(1276, 1536, 8960, 0) == 6 * 1276 * 1536 * 4 and gws(0, 1536, 64, 0) == 0
+    assert gws(4, 8, 12, 0) == -1 and gws(4, 8, 0, 0) == -1
+    a, b, o, w = 0x10000, 0x20000, 0x30000, 0x40000
+    big = gws(64, 64, 64, 0)
+    assert gf(a, 60, b, 64, 64, None, 0, None, 0, 0, 64, 64, o, w, big, None) == INVALID
+    assert gf(a + 8, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, o, w, big, None) == INVALID
+    assert gf(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, o, w, big - 4, None) == INVALID
+    assert gf(a, 64, b, 64, 64, None, 0, None, 0, 8, 64, 64, o, w, big, None) == INVALID
+    assert gf(a, 64, b, 64, 64, None, 0, None, 0, 0, 0, 64, o, w, 0, None) == 0
     # scale map: blocksize must divide the columns; NULL output
     assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536, 4096)), 0x50000, None) == INVALID
     assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536)), None, None) == INVALID
