@@ -307,7 +307,7 @@ def k_nf4_linear(dev, names):
 
     import torch
 
-    from claudemaxing_amd import _lib, nf4
+    from claudemaxing_amd import _lib, gemm, nf4
     from claudemaxing_amd.nf4_linear import _weights
 
     m, f, h = 1276, 8960, 1536
@@ -318,7 +318,7 @@ def k_nf4_linear(dev, names):
     flops = 2 * 2 * m * f * h
     in_bytes = sum(p.numel() for p, _ in qs) + x.numel() * 2
     out = []
-    fwd, fwd_ref, bwd, bwd_ref = [], [], [], []
+    fwd, fwd_ref, bwd, bwd_ref, bwd_split = [], [], [], [], []
     for _ in range(copies_for(in_bytes + 2 * g.numel() * 2)):
         pairs = [(p.to(dev), st.to(dev)) for p, st in qs]
         xd, gd = x.to(dev), g.to(dev)
@@ -346,8 +346,15 @@ def k_nf4_linear(dev, names):
             wg, wu = (nf4.dequantize_nf4(p, st, torch.float16) for p, st in pairs)
             torch.addmm(torch.mm(gd, wg), gd, wu)
 
+        def split_b(pairs=pairs, gd=gd):
+            # the training step's path: each weight expanded transposed, then one split-K launch
+            # over both products with an fp32 result
+            wgt, wut = (nf4.dequantize_nf4_t(p, st) for p, st in pairs)
+            gemm.gemm_f32((gd, wgt), (gd, wut))
+
         fwd_ref.append((ref_f, hold))
         bwd_ref.append((ref_b, hold))
+        bwd_split.append((split_b, hold))
     if "nf4_linear_fwd" in names:
         out.append(Kernel("nf4_linear_fwd", f"gate+up {m} tokens x 2 x [{f},{h}] nf4", "mfma",
                           flops, fwd))
@@ -357,6 +364,9 @@ def k_nf4_linear(dev, names):
         out.append(Kernel("nf4_linear_bwd", f"dgate Wg + dup Wu, {m} tokens", "mfma", flops, bwd))
         out.append(Kernel("nf4_linear_bwd_unfused", "the same: dequant x 2 + mm + addmm", "mfma",
                           flops, bwd_ref, step=False))
+        out.append(Kernel("nf4_linear_bwd_split", "the same: transposed dequant x 2 + split-K "
+                          "cm_gemm_f32 (fp32 dx; the training step's path)", "mfma", flops,
+                          bwd_split, step=False))
     return out
 
 

@@ -77,15 +77,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
       for (int k = 0; k < VEC; ++k) ss += xv[0][k] * xv[0][k];
     }
   }
-  // the weight's columns, loaded before the row's sum so that both share one memory round trip
-  float wc[kCache][VEC];
-  if constexpr (NV > 0) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = i * step + lane * VEC;
-      load_v<WT, VEC>(w + c, wc[i], c < n_cols ? min(VEC, n_cols - c) : 0);
-    }
-  }
   ss = cm::wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
   if (lane == 0) rstd[row] = r;
@@ -99,14 +90,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_kernel(
     float xi[VEC], wv[VEC], o[VEC], nv[VEC];
     if constexpr (NV > 0) {
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        xi[k] = xv[i][k];
-        wv[k] = wc[i][k];
-      }
+      for (int k = 0; k < VEC; ++k) xi[k] = xv[i][k];
     } else {
       load_v<XT, VEC>(xr + c, xi, cnt);
-      load_v<WT, VEC>(w + c, wv, cnt);
     }
+    load_v<WT, VEC>(w + c, wv, cnt);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
       nv[k] = cm::round_to<XT>(xi[k] * r);  // rounded to the input dtype before the weight
