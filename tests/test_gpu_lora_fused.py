@@ -101,3 +101,39 @@ def test_fused_adapter_without_input_grad(dev):
     assert fused[1] is None and unfused[1] is None
     torch.testing.assert_close(fused[2], unfused[2], rtol=2e-3, atol=2e-3 * float(unfused[2].abs().max()))
     torch.testing.assert_close(fused[3], unfused[3], rtol=2e-3, atol=2e-3 * float(unfused[3].abs().max()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens", [1276, 37, 300, 5000])
+def test_weight_grads_batch_matches_fp64(tokens, dev):
+    """cm_lora_weight_grads (the q and v adapters' four weight gradients in one call) against an
+    fp64 evaluation of the same fp16 operands; the same inputs give the same bits."""
+    from claudemaxing_amd.lora import _weight_grads
+
+    banner(f"lora weight grads tokens={tokens}")
+    g = torch.Generator(device=dev).manual_seed(tokens)
+    ga = torch.randn(tokens, 16, generator=g, device=dev).half()
+    xd = torch.randn(tokens, 1536, generator=g, device=dev).half()
+    gq = torch.randn(tokens, 1536, generator=g, device=dev).half()
+    gv = torch.randn(tokens, 256, generator=g, device=dev).half()
+    a16 = torch.randn(tokens, 16, generator=g, device=dev).half()
+    pairs = [(ga, xd), (gq, a16), (ga, xd[:, :1024]), (gv, a16)]  # the last two: other widths
+    out = _weight_grads(pairs)
+    assert out is not None and [o.shape for o in out] == [(16, 1536), (1536, 16), (16, 1024),
+                                                          (256, 16)]
+    for (p, q), o in zip(pairs, out):
+        ref = p.double().t() @ q.double()
+        err = float((o.double() - ref).abs().max())
+        assert err <= 2e-5 * float(ref.abs().max()) + 1e-5, err
+    again = _weight_grads(pairs)
+    assert all(torch.equal(a, b) for a, b in zip(out, again))
+
+
+@pytest.mark.gpu
+def test_weight_grads_batch_no_tokens(dev):
+    from claudemaxing_amd.lora import _weight_grads
+
+    ga = torch.empty(0, 16, device=dev, dtype=torch.float16)
+    xd = torch.empty(0, 1536, device=dev, dtype=torch.float16)
+    out = _weight_grads([(ga, xd)])
+    assert out is not None and torch.count_nonzero(out[0]) == 0
