@@ -76,10 +76,19 @@ __global__ __launch_bounds__(256) void gemm_f32_sum(const float4* __restrict__ w
                                                     int64_t n4, float4* __restrict__ out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n4) return;
+  // the slices are loaded 8 at a time before they are added in slice order (a runtime-length
+  // loop of load-then-add would wait for each load in turn)
   float4 a = ws[i];
-  for (int s = 1; s < S; ++s) {
-    const float4 b = ws[s * n4 + i];
-    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  for (int s0 = 1; s0 < S; s0 += 8) {
+    float4 b[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k < S) b[k] = ws[(s0 + k) * n4 + i];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k < S) {
+        a.x += b[k].x; a.y += b[k].y; a.z += b[k].z; a.w += b[k].w;
+      }
   }
   out[i] = a;
 }
