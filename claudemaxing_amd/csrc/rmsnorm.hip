@@ -294,7 +294,7 @@ extern "C" int cm_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, 
   CM_CHECK_ARG(n_rows >= 0 && n_cols > 0 && x_row_stride >= n_cols);
   if (n_rows == 0) return 0;
   CM_CHECK_ARG(x && w && out && rstd);
-  CM_CHECK_ARG(!low16 || (slot && small16 && n_small >= 1));
+  CM_CHECK_ARG(!low16 || (slot && small16 && n_small >= 0));  // n_small = 0: no tiny columns
   const int64_t blocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
   CM_CHECK_ARG(blocks <= 0x7fffffff);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -337,7 +337,7 @@ extern "C" int cm_rmsnorm_bwd(const void* dy, int dy_dtype, const void* xs, int 
   CM_CHECK_ARG(dy && xs && w && rstd && dx);
   if (saved_output) {
     // xs holds the fp16 output copy; dx has the dtype of x (fp32 on this path); no dw.
-    CM_CHECK_ARG(xs_dtype == CM_F16 && slot && small16 && n_small >= 1 && !dw_partial);
+    CM_CHECK_ARG(xs_dtype == CM_F16 && slot && small16 && n_small >= 0 && !dw_partial);
   }
   const bool want_dw = dw_partial != nullptr;
   const int64_t blocks = bwd_blocks(n_rows, want_dw);

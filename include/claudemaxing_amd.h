@@ -101,6 +101,7 @@ int cm_nf4_dequant_t(const uint8_t* packed, const void* absmax, int nested, cons
  * x is row-major [n_rows, n_cols] with row stride x_row_stride (elements); out is contiguous.
  * With low16 != NULL (the SAVE_LOW path: fp32 x, frozen fp32 w), also writes
  *   low16[r,c] = fp16(normed * w) and small16[r * n_small + slot[c]] = fp16(normed) for slot[c] >= 0.
+ * n_small = 0 says the weight has no tiny-|w| column: slot is then not read.
  */
 int cm_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, const void* w, int w_dtype,
                    void* out, int out_dtype, float* rstd, void* low16, const int32_t* slot,
