@@ -379,7 +379,7 @@ def k_lmhead(dev):
     h, w, t = inputs.lm_head(0)
     hd, wd, td = h.to(dev), w.to(dev), t.to(dev)
     flops = 4 * h.shape[0] * w.shape[0] * h.shape[1]
-    w16, wt16 = lm_head_loss._fp16_weights(wd, True)  # the host's cached W^T, as in training
+    w16, wt16 = lm_head_loss.fp16_head_weights(wd, True)  # the host's cached W^T, as in training
     keep = (hd, wd, td, w16, wt16)
 
     def launch(hd=hd, w16=w16, td=td, wt16=wt16):

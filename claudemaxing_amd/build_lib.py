@@ -31,6 +31,8 @@ COMMON_FLAGS = [
     # packed fp32 instructions (v_pk_*_f32) stay off: only scalar fp32 VALU ops are emitted
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # a struct of device pointers initialised with too few values leaves the rest null
+    "-Werror=missing-field-initializers",
 ]
 
 

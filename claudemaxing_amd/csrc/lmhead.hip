@@ -22,7 +22,8 @@
 //               keeps the small probabilities of a 152K vocabulary out of fp16's subnormal
 //               range.
 //   K4 final    (after the last chunk) lse, loss, entropy, correct; G = scale (sum_s G_s / 1024
-//               - W_t).
+//               + (p_t - 1) W_t): K2 zeroes the label's entry of E, so the label's coefficient
+//               is applied only here, in fp32.
 //
 // The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 1 GiB) lives in the
 // workspace. The chunk and the transposed weight are stored in 64-column panels
@@ -98,6 +99,7 @@ struct EpiProbs {
   int n_groups;
   const int64_t* target;
   float* label_logit;   // [n_tok]: z of the label, written by the one lane that holds it
+  float* label_off;     // [n_tok]: the label group's sum e^{z - m_g} over its other columns
   int store;            // write E (the gradient needs it)
   int64_t tgt[kTN];     // targets of the lane's tokens, loaded before the main loop
 
@@ -153,8 +155,9 @@ struct EpiProbs {
       best = other ? best_o : best;
       // the label's logit, if this lane holds it (rare: a divergent branch around the search)
       const int64_t local = tgt[nt] - c0 - mb;
-      if (tok_ok && local >= 0 && local < kGroup && ((local % 8) / 4) == half_id &&
-          mb + local < n_voc) {
+      const bool holds_label = tok_ok && local >= 0 && local < kGroup &&
+                               ((local % 8) / 4) == half_id && mb + local < n_voc;
+      if (holds_label) {
         float zt = 0.0f;
 #pragma unroll
         for (int e = 0; e < TM * 16; ++e) zt = vrow(e) == local ? z[e] : zt;
@@ -170,7 +173,16 @@ struct EpiProbs {
         d += ok ? x * z[e] : 0.0f;
         z[e] = x;
       }
-      s += __shfl_xor(s, 32, cm::kWave);
+      const float s_other = __shfl_xor(s, 32, cm::kWave);
+      if (holds_label) {
+        // the group's sum without the label's own term, summed term by term (subtracting the
+        // label's term from s would cancel when the label dominates its group)
+        float own = 0.0f;
+#pragma unroll
+        for (int e = 0; e < TM * 16; ++e) own += vrow(e) == local ? 0.0f : z[e];
+        label_off[tok] = own + s_other;
+      }
+      s += s_other;
       d += __shfl_xor(d, 32, cm::kWave);
       if (store) {
         // stage: 4 consecutive vocabulary rows (8 bytes) per (mt, q)
@@ -304,7 +316,7 @@ __global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm3(
   // initialised on the first chunk and rescaled on later ones.
   const int k_end = max(k_begin, min(A.k_len, k_begin + k_slice));
   EpiGrad epi{out.g[s], n_tok, hidden, factor, first};
-  ScaleP<BM / WM / 32> xp{scale, n_tok};
+  ScaleP<BM / WM / 32> xp{scale, n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
   cm::gemm::gemm_lds<BM, BN, WM, WN, BK, ST>(A, B, k_begin, k_end, tm, tn, epi, lds, xp);
 }
 
@@ -318,55 +330,133 @@ struct RowState {
   float* label_logit;
   float* lse;     // running log-sum-exp after the last merged chunk
   float* factor;  // e^{lse_before - lse_after} of the last merged chunk
+  float* off;        // running sum of e^{z - max} over the columns other than the label
+  float* label_off;  // K1 -> K2: the label group's sum over its other columns
+};
+constexpr int kRowArrays = 9;  // row-state arrays in the workspace, one per field
+static_assert(sizeof(RowState) == kRowArrays * sizeof(void*),
+              "RowState holds exactly one workspace array per field");
+
+// The row state's arrays, laid out one after another from `base`, `stride` bytes apart. Every
+// field is assigned by name here; `complete` says none was left null.
+RowState row_state(char* base, int64_t stride) {
+  auto at = [&](int i) { return reinterpret_cast<float*>(base + i * stride); };
+  RowState r;
+  r.max = at(0);
+  r.sum = at(1);
+  r.dot = at(2);
+  r.best = reinterpret_cast<int32_t*>(at(3));
+  r.label_logit = at(4);
+  r.lse = at(5);
+  r.factor = at(6);
+  r.off = at(7);
+  r.label_off = at(8);
+  return r;
+}
+
+bool complete(const RowState& r) {
+  const void* const* p = reinterpret_cast<const void* const*>(&r);
+  for (int i = 0; i < kRowArrays; ++i)
+    if (p[i] == nullptr) return false;
+  return true;
+}
+
+// The running statistics with the off-label mass beside them: `off` is the sum of e^{z - max}
+// over every column but the label, rescaled with the maximum like `sum`. The label's
+// probability is then p_t = 1 - off / sum exactly, however close to 1 it is (1 - p_t computed
+// from an fp32 log-sum-exp would be quantized to the 2^-24 steps of the sum near 1).
+struct OffState {
+  cm::SoftmaxState st;
+  float off;
+
+  static __device__ __forceinline__ OffState empty() {
+    return OffState{cm::SoftmaxState::empty(), 0.0f};
+  }
+  __device__ __forceinline__ void merge(const OffState& o) {
+    if (o.st.max == -__builtin_huge_valf()) return;
+    if (st.max == -__builtin_huge_valf()) {
+      *this = o;
+      return;
+    }
+    const float m = fmaxf(st.max, o.st.max);
+    off = off * cm::exp_f(st.max - m) + o.off * cm::exp_f(o.st.max - m);
+    st.merge(o.st);
+  }
 };
 
+// Merge the states of all lanes of a THREADS-lane workgroup; every lane gets the result.
+template <int THREADS>
+__device__ __forceinline__ OffState block_merge_off(OffState s, OffState* part) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) {
+    OffState o{cm::shfl_xor_state(s.st, d), __shfl_xor(s.off, d, cm::kWave)};
+    s.merge(o);
+  }
+  const int wave = threadIdx.x / cm::kWave;
+  if (threadIdx.x % cm::kWave == 0) part[wave] = s;
+  __syncthreads();
+  OffState r = part[0];
+#pragma unroll
+  for (int i = 1; i < THREADS / cm::kWave; ++i) r.merge(part[i]);
+  return r;
+}
+
 // K2: merge the chunk's partials into the running state; the factor; with a scale array, the
-// group scales s_g = e^{m_g - lse} * 1024 of labelled tokens ([groups][n_tok], 0 otherwise).
+// group scales s_g = e^{m_g - lse} * 1024 of labelled tokens ([groups][n_tok], 0 otherwise),
+// and the label's own entry of E set to 0 when the label falls in this chunk: the label's
+// coefficient p_t - 1 is applied by K4 in fp32, so its near-1 probability never enters the
+// fp32 accumulators (a ~1024 W_t term there would cancel against -1024 W_t only at the end,
+// losing the small difference 1 - p_t of a confident label to the accumulators' rounding).
 __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
     const Partial* __restrict__ part, int n_groups, RowState rs,
-    const int64_t* __restrict__ target, int n_tok, int n_voc, int first,
-    float* __restrict__ scale) {
+    const int64_t* __restrict__ target, int n_tok, int64_t c0, int n_voc, int first,
+    float* __restrict__ scale, _Float16* __restrict__ e16) {
   const int row = blockIdx.x;
-  cm::SoftmaxState st = cm::SoftmaxState::empty();
+  const int64_t t = target[row];
+  const bool labelled = t != -100;
+  // the label's statistics group in this chunk, or -1
+  const int64_t g_label = t >= c0 && t < c0 + n_voc ? (t - c0) / kGroup : -1;
+  OffState acc = OffState::empty();
   const int n_valid = (n_voc + kGroup - 1) / kGroup;  // groups K1 wrote for this chunk
   for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
     const Partial p = part[static_cast<int64_t>(row) * n_groups + g];
     if (p.best >= 0) {
-      cm::SoftmaxState q{p.max, p.sum, p.dot, static_cast<int64_t>(p.best)};
-      st.merge(q);
+      OffState q{{p.max, p.sum, p.dot, static_cast<int64_t>(p.best)},
+                 g == g_label ? rs.label_off[row] : p.sum};
+      acc.merge(q);
     }
   }
-  __shared__ cm::SoftmaxState s_part[kStatThreads / cm::kWave];
-  st = cm::block_merge<kStatThreads>(st, s_part);
-  cm::SoftmaxState prev = cm::SoftmaxState::empty();
+  __shared__ OffState s_part[kStatThreads / cm::kWave];
+  acc = block_merge_off<kStatThreads>(acc, s_part);
+  OffState now = OffState::empty();
   if (!first) {
-    prev.max = rs.max[row];
-    prev.sum = rs.sum[row];
-    prev.dot = rs.dot[row];
-    prev.best = rs.best[row];
+    now.st = cm::SoftmaxState{rs.max[row], rs.sum[row], rs.dot[row], rs.best[row]};
+    now.off = rs.off[row];
   }
-  const float lse_prev = first ? -__builtin_huge_valf() : prev.lse();
-  cm::SoftmaxState now = prev;
-  now.merge(st);
-  const float lse_now = now.lse();
+  const float lse_prev = first ? -__builtin_huge_valf() : now.st.lse();
+  now.merge(acc);
+  const float lse_now = now.st.lse();
   if (threadIdx.x == 0) {
-    rs.max[row] = now.max;
-    rs.sum[row] = now.sum;
-    rs.dot[row] = now.dot;
-    rs.best[row] = static_cast<int32_t>(now.best);
+    rs.max[row] = now.st.max;
+    rs.sum[row] = now.st.sum;
+    rs.dot[row] = now.st.dot;
+    rs.best[row] = static_cast<int32_t>(now.st.best);
+    rs.off[row] = now.off;
     rs.lse[row] = lse_now;
     rs.factor[row] = first ? 0.0f : cm::exp_f(lse_prev - lse_now);
   }
   if (scale == nullptr) return;
-  const bool labelled = target[row] != -100;
   for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
     const float m = part[static_cast<int64_t>(row) * n_groups + g].max;
     scale[static_cast<int64_t>(g) * n_tok + row] =
         labelled ? cm::exp_f(m - lse_now) * kPScale : 0.0f;
   }
+  if (threadIdx.x == 0 && g_label >= 0)
+    e16[panel_index(row, t - c0, n_tok)] = static_cast<_Float16>(0.0f);
 }
 
-// K4: final per-row outputs; G = scale * (sum_s G_s / 1024 - W[t]) for labelled rows, else 0.
+// K4: final per-row outputs; G = scale * (sum_s G_s / 1024 + (p_t - 1) W[t]) for labelled rows,
+// else 0.
 __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
     RowState rs, const int64_t* __restrict__ target, int64_t vocab, float* __restrict__ loss,
     float* __restrict__ entropy, int32_t* __restrict__ correct, GradSlices gs, int n_split,
@@ -379,18 +469,27 @@ __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
     cm::SoftmaxState st{rs.max[row], rs.sum[row], rs.dot[row], rs.best[row]};
     const float lse = st.lse();
     const float zt = in_range ? rs.label_logit[row] : __builtin_nanf("");
-    loss[row] = labelled ? lse - zt : 0.0f;
+    // lse - z_t = ln(e^{z_t - M} + off) - (z_t - M) = log1p(off e^{M - z_t}): no cancellation
+    // of two nearly equal logs when the label takes almost all of the probability. A label far
+    // below the maximum (loss >= 30, where e^{M - z_t} could overflow) takes lse - z_t.
+    const float gap = st.max - zt;
+    loss[row] = !labelled ? 0.0f
+                : gap < 30.0f ? cm::log1p_f(rs.off[row] * cm::exp_f(gap)) : lse - zt;
     entropy[row] = lse - st.dot / st.sum;
     correct[row] = labelled && st.best == t ? 1 : 0;
   }
   if (gs.g[0] == nullptr) return;
   const _Float16* w = weight + (in_range ? t : 0) * ld_w;
   const int64_t off = static_cast<int64_t>(row) * hidden;
+  // The label's column was zeroed in E (K2), so the accumulators hold sum_{v != t} p_v W_v; the
+  // label's whole coefficient p_t - 1 = -off / sum is applied here in fp32, with the relative
+  // precision of the off-label mass however confident the label is.
+  const float coef = labelled && in_range ? -rs.off[row] / rs.sum[row] : 0.0f;
   for (int h = threadIdx.x; h < hidden; h += kStatThreads) {
     float acc = gs.g[0][off + h];
     for (int s = 1; s < n_split; ++s) acc += gs.g[s][off + h];
     gs.g[0][off + h] = labelled && in_range
-                           ? grad_scale * (acc * (1.0f / kPScale) - static_cast<float>(w[h]))
+                           ? grad_scale * (acc * (1.0f / kPScale) + coef * static_cast<float>(w[h]))
                            : (labelled ? __builtin_nanf("") : 0.0f);
   }
 }
@@ -462,7 +561,7 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   L.off_part = off;
   off += round_up(n_rows * L.n_groups * static_cast<int64_t>(sizeof(Partial)), 256);
   L.off_rows = off;
-  off += 8 * round_up(n_rows * 4, 256);
+  off += kRowArrays * round_up(n_rows * 4, 256);
   L.off_scale = off;
   off += round_up(n_rows * L.n_groups * 4, 256);
   L.off_g = off;
@@ -502,12 +601,8 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
   _Float16* e16 = reinterpret_cast<_Float16*>(ws + L.off_e16);
   Partial* part = reinterpret_cast<Partial*>(ws + L.off_part);
   float* scale = want_grad ? reinterpret_cast<float*>(ws + L.off_scale) : nullptr;
-  const int64_t rstride = round_up(n_rows * 4, 256);
-  char* rb = ws + L.off_rows;
-  RowState rs{reinterpret_cast<float*>(rb), reinterpret_cast<float*>(rb + rstride),
-              reinterpret_cast<float*>(rb + 2 * rstride), reinterpret_cast<int32_t*>(rb + 3 * rstride),
-              reinterpret_cast<float*>(rb + 4 * rstride), reinterpret_cast<float*>(rb + 5 * rstride),
-              reinterpret_cast<float*>(rb + 6 * rstride)};
+  const RowState rs = row_state(ws + L.off_rows, round_up(n_rows * 4, 256));
+  if (!complete(rs)) return static_cast<int>(hipErrorInvalidValue);
   GradSlices gs{};
   gs.g[0] = grad;
   for (int i = 1; i < L.n_split; ++i)
@@ -528,7 +623,7 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
       RowMajor A{W16 + c0 * ld_w, ld_w, n_voc, hidden_size};
       RowMajor B{H16, ld_h, n_tok, hidden_size};
       EpiProbs epi{e16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups), target,
-                   rs.label_logit, want_grad ? 1 : 0};
+                   rs.label_logit, rs.label_off, want_grad ? 1 : 0, {}};  // tgt: prepare()
       hipLaunchKernelGGL((lmh_gemm1<EpiProbs, kBM1, kBN1, kWM1, kWN1, kBK1, kST1, kOcc1>), dim3(grid),
                          dim3(kThreads1), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
       int st = cm::launch_status();
@@ -536,8 +631,8 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
     }
     // K2: running statistics and the group scales
     hipLaunchKernelGGL(lmh_rows_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, part,
-                       static_cast<int>(L.n_groups), rs, target, n_tok, n_voc, first ? 1 : 0,
-                       scale);
+                       static_cast<int>(L.n_groups), rs, target, n_tok, c0, n_voc,
+                       first ? 1 : 0, scale, e16);
     int st = cm::launch_status();
     if (st) return st;
     if (!want_grad) continue;

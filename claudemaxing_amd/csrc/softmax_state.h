@@ -14,6 +14,14 @@ constexpr float kLn2 = 0.6931471805599453f;
 // away for the arguments used here.
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 __device__ __forceinline__ float log_f(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
+// ln(1 + x) for x >= 0 without the rounding of 1 + x near 0: the alternating Taylor series
+// through x^6 for x < 1/32 (the first omitted term is below 2^-37 of the result), log_f(1 + x)
+// beyond.
+__device__ __forceinline__ float log1p_f(float x) {
+  if (x < 0.03125f)
+    return x * (1.0f - x * (0.5f - x * (1.0f / 3 - x * (0.25f - x * (0.2f - x * (1.0f / 6))))));
+  return log_f(1.0f + x);
+}
 
 struct SoftmaxState {
   float max;

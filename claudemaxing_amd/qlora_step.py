@@ -32,7 +32,8 @@ import torch
 from . import apply
 from .attention import packed_rows
 from .embedding import shrink_tied_embedding
-from .lm_head_loss import _REQUEST_ATTR, _pack_batch, _packed_forward
+from .lm_head_loss import (_REQUEST_ATTR, _STEP_ATTR, _pack_batch, _packed_forward,
+                           head_metrics_from_logits, trl_metrics)
 from .lora import LoRALinear
 from .nf4_linear import NF4Linear
 
@@ -120,8 +121,13 @@ def make_optimizer(model, lr=2e-4):
                              weight_decay=0.0, fused=True)
 
 
-def train_step(model, opt, scaler, batch, fused=True):
-    """Forward (fp16 autocast), scaled backward, optimizer step; returns the loss tensor."""
+def train_step(model, opt, scaler, batch, fused=True, metrics=None):
+    """Forward (fp16 autocast), scaled backward, optimizer step; returns the loss tensor.
+
+    With a `metrics` dict, the step also fills in what TRL's compute_loss logs every step
+    (`trl_metrics`: the attention-mask weighted entropy, num_tokens, mean_token_accuracy), from
+    the fused head's per-token terms, or from the logits when the forward built them; like TRL
+    it reads them on the host before the backward."""
     if fused:
         model.__dict__[_REQUEST_ATTR] = True
     try:
@@ -129,6 +135,11 @@ def train_step(model, opt, scaler, batch, fused=True):
             out = model(**batch, use_cache=False)
     finally:
         model.__dict__.pop(_REQUEST_ATTR, None)
+    terms = model.__dict__.pop(_STEP_ATTR, None)
+    if metrics is not None:
+        if terms is None:
+            terms = head_metrics_from_logits(out.logits.detach(), batch["labels"])
+        metrics.update(trl_metrics(terms, batch))
     scaler.scale(out.loss).backward()
     scaler.step(opt)
     scaler.update()

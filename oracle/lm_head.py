@@ -19,11 +19,6 @@ import torch
 IGNORE_INDEX = -100
 
 
-def logits16(h16, w16):
-    """fp16 logits with fp32 accumulation (CPU)."""
-    return (h16.float() @ w16.float().t()).to(torch.float16)
-
-
 def head(h16, w16, target, want_grad=True, rows_per_block=256):
     """(loss [N], entropy [N], correct [N] int32, grad [N,H] fp32 or None, argmax [N], z16 or
     None). Rows are processed in blocks so big vocabularies stay within memory."""
@@ -54,6 +49,27 @@ def head(h16, w16, target, want_grad=True, rows_per_block=256):
             grad[r0:r1] = d @ w32
         del z, p
     return loss, entropy, correct, grad, best
+
+
+def grad_f64(h16, w16, target, rows_per_block=256):
+    """The hidden-state gradient of sum(loss) evaluated in float64 from the fp16 logits:
+    (softmax(z) - onehot(t)) @ w per labelled row, 0 otherwise. In float64 the label's p_t - 1
+    keeps its relative precision even for p_t within 1e-7 of 1, where the fp32 evaluation of
+    `head` (like any fp32 softmax) quantises it to steps of 2^-24."""
+    n = h16.shape[0]
+    out = torch.zeros(n, h16.shape[1], dtype=torch.float64)
+    w32, w64 = w16.float(), w16.double()
+    for r0 in range(0, n, rows_per_block):
+        r1 = min(n, r0 + rows_per_block)
+        z = (h16[r0:r1].float() @ w32.t()).to(torch.float16).double()
+        t = target[r0:r1]
+        lbl = t != IGNORE_INDEX
+        d = torch.softmax(z, dim=-1)
+        d[torch.arange(r1 - r0), t.clamp(min=0)] -= lbl.double()
+        d[~lbl] = 0
+        out[r0:r1] = d @ w64
+        del z, d
+    return out
 
 
 def top2_gap(h16, w16, rows_per_block=256):

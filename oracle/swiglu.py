@@ -5,7 +5,7 @@ F.silu(gate) * up, whose rounding the kernels reproduce (solution/swiglu_recompu
 silu in fp32 rounded to the gate dtype before it meets up, output dtype promote(gate, up);
 backward is torch autograd (the product's gradient rounded to the gate dtype before it goes
 back through silu). The MLP fast path without that rounding (ROUND_SILU off, fp16 buffers of
-an fp32 reference) is `forward_unrounded`.
+an fp32 reference) has its backward in `backward_unrounded`.
 
 What pins it (tests/test_oracle_float.py): silu(x) = x * sigmoid(x) against fp64; the derivative
 sig * (1 + g (1 - sig)) against a central difference in fp64.
@@ -25,11 +25,6 @@ def forward_backward(gate, up, grad):
     out = forward(g, u)
     out.backward(grad.to(out.dtype))
     return out.detach(), g.grad, u.grad
-
-
-def forward_unrounded(gate, up, out_dtype):
-    g, u = gate.float(), up.float()
-    return (g * torch.sigmoid(g) * u).to(out_dtype)
 
 
 def backward_unrounded(gate, up, grad):

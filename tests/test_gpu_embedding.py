@@ -103,7 +103,7 @@ def test_conversion_never_holds_both_copies(dev):
 def test_fused_head_reads_the_fp16_weight(dev):
     banner("tied embedding: the fused head uses the fp16 weight itself")
     from claudemaxing_amd import apply
-    from claudemaxing_amd.lm_head_loss import _REQUEST_ATTR, _fp16_weights
+    from claudemaxing_amd.lm_head_loss import _REQUEST_ATTR, fp16_head_weights
 
     apply()
     model = _tiny(dev)
@@ -117,5 +117,5 @@ def test_fused_head_reads_the_fp16_weight(dev):
     assert torch.isfinite(out.loss)
     w = model.get_input_embeddings().weight
     assert w.dtype == torch.float16
-    w16, _ = _fp16_weights(w, False)
+    w16, _ = fp16_head_weights(w, False)
     assert w16.data_ptr() == w.data_ptr()

@@ -149,3 +149,48 @@ def test_transposed_expansion_random_bytes(blocksize, blocksize2, dev):
                     absmax2=absmax2.numpy(), offset=np.float32(0.03125), blocksize=blocksize,
                     blocksize2=blocksize2)
     assert_bits_equal(out, torch.from_numpy(ref).reshape(rows, cols).t().contiguous(), "random")
+
+
+@pytest.mark.parametrize("nested", [True, False])
+def test_state_dict_checkpoint_dequantizes_bit_exact(nested, dev, tmp_path):
+    """A 4-bit layer's checkpoint in bitsandbytes Linear4bit's key layout ("<prefix>weight"
+    packed [numel/2, 1] uint8 and "<prefix>weight.<serialized QuantState>"), written to a
+    safetensors file, read back with NF4Linear.from_state_dict onto the GPU and dequantized
+    there: bit for bit the oracle's expansion of the raw tensors stored in the file (the oracle
+    reads the file's own absmax / quant_map / nested_* / JSON fields, not the loaded module)."""
+    import json
+
+    from safetensors.torch import load_file, save_file
+
+    from claudemaxing_amd.nf4_linear import NF4Linear
+
+    banner(f"nf4 checkpoint nested={nested}")
+    w = inputs.nf4_weight(3, rows=1536, cols=1536)
+    packed, state = quantize_nf4(w, 64, nested)
+    sd = {"model.layers.0.self_attn.q_proj.weight": packed.reshape(-1, 1).clone()}
+    for k, v in state.as_dict(packed=True).items():
+        sd["model.layers.0.self_attn.q_proj.weight." + k] = v.contiguous()
+    path = tmp_path / "layer.safetensors"
+    save_file(sd, str(path))
+    disk = load_file(str(path))
+    prefix = "model.layers.0.self_attn.q_proj."
+    lin = NF4Linear.from_state_dict(disk, prefix=prefix, device=dev)
+    out = dequantize_nf4(lin.packed, lin.quant_state, torch.float16)
+    torch.cuda.synchronize()
+    key = prefix + "weight"
+    fields = json.loads(bytes(disk[key + ".quant_state.bitsandbytes__nf4"].tolist()).decode())
+    kw = dict(nested=nested, blocksize=fields["blocksize"], out_dtype="f16")
+    if nested:
+        kw.update(code2=disk[key + ".nested_quant_map"].numpy(),
+                  absmax2=disk[key + ".nested_absmax"].numpy(),
+                  offset=np.float32(fields["nested_offset"]),
+                  blocksize2=fields["nested_blocksize"])
+    ref = O.dequant(disk[key].numpy(), disk[key + ".absmax"].numpy(),
+                    code=disk[key + ".quant_map"].numpy(), **kw)
+    assert tuple(fields["shape"]) == (1536, 1536)
+    assert_bits_equal(out, torch.from_numpy(ref).reshape(1536, 1536), f"checkpoint {nested}")
+    # and the loaded layer's product uses the same weight
+    x = torch.randn(7, 1536, generator=torch.Generator().manual_seed(2)).half()
+    y = lin(x.to(dev)).float().cpu()
+    r = x.float() @ torch.from_numpy(ref).reshape(1536, 1536).float().t()
+    assert (y - r).abs().max().item() <= 2e-3 * max(1.0, r.abs().max().item())

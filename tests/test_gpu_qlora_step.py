@@ -138,3 +138,131 @@ def test_graphed_step_trains_with_dropout(dev):
     gstep.load(qlora_step.make_batch(dev, seed=0)[0])  # same packed shape: accepted
     with pytest.raises(ValueError):
         gstep.load(qlora_step.make_batch(dev, seed=1)[0])  # other lengths: a new capture
+
+
+@pytest.mark.gpu
+def test_full_depth_step_trains(dev):
+    """Config 5 at its stated size: 28 layers of the Qwen2.5-1.5B shape, NF4 base weights, LoRA
+    r16 / alpha 32 on q/v, fp16 autocast + GradScaler + AdamW, batch 4 with lengths U[64, 512]
+    packed. Over 4 steps on one batch (dropout off, so the steps differ only by the updates) the
+    loss starts near ln(151936) and goes down, the LoRA weights move, TRL's metrics are sane, and
+    the peak HBM is reported."""
+    import math
+
+    banner("qlora step: 28 layers, 4 steps")
+    model = qlora_step.build_model(dev, seed=0, dropout=0.0)
+    assert len(model.model.layers) == 28
+    batch, lengths = qlora_step.make_batch(dev, seed=0)
+    opt = qlora_step.make_optimizer(model)
+    scaler = torch.amp.GradScaler("cuda")
+    b_before = [p.detach().clone() for n, p in model.named_parameters() if "lora_B" in n]
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    losses, metrics = [], []
+    for _ in range(4):
+        m = {}
+        losses.append(float(qlora_step.train_step(model, opt, scaler, batch, metrics=m)))
+        metrics.append(m)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() / 2 ** 30
+    print(f"28 layers, {int(lengths.sum())} tokens: losses {losses}; peak allocated "
+          f"{peak:.2f} GiB, reserved {torch.cuda.max_memory_reserved() / 2 ** 30:.2f} GiB; "
+          f"metrics {metrics[0]}", flush=True)
+    assert all(math.isfinite(x) for x in losses)
+    assert abs(losses[0] - math.log(151936)) < 1.5
+    assert losses[-1] < losses[0]
+    b_after = [p.detach() for n, p in model.named_parameters() if "lora_B" in n]
+    assert len(b_after) == 56 and any(not torch.equal(a, b) for a, b in zip(b_before, b_after))
+    for m in metrics:
+        assert m["num_tokens"] == int(lengths.sum())
+        assert 0 < m["entropy"] <= math.log(151936) + 1e-3
+        assert 0.0 <= m["mean_token_accuracy"] <= 1.0
+    assert peak < 16.0
+
+
+def _predicted_batch(model, dev, seed):
+    """A config-5 batch whose labels are mostly the model's own greedy prediction of the next
+    token (70%, the rest random), so that token accuracy and entropy are not trivial numbers
+    (tests_local/test_lm_head_trainer.py builds its rows the same way)."""
+    batch, _ = qlora_step.make_batch(dev, seed=seed)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16), qlora_step.unpatched():
+        logits = model(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                       use_cache=False).logits
+    pred = logits.argmax(-1)
+    g = torch.Generator(device=dev).manual_seed(100 + seed)
+    take = torch.rand(pred.shape, generator=g, device=dev) < 0.7
+    labels = batch["labels"].clone()
+    labels[:, 1:] = torch.where(take[:, :-1], pred[:, :-1], labels[:, 1:])
+    labels[batch["attention_mask"] == 0] = -100
+    batch["labels"] = labels
+    return batch
+
+
+def _stock_step(model, opt, scaler, batch):
+    """The unpatched transformers step with TRL's metrics evaluated on its fp16 logits."""
+    import torch.nn.functional as F
+
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = model(**batch, use_cache=False)
+    with torch.no_grad():
+        z = out.logits.float()
+        logp = F.log_softmax(z, -1)
+        ent = -(logp.exp() * logp).sum(-1)
+        mask = batch["attention_mask"]
+        lab = batch["labels"][:, 1:]
+        hit = (z[:, :-1].argmax(-1) == lab) & (lab != -100)
+        m = dict(entropy=float((ent * mask).sum() / mask.sum()), num_tokens=int(mask.sum()),
+                 mean_token_accuracy=float(hit.sum() / (lab != -100).sum()))
+        del z, logp, ent
+    scaler.scale(out.loss).backward()
+    scaler.step(opt)
+    scaler.update()
+    opt.zero_grad(set_to_none=True)
+    return float(out.loss.detach()), m
+
+
+@pytest.mark.gpu
+def test_training_curve_matches_stock(dev):
+    """8 training steps on 8 different batches, fused path against the stock transformers path
+    from identical weights, by the reference's end-to-end rules (tests_local/
+    test_lm_head_trainer.py:164-188): num_tokens identical every step; first-step loss within
+    1%; mean relative gap of the loss, entropy and token-accuracy curves within 3%. Dropout is off
+    so that both runs see the same computation (the two paths draw their masks differently)."""
+    banner("qlora step: 8-step curve, fused vs stock, 2 layers")
+    runs = []
+    for fused in (True, False):
+        model = qlora_step.build_model(dev, seed=0, dropout=0.0, **TWO_LAYERS)
+        if fused:
+            batches = [_predicted_batch(model, dev, s) for s in range(8)]
+        opt = qlora_step.make_optimizer(model)
+        scaler = torch.amp.GradScaler("cuda")
+        curve = []
+        for b in batches:
+            if fused:
+                m = {}
+                loss = float(qlora_step.train_step(model, opt, scaler, b, metrics=m))
+            else:
+                with qlora_step.unpatched():
+                    loss, m = _stock_step(model, opt, scaler, b)
+            curve.append(dict(loss=loss, **m))
+        torch.cuda.synchronize()
+        runs.append(curve)
+        del model, opt
+        torch.cuda.empty_cache()
+    fused_c, stock_c = runs
+
+    def gap(key):
+        return sum(abs(f[key] - s[key]) / max(abs(s[key]), 1e-12)
+                   for f, s in zip(fused_c, stock_c)) / len(stock_c)
+
+    for f, s in zip(fused_c, stock_c):
+        print(f"  loss {s['loss']:.5f} / {f['loss']:.5f}   entropy {s['entropy']:.4f} / "
+              f"{f['entropy']:.4f}   acc {s['mean_token_accuracy']:.4f} / "
+              f"{f['mean_token_accuracy']:.4f}   tokens {s['num_tokens']}", flush=True)
+    gaps = {k: gap(k) for k in ("loss", "entropy", "mean_token_accuracy")}
+    first = abs(fused_c[0]["loss"] - stock_c[0]["loss"]) / abs(stock_c[0]["loss"])
+    print(f"first-step loss gap {first:.4%}; mean gaps {gaps}", flush=True)
+    assert [f["num_tokens"] for f in fused_c] == [s["num_tokens"] for s in stock_c]
+    assert first <= 0.01
+    assert all(v <= 0.03 for v in gaps.values()), gaps
+    assert 0.2 < stock_c[0]["mean_token_accuracy"] < 0.95  # the labels are learnable, not noise

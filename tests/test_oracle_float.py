@@ -180,3 +180,62 @@ def test_head_single_row_by_hand():
     assert abs(ent.item() - (lse - sum(pi * zi for pi, zi in zip(p, z)))) < 1e-6
     g0 = sum((p[i] - (i == 1)) * w16[i, 0].item() for i in range(3))
     assert abs(grad[0, 0].item() - g0) < 1e-6 and corr.item() == 1
+
+
+def _brute_top2(row):
+    """Largest and second-largest entries by a plain scan (a tie gives gap 0) and the fp16
+    spacing of the largest |value|'s binade: 2^(e - 11) for |x| = m 2^e with m in [0.5, 1)
+    (math.frexp), 2^-24 in the subnormal range below 2^-14."""
+    import math
+
+    vals = sorted(float(v) for v in row)
+    top, second = vals[-1], vals[-2]
+    if abs(top) < 2.0 ** -14:
+        return top - second, 2.0 ** -24
+    _, e = math.frexp(abs(top))
+    return top - second, 2.0 ** (e - 11)
+
+
+def test_top2_gap_against_brute_force():
+    """OL.top2_gap decides which argmax mismatches the GPU tests excuse: pinned on tiny rows
+    whose fp16 logits are set directly (identity hidden states, z = W^T): exact ties, a gap of
+    one ulp, negative maxima, maxima at power-of-two boundaries and in the fp16 subnormal
+    range."""
+    rows = [
+        [1.0, 1.0, 0.5, -2.0],                  # exact tie
+        [1.0, 1.0 - 2 ** -11, 0.0, 0.0],        # one ulp below 1 (ulp above 1 is 2^-10)
+        [-3.0, -3.5, -4.0, -5.0],               # all negative
+        [2.0, 1.0, 0.25, 0.0],                  # power-of-two maximum
+        [2.0 ** -15, 2.0 ** -16, 0.0, -1.0],    # subnormal maximum: ulp 2^-24
+        [-0.0, -1e-3, -2.0, -65504.0],          # maximum -0
+        [65504.0, 65504.0, 1.0, 0.0],           # fp16 max, tied
+        [7.0, -7.5, 6.9, 6.875],                # gap smaller than the row's spread
+    ]
+    n = len(rows)
+    w16 = torch.tensor(rows).t().contiguous().half()  # [V=4, H=n]
+    h16 = torch.eye(n).half()
+    gaps, ulps = OL.top2_gap(h16, w16)
+    for r, row in enumerate(rows):
+        z = [float(torch.tensor(v).half()) for v in row]
+        gap, ulp = _brute_top2(z)
+        assert gaps[r].item() == gap, (r, gaps[r].item(), gap)
+        assert ulps[r].item() == ulp, (r, ulps[r].item(), ulp)
+    assert gaps[0] == 0 and gaps[6] == 0 and ulps[4] == 2.0 ** -24 and ulps[6] == 32.0
+
+
+def test_head_grad_f64_against_float64_autograd():
+    """grad_f64 against autograd of F.cross_entropy in float64 on the same fp16 logits,
+    including a row whose label holds all but ~1e-9 of the probability."""
+    h16, w16, t = _head_case(n=24, v=97, h=16, seed=3)
+    h16[5] = 0
+    h16[5, 0] = 8.0
+    w16[:, 0] = 0
+    w16[40, 0] = 3.0  # row 5: z_40 = 24 against 0 elsewhere, p_40 = 1 - ~4e-9
+    t[5] = 40
+    ours = OL.grad_f64(h16, w16, t)
+    z = (h16.float() @ w16.float().t()).half().double().requires_grad_(True)
+    F.cross_entropy(z, t, ignore_index=-100, reduction="sum").backward()
+    ref = z.grad @ w16.double()
+    torch.testing.assert_close(ours, ref, rtol=1e-12, atol=1e-15)
+    assert 0 < ref[5].abs().max() < 1e-6  # a tiny, nonzero row survives in float64
+    assert torch.all(ours[t == -100] == 0)

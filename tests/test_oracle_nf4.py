@@ -122,3 +122,30 @@ def test_package_quantizer_matches_the_oracle_quantizer():
     np.testing.assert_allclose(state.state2.code.numpy(), q["code2"], rtol=1e-6, atol=1e-12)
     mismatch = np.count_nonzero(state.absmax.numpy() != q["absmax"])
     assert mismatch <= 2
+
+
+def test_to_bf16_bits_matches_torch_rounding():
+    """The oracle's fp32 -> bf16 rounding (the checker of the kernels' bf16 outputs) against
+    torch's own `.to(torch.bfloat16)`: every fp16 value, fp32 specials, subnormals, exact
+    halfway cases (ties to even, both parities), the overflow edge and random bit patterns."""
+    fp16_all = np.arange(65536, dtype=np.uint16).view(np.float16).astype(F32)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.finfo(F32).max, -np.finfo(F32).max,
+                         np.finfo(F32).tiny, np.finfo(F32).tiny / 3, 1e-45, -1e-45], dtype=F32)
+    rng = np.random.default_rng(7)
+    hi = rng.integers(0, 1 << 16, 4096, dtype=np.uint32) << 16
+    halves = np.concatenate([hi | 0x8000, hi | 0x7FFF, hi | 0x8001]).view(F32)  # ties + edges
+    edge = np.array([0x7F7F8000, 0x7F7F7FFF, 0xFF7F8000], dtype=np.uint32).view(F32)
+    randbits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(F32)
+    x = np.concatenate([fp16_all, specials, halves, edge, randbits])
+    nan = np.isnan(x)
+    ours = O.to_bf16_bits(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours[~nan], ref[~nan])
+    # NaN stays NaN (sign kept, quiet bit set), as the kernel's conversion does
+    nan_in = np.array([0x7FC00000, 0xFF800001, 0x7F800001], dtype=np.uint32).view(F32)
+    out = O.to_bf16_bits(nan_in)
+    assert np.all((out & 0x7F80) == 0x7F80) and np.all(out & 0x0040)
+    assert list(out >> 15) == [0, 1, 0]
+    # a plausible slip, truncation instead of rounding, fails the same comparison
+    trunc = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert not np.array_equal(trunc[~nan], ref[~nan])
