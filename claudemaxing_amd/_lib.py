@@ -74,6 +74,8 @@ SIGNATURES = {
     "cm_xent_rows": (_I, [_P, _I, _L, _P, _P, _P, _P, _L, _L, _I, _F, _P]),
     "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L, _P]),
     "cm_lmhead_ce_workspace_bytes": (_L, [_L, _L, _I, _L]),
+    "cm_lmhead_ce_noalloc": (_I, [_P, _L, _P, _L, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F,
+                                  _P]),
     "cm_attn_fwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _I, _I, _I, _F,
                          _P, _P, _P, _L, _P]),
     "cm_attn_bwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _P, _P, _I, _I,

@@ -29,6 +29,8 @@
 // workspace. The chunk and the transposed weight are stored in 64-column panels
 // ([C/64][tokens][64], [V/64][H][64]) so that every K3 operand tile is one contiguous 16 KiB
 // read.
+#include <mutex>
+
 #include "common.h"
 #include "gemm_lds.h"
 #include "softmax_state.h"
@@ -580,24 +582,30 @@ extern "C" int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, i
   return layout(n_rows, vocab, hidden_size, chunk_cols, true, true).total;
 }
 
-extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-                            const void* weight_t, const int64_t* target, int64_t n_rows,
-                            int64_t vocab, int hidden_size, int64_t chunk_cols, float* loss,
-                            float* entropy, int32_t* correct, float* grad, float grad_scale,
-                            void* workspace, int64_t workspace_bytes, void* stream) {
-  CM_CHECK_ARG(n_rows >= 0 && vocab > 0 && hidden_size > 0 && chunk_cols >= 0);
-  if (n_rows == 0) return 0;
-  CM_CHECK_ARG(hidden && weight && target && loss && entropy && correct && workspace);
-  CM_CHECK_ARG(n_rows < (int64_t{1} << 31) && vocab < (int64_t{1} << 31));
+namespace {
+
+// Argument checks shared by both entry points (everything but the workspace).
+bool args_ok(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
+             const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
+             int hidden_size, int64_t chunk_cols, const float* loss, const float* entropy,
+             const int32_t* correct) {
+  if (!(n_rows > 0 && vocab > 0 && hidden_size > 0 && chunk_cols >= 0)) return false;
+  if (!(hidden && weight && target && loss && entropy && correct)) return false;
+  if (!(n_rows < (int64_t{1} << 31) && vocab < (int64_t{1} << 31))) return false;
   // 16-byte tile rows: hidden size, leading dimensions and bases multiples of 8 fp16.
-  CM_CHECK_ARG(hidden_size % 8 == 0 && ld_h % 8 == 0 && ld_w % 8 == 0 && ld_h >= hidden_size &&
-               ld_w >= hidden_size && cm::aligned(hidden, 16) && cm::aligned(weight, 16));
-  if (weight_t) CM_CHECK_ARG(cm::aligned(weight_t, 16));
+  if (!(hidden_size % 8 == 0 && ld_h % 8 == 0 && ld_w % 8 == 0 && ld_h >= hidden_size &&
+        ld_w >= hidden_size && cm::aligned(hidden, 16) && cm::aligned(weight, 16)))
+    return false;
+  return weight_t == nullptr || cm::aligned(weight_t, 16);
+}
+
+// The launches of one call (K1..K4 per chunk), on `ws` laid out as L; the arguments and the
+// workspace's size and alignment have been checked.
+int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
+               const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
+               int hidden_size, float* loss, float* entropy, int32_t* correct, float* grad,
+               float grad_scale, char* ws, const Layout& L, hipStream_t s) {
   const bool want_grad = grad != nullptr;
-  const Layout L = layout(n_rows, vocab, hidden_size, chunk_cols, want_grad, want_grad && !weight_t);
-  CM_CHECK_ARG(workspace_bytes >= L.total && cm::aligned(workspace, 256));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
   _Float16* e16 = reinterpret_cast<_Float16*>(ws + L.off_e16);
   Partial* part = reinterpret_cast<Partial*>(ws + L.off_part);
   float* scale = want_grad ? reinterpret_cast<float*>(ws + L.off_scale) : nullptr;
@@ -671,4 +679,99 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
   hipLaunchKernelGGL(lmh_final_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, rs, target, vocab,
                      loss, entropy, correct, fin, L.n_split, W16, ld_w, hidden_size, grad_scale);
   return cm::launch_status();
+}
+
+}  // namespace
+
+extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
+                            const void* weight_t, const int64_t* target, int64_t n_rows,
+                            int64_t vocab, int hidden_size, int64_t chunk_cols, float* loss,
+                            float* entropy, int32_t* correct, float* grad, float grad_scale,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  CM_CHECK_ARG(n_rows >= 0);
+  if (n_rows == 0) return 0;
+  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+                       chunk_cols, loss, entropy, correct));
+  CM_CHECK_ARG(workspace != nullptr);
+  const bool want_grad = grad != nullptr;
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk_cols, want_grad, want_grad && !weight_t);
+  CM_CHECK_ARG(workspace_bytes >= L.total && cm::aligned(workspace, 256));
+  return run_lmhead(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+                    loss, entropy, correct, grad, grad_scale, static_cast<char*>(workspace), L,
+                    static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------------------------
+// The entry point that allocates nothing: the same computation on a file-scope device array.
+// Each GPU the library runs on holds its own copy of `scratch` (at its own address) until the
+// process ends. Host code never passes the array's name to a kernel or copy (on the host the
+// name is a stand-in, not a device address): it uses the address hipGetSymbolAddress returns
+// for the current device, looked up once per device and kept.
+namespace {
+
+constexpr int64_t kScratchBytes = CM_LMHEAD_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_addr[kMaxDevices];  // device address of `scratch` per device, null until found
+
+// The current device's copy of `scratch`, or an error code.
+int scratch_of_current_device(char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return static_cast<int>(hipErrorInvalidDevice);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (addr == nullptr || !cm::aligned(addr, 256)) return static_cast<int>(hipErrorInvalidSymbol);
+    g_scratch_addr[dev] = static_cast<char*>(addr);
+  }
+  *out = g_scratch_addr[dev];
+  return 0;
+}
+
+// The chunk the scratch can hold: chunk_cols itself when given (0 when it does not fit), else
+// the largest multiple of 256 columns (at most the whole vocabulary) whose layout fits.
+int64_t scratch_chunk(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_cols,
+                      bool want_grad, bool need_wt) {
+  auto fits = [&](int64_t c) {
+    return layout(n_rows, vocab, hidden, c, want_grad, need_wt).total <= kScratchBytes;
+  };
+  if (chunk_cols > 0) return fits(chunk_cols) ? chunk_cols : 0;
+  int64_t lo = 0, hi = round_up(vocab, kChunkAlign) / kChunkAlign;  // in units of 256 columns
+  while (lo < hi) {  // largest fitting multiple; the layout grows with the chunk
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (fits(mid * kChunkAlign)) lo = mid; else hi = mid - 1;
+  }
+  return lo * kChunkAlign;
+}
+
+}  // namespace
+
+extern "C" int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void* weight,
+                                    int64_t ld_w, const void* weight_t, const int64_t* target,
+                                    int64_t n_rows, int64_t vocab, int hidden_size,
+                                    int64_t chunk_cols, float* loss, float* entropy,
+                                    int32_t* correct, float* grad, float grad_scale,
+                                    void* stream) {
+  CM_CHECK_ARG(n_rows >= 0);
+  if (n_rows == 0) return 0;
+  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+                       chunk_cols, loss, entropy, correct));
+  const bool want_grad = grad != nullptr;
+  const bool need_wt = want_grad && !weight_t;
+  const int64_t chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad, need_wt);
+  if (chunk == 0) return CM_ERROR_SCRATCH_TOO_SMALL;
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad, need_wt);
+  if (L.total > kScratchBytes) return CM_ERROR_SCRATCH_TOO_SMALL;
+  char* ws = nullptr;
+  const int st = scratch_of_current_device(&ws);
+  if (st) return st;
+  return run_lmhead(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+                    loss, entropy, correct, grad, grad_scale, ws, L,
+                    static_cast<hipStream_t>(stream));
 }

@@ -4,7 +4,8 @@
  * Every entry point
  *   - takes plain device pointers, element counts and strides, never torch types;
  *   - is stream-ordered on `stream` (a hipStream_t passed as void*, NULL = the null stream);
- *   - never allocates, never synchronises the host, holds no mutable global state;
+ *   - never allocates, never synchronises the host, holds no mutable global state (save the
+ *     per-device address of cm_lmhead_ce_noalloc's scratch array, found once);
  *   - returns 0 on success, or a hipError_t value (hipErrorInvalidValue = 1 for bad arguments;
  *     launch failures are reported from hipGetLastError()). cm_error_string() names a code.
  *
@@ -223,6 +224,30 @@ int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t l
 /* Workspace bytes cm_lmhead_ce needs for these sizes (chunk_cols as passed to cm_lmhead_ce). */
 int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_size,
                                      int64_t chunk_cols);
+
+/* cm_lmhead_ce without a workspace argument: it allocates nothing (no hipMalloc / hipFree or
+ * allocating library call, on any call). No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). The arguments and results are cm_lmhead_ce's.
+ *
+ * Its scratch is a file-scope device array of CM_LMHEAD_NOALLOC_SCRATCH_BYTES, one per GPU,
+ * held by that GPU until the process ends; its device address is looked up once per device on
+ * the first call with that device current, so call it with the stream's device current. The
+ * vocabulary chunk is chunk_cols when given, else the largest multiple of 256 columns whose
+ * workspace (cm_lmhead_ce_workspace_bytes with that chunk; less without a gradient or with
+ * weight_t) fits the scratch: with the same chunk the results are bit-identical to
+ * cm_lmhead_ce's. Sizes whose smallest layout (or the given chunk's) does not fit return
+ * CM_ERROR_SCRATCH_TOO_SMALL before anything is launched. Every call on one GPU uses that GPU's
+ * one array: calls that overlap on one GPU (other streams, other threads) race; nothing in the
+ * array needs to start at any value, so stream-ordered calls need nothing between them.
+ */
+#define CM_LMHEAD_NOALLOC_SCRATCH_BYTES (64LL << 20)
+#define CM_ERROR_SCRATCH_TOO_SMALL 20001
+int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
+                         const void* weight_t, const int64_t* target, int64_t n_rows,
+                         int64_t vocab, int hidden_size, int64_t chunk_cols, float* loss,
+                         float* entropy, int32_t* correct, float* grad, float grad_scale,
+                         void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
 /* Causal grouped-query attention over a packed batch of variable-length rows, forward. Replaces,
