@@ -7,8 +7,11 @@ Every kernel runs on inputs already resident in HBM, at the shapes of BASELINE.j
   2  RMSNorm fwd/bwd and RoPE fwd/bwd on 4 packed rows of U[128,512] tokens (hidden 1536)
   3  SwiGLU forward and in-place recompute-backward on [2048,8960] fp16
   4  fused LM head + cross-entropy, hidden [2048,1536], tied weight [151936,1536] fp16
-plus the LoRA mask pack/unpack at the q/v input shape of config 5, bandwidth-scale shapes of the
-row kernels (32768 tokens) and torch's device copy as the practical HBM ceiling.
+plus the LoRA mask pack/unpack at the q/v input shape of config 5, every streaming kernel at a
+bandwidth-scale shape (32768 tokens; NF4 over one decoder layer's weights), the launch floor of
+the box (an empty kernel, a one-wavefront kernel, a 1 MiB copy), torch's device copy as the
+practical HBM ceiling, and config 5's QLoRA training step (eager over distinct batches, and
+replayed from a HIP graph).
 
 Cold-cache protocol: each timed launch works on its own copy of the inputs, rotating through
 enough copies to exceed 512 MiB (twice the 256 MiB Infinity Cache), so no launch finds its
@@ -266,15 +269,105 @@ def k_copy_ref(dev):
                    launches, step=False)]
 
 
-def k_bandwidth_scale(dev, names):
-    """The row kernels at 32768 tokens, where launch latency no longer dominates."""
+def k_floor(dev, names):
+    """What a launch costs on this box whatever it does, under the same cold-cache rotation:
+    a kernel that does no work (torch's spin kernel with a zero cycle count), a one-wavefront
+    kernel (a 64-element fill) and a 1 MiB device copy. These set the floor under the small
+    config-2 / config-5 launches."""
     import torch
 
-    from claudemaxing_amd import _lib
+    out = []
+    if "floor_empty" in names:
+        out.append(Kernel("floor_empty", "torch.cuda._sleep(0): one empty workgroup", "hbm", 0,
+                          [((lambda: torch.cuda._sleep(0)), ())], step=False))
+    if "floor_one_wave" in names:
+        launches = []
+        for _ in range(64):
+            x = torch.empty(64, device=dev)
+            launches.append(((lambda x=x: x.fill_(1.0)), (x,)))
+        out.append(Kernel("floor_one_wave", "64-element fp32 fill (one wavefront)", "hbm", 256,
+                          launches, step=False))
+    if "floor_copy_1mib" in names:
+        n_el = 2 ** 18
+        launches = []
+        for _ in range(copies_for(8 * n_el, cap=600)):
+            a = torch.randn(n_el, device=dev)
+            b = torch.empty_like(a)
+            launches.append(((lambda a=a, b=b: b.copy_(a)), (a, b)))
+        out.append(Kernel("floor_copy_1mib", "1 MiB fp32 device copy (torch)", "hbm", 8 * n_el,
+                          launches, step=False))
+    return out
+
+
+def k_bandwidth_scale(dev, names):
+    """Every streaming kernel at a size where launch latency no longer dominates: the row
+    kernels at 32768 tokens, NF4 over all of one decoder layer's NF4 elements."""
+    import torch
+
+    from claudemaxing_amd import _lib, nf4
     from oracle import rope as orope
 
     nb, hid = 32768, 1536
     out = []
+    if "nf4_dequant_bw" in names:
+        # q, k, v, o, gate, up, down of one Qwen2.5-1.5B layer: 46.6M elements, one tensor
+        rows = 1536 + 256 + 256 + 1536 + 8960 + 8960 + 8960
+        w = torch.randn(rows, hid, generator=torch.Generator().manual_seed(1)) * 0.02
+        packed, state = nf4.quantize_nf4(w, 64, True)
+        n_el, n_bytes = w.numel(), w.numel() // 2
+        work = n_bytes + state.absmax.numel() + state.state2.absmax.numel() * 4 + 256 * 4 + \
+            16 * 4 + 4 + n_el * 2
+        launches = []
+        for _ in range(copies_for(work)):
+            p, st = packed.to(dev), state.to(dev)
+            o = torch.empty(w.shape, dtype=torch.float16, device=dev)
+            assert p.numel() == n_bytes and o.numel() == n_el
+            launches.append((bound("cm_nf4_dequant", p.data_ptr(), st.absmax.data_ptr(), 1,
+                                   st.code.data_ptr(), st.state2.code.data_ptr(),
+                                   st.state2.absmax.data_ptr(), st.offset.data_ptr(),
+                                   o.data_ptr(), _lib.F16, n_bytes, 64, 256, _stream(dev)),
+                             (p, st, o)))
+        out.append(Kernel("nf4_dequant_bw", f"[{rows},1536] nf4->fp16 (one layer's NF4 "
+                          "elements)", "hbm", work, launches, step=False))
+    if "rmsnorm_bwd_bw" in names:
+        xb = torch.randn(nb, hid, device=dev).half()
+        wb = torch.rand(hid, device=dev).half() + 0.5
+        rstd = torch.empty(nb, dtype=torch.float32, device=dev)
+        o = torch.empty(nb, hid, dtype=torch.float16, device=dev)
+        bound("cm_rmsnorm_fwd", xb.data_ptr(), _lib.F16, hid, wb.data_ptr(), _lib.F16,
+              o.data_ptr(), _lib.F16, rstd.data_ptr(), None, None, None, 0, nb, hid, 1e-6,
+              _stream(dev))()  # real rstd before the backward is timed
+        launches = []
+        for _ in range(2):
+            dy = torch.randn(nb, hid, device=dev).half()
+            dx = torch.empty(nb, hid, dtype=torch.float16, device=dev)
+            launches.append((bound("cm_rmsnorm_bwd", dy.data_ptr(), _lib.F16, xb.data_ptr(),
+                                   _lib.F16, wb.data_ptr(), _lib.F16, rstd.data_ptr(),
+                                   dx.data_ptr(), _lib.F16, None, None, None, 0, 0, nb, hid,
+                                   _stream(dev)), (xb, wb, rstd, dy, dx)))
+        out.append(Kernel("rmsnorm_bwd_bw", f"N={nb} H=1536 fp16", "hbm",
+                          6 * nb * hid + 4 * nb + 2 * hid, launches, step=False))
+    if "lora_pack_bw" in names or "lora_unpack_bw" in names:
+        n_el = nb * hid
+        x = torch.randn(n_el, device=dev)
+        keep = torch.rand(n_el, device=dev) > 0.05
+        xd = torch.empty(n_el, dtype=torch.float16, device=dev)
+        bits = torch.empty(n_el // 8, dtype=torch.uint8, device=dev)
+        g16 = torch.randn(n_el, device=dev).half()
+        dx = torch.empty(n_el, device=dev)
+        xd2 = torch.empty(n_el, dtype=torch.float16, device=dev)
+        t = (x, keep, xd, bits, g16, dx, xd2)
+        p = bound("cm_lora_pack", x.data_ptr(), _lib.F32, keep.data_ptr(), xd.data_ptr(),
+                  bits.data_ptr(), n_el, 1 / 0.95, _stream(dev))
+        p()
+        if "lora_pack_bw" in names:
+            out.append(Kernel("lora_pack_bw", f"[{nb},1536] fp32 x", "hbm", 7 * n_el + n_el // 8,
+                              [(p, t)], step=False))
+        if "lora_unpack_bw" in names:
+            u = bound("cm_lora_unpack", xd.data_ptr(), bits.data_ptr(), g16.data_ptr(),
+                      xd2.data_ptr(), dx.data_ptr(), _lib.F32, n_el, 1 / 0.95, _stream(dev))
+            out.append(Kernel("lora_unpack_bw", f"[{nb},1536] -> fp32 dx", "hbm",
+                              10 * n_el + n_el // 8, [(u, t)], step=False))
     if "rmsnorm_fwd_bw" in names:
         xb = torch.randn(nb, hid, device=dev).half()
         wb = torch.rand(hid, device=dev).half() + 0.5
@@ -294,6 +387,14 @@ def k_bandwidth_scale(dev, names):
         cos, sin = cos.to(dev), sin.to(dev)
         launches = [_rope_launch(dev, q, k, cos, sin, False)]
         out.append(Kernel("rope_fwd_bw", f"N={nb} 12+2 heads x 128", "hbm",
+                          2 * 2 * nb * 14 * 128 + 2 * 2 * nb * 128, launches, step=False))
+    if "rope_bwd_bw" in names:
+        q = torch.randn(1, nb, 12 * 128, device=dev).half().view(1, nb, 12, 128).transpose(1, 2)
+        k = torch.randn(1, nb, 2 * 128, device=dev).half().view(1, nb, 2, 128).transpose(1, 2)
+        cos, sin = orope.cos_sin(torch.arange(nb) % 512, 128, 1e6, torch.float16)
+        cos, sin = cos.to(dev), sin.to(dev)
+        launches = [_rope_launch(dev, q, k, cos, sin, True)]
+        out.append(Kernel("rope_bwd_bw", f"N={nb} 12+2 heads x 128", "hbm",
                           2 * 2 * nb * 14 * 128 + 2 * 2 * nb * 128, launches, step=False))
     return out
 
@@ -385,14 +486,26 @@ def k_lmhead(dev):
     def launch(hd=hd, w16=w16, td=td, wt16=wt16):
         return lm_head_loss._fused_rows(hd, w16, td, True, None, wt16)
 
+    def launch_8192(hd=hd, w16=w16, td=td, wt16=wt16):
+        return lm_head_loss._fused_rows(hd, w16, td, True, 8192, wt16)
+
     launch()
+    launch_8192()
     torch.cuda.synchronize()
-    return [Kernel("lmhead_ce", "N=2048 V=151936 H=1536 fp16", "mfma", flops, [(launch, keep)])]
+    return [Kernel("lmhead_ce", "N=2048 V=151936 H=1536 fp16", "mfma", flops, [(launch, keep)]),
+            Kernel("lmhead_ce_chunk8192", "the same in 8192-column vocabulary chunks (config 4's "
+                   "stated chunk: a 32 MiB E buffer)", "mfma", flops, [(launch_8192, keep)],
+                   step=False)]
 
 
 ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd", "swiglu_fwd",
-       "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "rmsnorm_fwd_bw", "rope_fwd_bw",
-       "nf4_linear_fwd", "nf4_linear_bwd", "lmhead_ce"]
+       "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "floor_empty", "floor_one_wave",
+       "floor_copy_1mib", "nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw",
+       "rope_bwd_bw", "lora_pack_bw", "lora_unpack_bw", "nf4_linear_fwd", "nf4_linear_bwd",
+       "lmhead_ce"]
+BW_ROWS = {"nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw", "rope_bwd_bw",
+           "lora_pack_bw", "lora_unpack_bw"}
+FLOORS = {"floor_empty", "floor_one_wave", "floor_copy_1mib"}
 
 
 def build_kernels(dev, only):
@@ -413,7 +526,9 @@ def build_kernels(dev, only):
         kernels += k_lora(dev, names)
     if "hbm_copy_ref" in names:
         kernels += k_copy_ref(dev)
-    if names & {"rmsnorm_fwd_bw", "rope_fwd_bw"}:
+    if names & FLOORS:
+        kernels += k_floor(dev, names)
+    if names & BW_ROWS:
         kernels += k_bandwidth_scale(dev, names)
     if names & {"nf4_linear_fwd", "nf4_linear_bwd"}:
         kernels += k_nf4_linear(dev, names)
@@ -520,11 +635,29 @@ def qlora_step_bench(dev, steps, warmup=2):
     opt = qlora_step.make_optimizer(model)
     scaler = torch.amp.GradScaler("cuda")
     build_s = time.perf_counter() - t0
+    # the headline step figure: a fresh batch (new lengths) every step, eager, TRL's metrics
+    # computed every step; then the same with a new HIP graph captured for every batch
+    # (capture inside the timed step), then one repeated batch eager and replayed from a graph
+    rd = qlora_step.time_distinct_batches(model, opt, scaler, steps, warmup)
+    rdg = qlora_step.time_distinct_batches(model, opt, scaler, max(3, steps // 3), 1,
+                                           graphed=True)
     r = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup)
     rg = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup, graphed=True)
     tokens = int(lengths.sum())
-    out = dict(config="Qwen2.5-1.5B shape, 28 layers, NF4 + LoRA r16 q/v, batch 4, "
-                      f"{tokens} real tokens (lengths {lengths.tolist()}), fp16 autocast",
+    out = dict(config="Qwen2.5-1.5B shape, 28 layers, NF4 + LoRA r16 q/v, batch 4 of U[64,512] "
+                      "tokens packed out, fp16 autocast, AdamW + GradScaler",
+               distinct_batches=dict(
+                   median_ms=round(rd["median_ms"], 2), step_ms=[round(x, 2) for x in rd["step_ms"]],
+                   tokens=rd["tokens"], tokens_per_s=round(rd["tokens_per_s"], 1),
+                   peak_allocated_gb=round(rd["peak_allocated_gb"], 3),
+                   peak_reserved_gb=round(rd["peak_reserved_gb"], 3),
+                   note="eager, a new batch every step (the headline step figure)",
+                   graphed_with_capture=dict(
+                       median_ms=round(rdg["median_ms"], 2),
+                       step_ms=[round(x, 2) for x in rdg["step_ms"]],
+                       note="a new HIP graph captured (one warm-up pass + capture) and replayed "
+                            "for every batch, all inside the timed step")),
+               fixed_batch=f"{tokens} real tokens (lengths {lengths.tolist()}), repeated",
                median_ms=round(r["median_ms"], 2), step_ms=[round(x, 2) for x in r["step_ms"]],
                tokens_per_s=round(tokens / (r["median_ms"] * 1e-3), 1),
                peak_allocated_gb=round(r["peak_allocated_gb"], 3),
@@ -562,6 +695,8 @@ def main():
         ms = time_kernel(kern, args.steps, args.warmup)
         if kern.bound == "hbm":
             achieved, peak, unit = kern.work / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+            if kern.name in FLOORS:
+                unit = "GB/s (launch floor)"
         else:
             achieved, peak, unit = kern.work / (ms * 1e-3) / 1e12, MFMA_FP16_PEAK_TFLOPS, "TFLOP/s"
         results[kern.name] = dict(config=kern.config, us=round(ms * 1e3, 2),
@@ -586,7 +721,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sum(r["us"] for r in results.values() if r["in_step"]) / 1e3, 4),
+        "ms_per_step": round(hr["us"] / 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -599,14 +734,19 @@ def main():
                      "unit": hr["unit"], "frac": hr["frac"],
                      "traffic": traffic_from_profile(headline)},
         "kernels": results,
+        "ms_per_step_note": "one headline call (the fused LM head at config 4) per step",
+        "in_step_kernel_sum_ms": round(sum(r["us"] for r in results.values()
+                                           if r["in_step"]) / 1e3, 4),
     }
     if not args.no_step and (not only or "qlora_step" in only):
         print("[bench] qlora_step ...", file=sys.stderr, flush=True)
         line["qlora_step"] = qlora_step_bench(dev, args.step_steps)
-        print(f"[bench] qlora_step: {line['qlora_step']['median_ms']} ms per step eager, "
-              f"{line['qlora_step']['graphed']['median_ms']} ms graphed, peak "
-              f"{line['qlora_step']['peak_allocated_gb']} GB allocated", file=sys.stderr,
-              flush=True)
+        q = line["qlora_step"]
+        print(f"[bench] qlora_step: {q['distinct_batches']['median_ms']} ms per step eager over "
+              f"distinct batches ({q['distinct_batches']['graphed_with_capture']['median_ms']} ms "
+              f"capturing a graph per batch); fixed batch {q['median_ms']} ms eager, "
+              f"{q['graphed']['median_ms']} ms graphed; peak {q['peak_allocated_gb']} GB "
+              f"allocated", file=sys.stderr, flush=True)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(headline)
     print(json.dumps(line), flush=True)

@@ -43,6 +43,9 @@ using cm::gemm::half8;
 using cm::gemm::RowMajor;
 
 constexpr int kPanel = 64;          // columns per panel of the blocked layouts
+// Logit given to vocabulary rows past a chunk's last column in K1's epilogue: below every fp16
+// value (and finite, so that e^{z - m} z is 0, not NaN).
+constexpr float kNoLogit = -3.0e38f;
 constexpr float kPScale = 1024.0f;  // P16 = fp16(p * kPScale)
 constexpr int kStatThreads = 256;
 constexpr int kMaxSplit = 8;
@@ -72,6 +75,7 @@ constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 4, kWN3 = 2, kBK3 = 64, kST3 = 2, k
 constexpr int kThreads1 = kWM1 * kWN1 * cm::kWave;
 constexpr int kThreads3 = kWM3 * kWN3 * cm::kWave;
 constexpr int kGroup = kBM1 / kWM1;  // vocabulary columns per partial-statistics group
+constexpr int kEpiRows = kGroup / 2;  // group rows one lane of K1's epilogue holds per token
 static_assert(kGroup % kPanel == 0, "a statistics group is whole panels");
 
 __device__ __forceinline__ int64_t panel_index(int64_t row, int64_t col, int64_t rows) {
@@ -100,8 +104,7 @@ struct EpiProbs {
   Partial* part;        // [n_tok, n_groups]
   int n_groups;
   const int64_t* target;
-  float* label_logit;   // [n_tok]: z of the label, written by the one lane that holds it
-  float* label_off;     // [n_tok]: the label group's sum e^{z - m_g} over its other columns
+  _Float16* label_z;    // [n_tok][2][64]: the label group's fp16 logits, lane by lane
   int store;            // write E (the gradient needs it)
   int64_t tgt[kTN];     // targets of the lane's tokens, loaded before the main loop
 
@@ -136,55 +139,57 @@ struct EpiProbs {
     for (int nt = 0; nt < TN; ++nt) {
       const int tok = nb + nt * 32 + lane % 32;
       const bool tok_ok = tok < n_tok;
-      // fp16 logits of this lane's token
-      float z[TM * 16];
+      // fp16 logits of this lane's token, in place of its accumulators (a separate array of 64
+      // values made the epilogue spill); rows past the chunk's last column get kNoLogit, which
+      // no fp16 logit reaches and whose e^{z - m} is 0, so the loops below need no validity
+      // test per element
+#define Z(e) acc[(e) / 16][nt][(e) % 16]
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e)
-        z[e] = static_cast<float>(cm::from_f32<_Float16>(acc[e / 16][nt][e % 16]));
+        Z(e) = mb + vrow(e) < n_voc ? static_cast<float>(cm::from_f32<_Float16>(Z(e))) : kNoLogit;
       // group max and first argmax over both halves of the wavefront (branch-free)
-      float m = -__builtin_huge_valf();
+      float m = kNoLogit;
       int best = -1;
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e) {
-        const bool take = mb + vrow(e) < n_voc && z[e] > m;
-        m = take ? z[e] : m;
+        const bool take = Z(e) > m;
+        m = take ? Z(e) : m;
         best = take ? mb + vrow(e) : best;
       }
       const float m_o = __shfl_xor(m, 32, cm::kWave);
       const int best_o = __shfl_xor(best, 32, cm::kWave);
       const bool other = m_o > m || (m_o == m && best_o >= 0 && (best < 0 || best_o < best));
-      const float mg = other ? m_o : m;
       best = other ? best_o : best;
-      // the label's logit, if this lane holds it (rare: a divergent branch around the search)
+      // a group with no usable logit: every e^{z - mg} below is then 0
+      const float mg = best < 0 ? __builtin_huge_valf() : (other ? m_o : m);
+      // The token's label falls in this group (rare): both lanes of the token copy their 64
+      // fp16 logits out, and K2 takes the label's logit and the group's sum over its other
+      // columns from them (that sum, kept apart from the label's term, is exact where the
+      // label dominates its group; forming it here raised the live set past the register file).
       const int64_t local = tgt[nt] - c0 - mb;
-      const bool holds_label = tok_ok && local >= 0 && local < kGroup &&
-                               ((local % 8) / 4) == half_id && mb + local < n_voc;
-      if (holds_label) {
-        float zt = 0.0f;
+      if (tok_ok && local >= 0 && local < kGroup && mb + local < n_voc) {
+        _Float16* dst = label_z + (static_cast<int64_t>(tok) * 2 + half_id) * (TM * 16);
 #pragma unroll
-        for (int e = 0; e < TM * 16; ++e) zt = vrow(e) == local ? z[e] : zt;
-        label_logit[tok] = zt;
+        for (int e = 0; e < TM * 16; e += 4) {
+          union {
+            uint2 u;
+            _Float16 h[4];
+          } pk;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pk.h[j] = static_cast<_Float16>(Z(e + j));  // exact
+          *reinterpret_cast<uint2*>(dst + e) = pk.u;
+        }
       }
       // E = e^{z - m_g} (in place of z) and the sums, relative to the group max
       float s = 0.0f, d = 0.0f;
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e) {
-        const bool ok = mb + vrow(e) < n_voc;
-        const float x = ok ? cm::exp_f(z[e] - mg) : 0.0f;
+        const float x = cm::exp_f(Z(e) - mg);  // 0 for kNoLogit rows, so x z = -0 there
         s += x;
-        d += ok ? x * z[e] : 0.0f;
-        z[e] = x;
+        d += x * Z(e);
+        Z(e) = x;
       }
-      const float s_other = __shfl_xor(s, 32, cm::kWave);
-      if (holds_label) {
-        // the group's sum without the label's own term, summed term by term (subtracting the
-        // label's term from s would cancel when the label dominates its group)
-        float own = 0.0f;
-#pragma unroll
-        for (int e = 0; e < TM * 16; ++e) own += vrow(e) == local ? 0.0f : z[e];
-        label_off[tok] = own + s_other;
-      }
-      s += s_other;
+      s += __shfl_xor(s, 32, cm::kWave);
       d += __shfl_xor(d, 32, cm::kWave);
       if (store) {
         // stage: 4 consecutive vocabulary rows (8 bytes) per (mt, q)
@@ -198,16 +203,17 @@ struct EpiProbs {
               _Float16 h[4];
             } pk;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pk.h[j] = cm::from_f32<_Float16>(z[mt * 16 + q * 4 + j]);
+            for (int j = 0; j < 4; ++j) pk.h[j] = cm::from_f32<_Float16>(Z(mt * 16 + q * 4 + j));
             const int v = mb - m0 + mt * 32 + q * 8 + half_id * 4;  // tile-local vocabulary row
             uint2* dst = reinterpret_cast<uint2*>(lds + stage_slot(v / 64, t, (v % 64) / 8));
             dst[half_id] = pk.u;
           }
         }
       }
+#undef Z
       if (half_id == 0 && tok_ok) {
         Partial p;
-        p.max = mg;
+        p.max = best < 0 ? -__builtin_huge_valf() : mg;
         p.sum = s;
         p.dot = d;
         p.best = best >= 0 ? static_cast<int32_t>(c0 + best) : -1;
@@ -332,10 +338,9 @@ struct RowState {
   float* label_logit;
   float* lse;     // running log-sum-exp after the last merged chunk
   float* factor;  // e^{lse_before - lse_after} of the last merged chunk
-  float* off;        // running sum of e^{z - max} over the columns other than the label
-  float* label_off;  // K1 -> K2: the label group's sum over its other columns
+  float* off;  // running sum of e^{z - max} over the columns other than the label
 };
-constexpr int kRowArrays = 9;  // row-state arrays in the workspace, one per field
+constexpr int kRowArrays = 8;  // row-state arrays in the workspace, one per field
 static_assert(sizeof(RowState) == kRowArrays * sizeof(void*),
               "RowState holds exactly one workspace array per field");
 
@@ -352,7 +357,6 @@ RowState row_state(char* base, int64_t stride) {
   r.lse = at(5);
   r.factor = at(6);
   r.off = at(7);
-  r.label_off = at(8);
   return r;
 }
 
@@ -412,19 +416,44 @@ __device__ __forceinline__ OffState block_merge_off(OffState s, OffState* part) 
 __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
     const Partial* __restrict__ part, int n_groups, RowState rs,
     const int64_t* __restrict__ target, int n_tok, int64_t c0, int n_voc, int first,
-    float* __restrict__ scale, _Float16* __restrict__ e16) {
+    float* __restrict__ scale, _Float16* __restrict__ e16, const _Float16* __restrict__ label_z) {
   const int row = blockIdx.x;
   const int64_t t = target[row];
   const bool labelled = t != -100;
   // the label's statistics group in this chunk, or -1
   const int64_t g_label = t >= c0 && t < c0 + n_voc ? (t - c0) / kGroup : -1;
+  // From the label group's 128 fp16 logits (K1 copied them out lane by lane: entry e of the
+  // lane in half h is group row (e/16)*32 + ((e%16)/4)*8 + 4h + e%4): the label's logit and the
+  // group's sum of e^{z - m_g} over its other columns, relative to the group max as K1's sums
+  // are. Rows past the chunk hold -inf.
+  __shared__ float s_red[kStatThreads / cm::kWave];
+  __shared__ float s_zt;
+  float label_off = 0.0f;
+  if (g_label >= 0) {  // uniform over the workgroup
+    const int local = static_cast<int>(t - c0 - g_label * kGroup);
+    const float mg = part[static_cast<int64_t>(row) * n_groups + g_label].max;
+    float v = 0.0f;
+    if (threadIdx.x < 2 * kEpiRows) {
+      const int h = threadIdx.x / kEpiRows, e = threadIdx.x % kEpiRows;
+      const int r = (e / 16) * 32 + ((e % 16) / 4) * 8 + h * 4 + e % 4;
+      const float z = static_cast<float>(label_z[static_cast<int64_t>(row) * 2 * kEpiRows +
+                                                 threadIdx.x]);
+      if (r == local) s_zt = z;
+      else v = cm::exp_f(z - mg);
+    }
+    v = cm::wave_sum(v);
+    if (threadIdx.x % cm::kWave == 0) s_red[threadIdx.x / cm::kWave] = v;
+    __syncthreads();
+    for (int w = 0; w < kStatThreads / cm::kWave; ++w) label_off += s_red[w];
+    if (threadIdx.x == 0) rs.label_logit[row] = s_zt;
+  }
   OffState acc = OffState::empty();
   const int n_valid = (n_voc + kGroup - 1) / kGroup;  // groups K1 wrote for this chunk
   for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
     const Partial p = part[static_cast<int64_t>(row) * n_groups + g];
     if (p.best >= 0) {
       OffState q{{p.max, p.sum, p.dot, static_cast<int64_t>(p.best)},
-                 g == g_label ? rs.label_off[row] : p.sum};
+                 g == g_label ? label_off : p.sum};
       acc.merge(q);
     }
   }
@@ -547,7 +576,7 @@ int n_split_for(int64_t n_rows, int hidden) {
 struct Layout {
   int64_t chunk, n_groups;
   int n_split;
-  int64_t off_e16, off_part, off_rows, off_scale, off_g, off_wt, total;
+  int64_t off_e16, off_part, off_rows, off_labz, off_scale, off_g, off_wt, total;
 };
 
 Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad,
@@ -564,6 +593,8 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   off += round_up(n_rows * L.n_groups * static_cast<int64_t>(sizeof(Partial)), 256);
   L.off_rows = off;
   off += kRowArrays * round_up(n_rows * 4, 256);
+  L.off_labz = off;
+  off += round_up(n_rows * 2 * kEpiRows * 2, 256);
   L.off_scale = off;
   off += round_up(n_rows * L.n_groups * 4, 256);
   L.off_g = off;
@@ -611,6 +642,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
   float* scale = want_grad ? reinterpret_cast<float*>(ws + L.off_scale) : nullptr;
   const RowState rs = row_state(ws + L.off_rows, round_up(n_rows * 4, 256));
   if (!complete(rs)) return static_cast<int>(hipErrorInvalidValue);
+  _Float16* label_z = reinterpret_cast<_Float16*>(ws + L.off_labz);
   GradSlices gs{};
   gs.g[0] = grad;
   for (int i = 1; i < L.n_split; ++i)
@@ -631,7 +663,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
       RowMajor A{W16 + c0 * ld_w, ld_w, n_voc, hidden_size};
       RowMajor B{H16, ld_h, n_tok, hidden_size};
       EpiProbs epi{e16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups), target,
-                   rs.label_logit, rs.label_off, want_grad ? 1 : 0, {}};  // tgt: prepare()
+                   label_z, want_grad ? 1 : 0, {}};  // tgt: prepare()
       hipLaunchKernelGGL((lmh_gemm1<EpiProbs, kBM1, kBN1, kWM1, kWN1, kBK1, kST1, kOcc1>), dim3(grid),
                          dim3(kThreads1), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
       int st = cm::launch_status();
@@ -640,7 +672,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     // K2: running statistics and the group scales
     hipLaunchKernelGGL(lmh_rows_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, part,
                        static_cast<int>(L.n_groups), rs, target, n_tok, c0, n_voc,
-                       first ? 1 : 0, scale, e16);
+                       first ? 1 : 0, scale, e16, label_z);
     int st = cm::launch_status();
     if (st) return st;
     if (!want_grad) continue;

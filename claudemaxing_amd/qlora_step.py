@@ -241,6 +241,41 @@ def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
                 losses=[float(x) for x in losses])
 
 
+def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, graphed=False):
+    """Per-step wall times (ms) over a fresh batch every step (new U[64, 512] lengths, so the
+    packed shape changes every step, as in SFT), each step between two device syncs, with TRL's
+    three metrics computed every step as its compute_loss does. With graphed, every step
+    captures a new GraphedStep for its batch and replays it once: the capture (and its warm-up
+    passes) is inside the timed step. Returns the median, the times, the real tokens per step
+    and the peak HBM."""
+    def batch_of(i):
+        return make_batch(next(model.parameters()).device, seed=seed0 + i)
+
+    def run(batch):
+        if graphed:
+            return GraphedStep(model, opt, scaler, batch, warmup=1).step()
+        return train_step(model, opt, scaler, batch, metrics={})
+
+    for i in range(warmup):
+        run(batch_of(i)[0])
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    times, tokens = [], []
+    for i in range(steps):
+        batch, lengths = batch_of(warmup + i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run(batch)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+        tokens.append(int(lengths.sum()))
+    ordered = sorted(times)
+    return dict(median_ms=ordered[len(ordered) // 2], step_ms=times, tokens=tokens,
+                tokens_per_s=sum(tokens) / (sum(times) * 1e-3),
+                peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
+                peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30)
+
+
 @contextlib.contextmanager
 def unpatched():
     """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, attention block, causal-LM
