@@ -28,8 +28,11 @@ def gemm_f32_supported(m, n, *pairs):
     contractions multiples of 8, on the GPU, and an output of a multiple of 4 elements."""
     if not pairs or len(pairs) > 2 or (m * n) % 4:
         return False
+    dev = pairs[0][0].device
     for a, b in pairs:
-        if _operand(a) is None or _operand(b) is None or not a.is_cuda:
+        if _operand(a) is None or _operand(b) is None:
+            return False
+        if not (a.is_cuda and b.is_cuda and a.device == dev and b.device == dev):
             return False
         if a.shape[0] != m or b.shape[0] != n or a.shape[1] != b.shape[1]:
             return False
