@@ -253,6 +253,110 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_kernel(
   }
 }
 
+// Forward for rows of NV * 512 columns: the lane's x vectors and weight vectors are loaded
+// together before any arithmetic (one memory round trip per row); with `low16` the fp16 copy of
+// the output is written beside it (the case without tiny-|w| columns to keep apart).
+template <typename XT, typename WT, typename OT, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_full_kernel(
+    const XT* __restrict__ x, int64_t x_stride, const WT* __restrict__ w, OT* __restrict__ out,
+    float* __restrict__ rstd, _Float16* __restrict__ low16, int64_t n_rows, int n_cols,
+    float eps) {
+  constexpr int VEC = 8;
+  const int lane = threadIdx.x % cm::kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / cm::kWave;
+  if (row >= n_rows) return;
+  const XT* xr = x + row * x_stride + lane * VEC;
+  float xv[NV][VEC], wv[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    cm::Vec8<XT, true>::load(xr + i * cm::kWave * VEC, xv[i]);
+    cm::Vec8<WT, true>::load(w + i * cm::kWave * VEC + lane * VEC, wv[i]);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) ss += xv[i][k] * xv[i][k];
+  ss = cm::wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+  const int64_t obase = row * static_cast<int64_t>(n_cols) + lane * VEC;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = cm::round_to<XT>(xv[i][k] * r) * wv[i][k];
+    cm::Vec8<OT, true>::store(out + obase + i * cm::kWave * VEC, o);
+    if (low16 != nullptr) cm::Vec8<_Float16, true>::store(low16 + obase + i * cm::kWave * VEC, o);
+  }
+}
+
+// Backward for rows of NV * 512 columns (full 16-byte vectors everywhere), the Qwen2 shapes:
+// a wavefront keeps its lane's weight columns in registers across its rows, and issues every
+// load of a row (dy, x or the saved fp16 output, rstd) before any arithmetic, so a row costs one
+// memory round trip (the general kernel's per-vector length tests made each load wait for the
+// previous one). SAVED: xs holds the fp16 copy of the output and normed = copy / w, gn = dy * w
+// (the path of fp32 x with a frozen fp32 weight and no tiny-|w| column); otherwise xs holds x,
+// normed = x * rstd and gn = round_x(dy * w).
+template <typename DT, typename XT, typename WT, typename DXT, int NV, bool SAVED>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_full_kernel(
+    const DT* __restrict__ dy, const void* __restrict__ xs_v, const WT* __restrict__ w,
+    const float* __restrict__ rstd, DXT* __restrict__ dx, float* __restrict__ dw_partial,
+    int64_t n_rows, int n_cols) {
+  constexpr int VEC = 8;
+  using SrcT = typename std::conditional<SAVED, _Float16, XT>::type;
+  const int lane = threadIdx.x % cm::kWave;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / cm::kWave;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
+  const SrcT* xs = static_cast<const SrcT*>(xs_v);
+  const bool want_dw = dw_partial != nullptr;
+  float wv[NV][VEC], dwacc[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    cm::Vec8<WT, true>::load(w + i * cm::kWave * VEC + lane * VEC, wv[i]);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) dwacc[i][k] = 0.0f;
+  }
+  for (int64_t row = wave; row < n_rows; row += n_waves) {
+    const int64_t base = row * static_cast<int64_t>(n_cols) + lane * VEC;
+    const float r = rstd[row];
+    float d[NV][VEC], v[NV][VEC];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      cm::Vec8<DT, true>::load(dy + base + i * cm::kWave * VEC, d[i]);
+      cm::Vec8<SrcT, true>::load(xs + base + i * cm::kWave * VEC, v[i]);
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float nv = SAVED ? v[i][k] / wv[i][k] : v[i][k] * r;
+        const float gv = SAVED ? d[i][k] * wv[i][k] : cm::round_to<XT>(d[i][k] * wv[i][k]);
+        if (!SAVED && want_dw) dwacc[i][k] += d[i][k] * cm::round_to<XT>(nv);
+        dot += gv * nv;
+        v[i][k] = nv;
+        d[i][k] = gv;
+      }
+    }
+    const float mean_dot = cm::wave_sum(dot) / static_cast<float>(n_cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) o[k] = (d[i][k] - v[i][k] * mean_dot) * r;
+      cm::Vec8<DXT, true>::store(dx + base + i * cm::kWave * VEC, o);
+    }
+  }
+  if (want_dw) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      cm::Vec8<float, true>::store(dw_partial + wave * static_cast<int64_t>(n_cols) +
+                                       i * cm::kWave * VEC + lane * VEC,
+                                   dwacc[i]);
+  }
+}
+
 // torch.promote_types over the three float dtypes: equal types stay, anything else is fp32
 // (fp16 with bf16 promotes to fp32 as well).
 int promote(int a, int b) { return a == b ? a : CM_F32; }
@@ -304,9 +408,17 @@ extern "C" int cm_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, 
   const int nv = pick_nv(n_cols, vec);
   // The output dtype is torch.promote_types(x, w), as in the reference.
   CM_CHECK_ARG(out_dtype == promote(x_dtype, w_dtype));
+  // rows of whole 512-column vectors and no tiny-|w| column to keep apart: one round trip a row
+  const bool full = v8 && nv > 0 && n_cols % (cm::kWave * 8) == 0 && (!low16 || n_small == 0);
   CM_FLOAT_SWITCH(x_dtype, XT, CM_FLOAT_SWITCH(w_dtype, WT, {
     using OT = Promoted<XT, WT>;
-    if (v8) {
+    if (full) {
+      CM_NV_SWITCH(nv, NV, if constexpr (NV > 0) hipLaunchKernelGGL(
+                               (rmsnorm_fwd_full_kernel<XT, WT, OT, NV>), dim3(blocks),
+                               dim3(kThreads), 0, s, static_cast<const XT*>(x), x_row_stride,
+                               static_cast<const WT*>(w), static_cast<OT*>(out), rstd,
+                               static_cast<_Float16*>(low16), n_rows, n_cols, eps));
+    } else if (v8) {
       CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_fwd_kernel<XT, WT, OT, 8, NV>),
                                               dim3(blocks), dim3(kThreads), 0, s,
                                               static_cast<const XT*>(x), x_row_stride,
@@ -353,10 +465,26 @@ extern "C" int cm_rmsnorm_bwd(const void* dy, int dy_dtype, const void* xs, int 
   const int x_dtype = saved_output ? dx_dtype : xs_dtype;
   // dx has the dtype of x; dy the dtype of the forward output, promote(x, w).
   CM_CHECK_ARG(dx_dtype == x_dtype && dy_dtype == promote(x_dtype, w_dtype));
+  // rows of whole 512-column vectors, no tiny-|w| column map to read: the one-round-trip kernel
+  const bool full = v8 && nv > 0 && n_cols % (cm::kWave * 8) == 0 && (!saved_output || n_small == 0);
   CM_FLOAT_SWITCH(x_dtype, XT, CM_FLOAT_SWITCH(w_dtype, WT, {
     using DT = Promoted<XT, WT>;
     using DXT = XT;
-    {
+    if (full) {
+      if (saved_output) {
+        CM_NV_SWITCH(nv, NV, if constexpr (NV > 0) hipLaunchKernelGGL(
+                                 (rmsnorm_bwd_full_kernel<DT, XT, WT, DXT, NV, true>),
+                                 dim3(blocks), dim3(kThreads), 0, s, static_cast<const DT*>(dy),
+                                 xs, static_cast<const WT*>(w), rstd, static_cast<DXT*>(dx),
+                                 dw_partial, n_rows, n_cols));
+      } else {
+        CM_NV_SWITCH(nv, NV, if constexpr (NV > 0) hipLaunchKernelGGL(
+                                 (rmsnorm_bwd_full_kernel<DT, XT, WT, DXT, NV, false>),
+                                 dim3(blocks), dim3(kThreads), 0, s, static_cast<const DT*>(dy),
+                                 xs, static_cast<const WT*>(w), rstd, static_cast<DXT*>(dx),
+                                 dw_partial, n_rows, n_cols));
+      }
+    } else {
       if (v8) {
         CM_NV_SWITCH(nv, NV, hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, XT, WT, DXT, 8, NV>),
                                                 dim3(blocks), dim3(kThreads), 0, s,

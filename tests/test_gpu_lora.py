@@ -33,6 +33,37 @@ def test_pack_unpack_match_oracle(n, x_dtype, dev):
     assert_bits_equal(dx, torch.from_numpy(udx), "unpack dx")
 
 
+@pytest.mark.parametrize("dx_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("in_off,dx_off", [(0, 0), (1, 0), (0, 1), (0, 2), (4, 4)])
+def test_unpack_gradient_dtypes_and_misaligned_buffers(dx_dtype, in_off, dx_off, dev):
+    """cm_lora_unpack called directly on buffers that start in_off / dx_off elements into their
+    storage (2-, 4- and 8-byte offsets take the element-wise path), over whole workgroups and a
+    ragged tail, for every gradient dtype."""
+    from claudemaxing_amd import _lib
+
+    n = 4096 * 3 + 8 * 37
+    banner(f"lora unpack dx={dx_dtype} offsets x/g/xd {in_off} dx {dx_off}")
+    g = torch.Generator().manual_seed(11 + 3 * in_off + dx_off)
+    x16 = torch.randn(n, generator=g).half()
+    g16 = torch.randn(n, generator=g).half()
+    bits = torch.randint(0, 256, (n // 8,), generator=g, dtype=torch.uint8)
+    scale = 1.0 / 0.9
+
+    def placed(dtype, off, src=None):
+        buf = torch.zeros(n + off, dtype=dtype, device=dev)[off:]
+        return buf.copy_(src) if src is not None else buf
+
+    xs, gs = placed(torch.float16, in_off, x16), placed(torch.float16, in_off, g16)
+    xd, dx = placed(torch.float16, in_off), placed(dx_dtype, dx_off)
+    bd = bits.to(dev)
+    _lib.call("cm_lora_unpack", xs.data_ptr(), bd.data_ptr(), gs.data_ptr(), xd.data_ptr(),
+              dx.data_ptr(), _lib.dtype_code(dx_dtype), n, scale, _lib.stream(xs.device))
+    uxd, udx = O.unpack(x16.numpy(), bits.numpy(), g16.numpy(), scale, np.float32)
+    assert_bits_equal(xd, torch.from_numpy(uxd), "unpack xd")
+    # the gradient is formed in fp32 and rounded once to its dtype (round to nearest even)
+    assert_bits_equal(dx, torch.from_numpy(udx).to(dx_dtype), "unpack dx")
+
+
 def test_known_answer_closed_forms(dev):
     """tests_local/test_lora.py:24-33."""
     banner("lora known answer")
