@@ -29,6 +29,12 @@ struct EpiSlice {
   template <int TM, int TN>
   __device__ __forceinline__ void prepare(int, int, int) {}
   template <int TM, int TN>
+  __device__ __forceinline__ void start(floatx16 (&acc)[TM][TN], int mb, int nb, int lane) {
+    cm::gemm::ZeroStart::start<TM, TN>(acc, mb, nb, lane);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void started(floatx16 (&)[TM][TN]) {}
+  template <int TM, int TN>
   __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb, int lane,
                                         uint4*) const {
 #pragma unroll

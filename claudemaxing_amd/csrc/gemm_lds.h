@@ -17,8 +17,10 @@
 //
 // An A-fragment transform FX may rescale each 8-element A fragment between the LDS read and the
 // MFMA (used by the LM head's gradient GEMM to turn stored e^{z - m} into probabilities). The
-// epilogue's prepare() runs before the main loop (to issue its own loads early); apply() receives
-// the accumulators and the LDS ring, which it may reuse after a barrier.
+// epilogue's prepare() runs before the main loop (to issue its own loads early), start() gives
+// the accumulators their initial values (it may issue loads) and started() runs after the
+// prologue's loads; apply() receives the accumulators and the LDS ring, which it may reuse
+// after a barrier. ZeroStart is the plain start (zero accumulators).
 #pragma once
 
 #include "common.h"
@@ -59,49 +61,71 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// LDS tile rows of BK fp16 = BK / 8 chunks of 16 bytes. Physical chunk = logical chunk ^
-// swz(row), chosen for the 64 banks of 4 bytes of the gfx950 LDS: a ds_read_b128 is served 16
-// lanes (256 bytes) at a time, and the 16 lanes of a fragment read are 16 consecutive rows at
-// one logical chunk, so those rows must land in 16 distinct 16-byte bank groups. With 8-chunk
-// rows the row parity already picks the half of the 256-byte bank span and (row >> 1) & 7 the
-// chunk; with 4-chunk rows row & 3 picks the quarter and (row >> 2) & 3 the chunk.
-template <int BK>
-struct LdsRows {
+// LDS operand tiles of ROWS rows x BK fp16 columns = BK / 8 chunks of 16 bytes per row, in one of
+// two layouts, chosen per operand by its source layout (Src::kChunkMajor):
+//  - row-major (CM = false): slot row * kRC + (chunk ^ swz(row)). The XOR swizzle is chosen for
+//    the 64 banks of 4 bytes of the gfx950 LDS: a ds_read_b128 is served 16 lanes (256 bytes)
+//    at a time, and the 16 lanes of a fragment read are 16 consecutive rows at one logical
+//    chunk, so those rows must land in 16 distinct 16-byte bank groups. With 8-chunk rows the
+//    row parity already picks the half of the 256-byte bank span and (row >> 1) & 7 the chunk;
+//    with 4-chunk rows row & 3 picks the quarter and (row >> 2) & 3 the chunk. A wavefront's
+//    direct load then fetches 8 rows x 128 bytes, the right shape for row-contiguous sources.
+//  - chunk-major (CM = true): slot chunk * ROWS + row. A fragment read's 16 rows are 16
+//    consecutive slots (conflict-free with no swizzle), and a wavefront's direct load fetches 64
+//    consecutive rows at one chunk: two 512-byte spans of a Tiled32 source.
+template <int BK, bool CM, int ROWS>
+struct LdsTile {
   static constexpr int kRC = BK / 8;
   static_assert(kRC == 8 || kRC == 4, "stages of 64 or 32 columns");
   static __device__ __forceinline__ int swz(int row) {
     return kRC == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
   }
+  static __device__ __forceinline__ int slot(int row, int ch) {
+    return CM ? ch * ROWS + row : row * kRC + (ch ^ swz(row));
+  }
   static __device__ __forceinline__ half8 frag(const uint4* lds, int row, int ch) {
-    return __builtin_bit_cast(half8, lds[row * kRC + (ch ^ swz(row))]);
+    return __builtin_bit_cast(half8, lds[slot(row, ch)]);
   }
 };
 
-// Direct loads of one ROWS x BK operand tile by NW wavefronts. Instruction i of a lane fetches
-// chunk c = (i * NW + wave) * 64 + lane of the tile: row row0 + i * kRowStep, and (with NW >= 2)
-// the same swizzled column for every i, since kRowStep is a multiple of the swizzle's period.
-// So a lane keeps one byte offset from the stage origin, and instruction i adds i times a
-// wave-uniform row step; a stage's origin is a wave-uniform pointer. Tiles that are wholly
-// inside the operand take that path; the others select the zero chunk per lane.
-template <int ROWS, int NW, int BK>
+// The row-major layout on its own (its slots do not depend on the tile's row count).
+template <int BK>
+using LdsRows = LdsTile<BK, false, 0>;
+
+// Direct loads of one ROWS x BK operand tile by NW wavefronts. Instruction i of a lane fills
+// LDS slot (i * NW + wave) * 64 + lane of the tile. Row-major: row row0 + i * kRowStep and (with
+// NW >= 2) the same swizzled column for every i, since kRowStep is a multiple of the swizzle's
+// period. Chunk-major: row row0 and column col0 + 8 i * kColStep. Either way a lane keeps one
+// byte offset from the stage origin, and instruction i adds i times a wave-uniform step; a
+// stage's origin is a wave-uniform pointer. Tiles that are wholly inside the operand take that
+// path; the others select the zero chunk per lane.
+template <int ROWS, int NW, int BK, bool CM = false>
 struct DmaTile {
-  using L = LdsRows<BK>;
+  using L = LdsTile<BK, CM, ROWS>;
   static constexpr int kChunks = ROWS * L::kRC;
   static constexpr int kPer = kChunks / (NW * kWave);  // instructions per lane
-  static constexpr int kRowStep = NW * kWave / L::kRC;  // tile rows between instructions
+  static constexpr int kRowStep = CM ? 0 : NW * kWave / L::kRC;  // tile rows between them
+  static constexpr int kColStep = CM ? NW * kWave / ROWS : 0;    // chunks between them
   static_assert(kPer * NW * kWave == kChunks, "tile chunks must split over the wavefronts");
-  static_assert(NW >= 2, "one swizzled column per lane needs a row step of 16 or more");
+  static_assert(CM || NW >= 2, "one swizzled column per lane needs a row step of 16 or more");
+  static_assert(!CM || kColStep * ROWS == NW * kWave, "an instruction covers whole chunk columns");
   uint32_t off0;      // byte offset of the lane's chunk of instruction 0 from the stage origin
   uint32_t step;      // bytes between instructions (wave-uniform)
-  int row0, col0;     // tile row of instruction 0 and column of every chunk of the lane
+  int row0, col0;     // tile row and column of the lane's chunk of instruction 0
 
   template <class Src>
   __device__ __forceinline__ void init(const Src& src, int wave, int lane) {
     const int c = wave * kWave + lane;
-    row0 = c / L::kRC;
-    col0 = ((c % L::kRC) ^ L::swz(row0)) * 8;
+    if (CM) {
+      row0 = c % ROWS;
+      col0 = (c / ROWS) * 8;
+      step = src.tile_offset(0, kColStep * 8);
+    } else {
+      row0 = c / L::kRC;
+      col0 = ((c % L::kRC) ^ L::swz(row0)) * 8;
+      step = src.tile_offset(kRowStep, 0);
+    }
     off0 = src.tile_offset(row0, col0);
-    step = src.tile_offset(kRowStep, 0);
   }
 
   // Instruction i of the stage whose origin is (r0, k0); `inside` = the tile is wholly inside
@@ -110,7 +134,8 @@ struct DmaTile {
   __device__ __forceinline__ void issue(const Src& src, int r0, int k0, uint4* tile, int wave,
                                         int i, bool inside) const {
     const char* base = reinterpret_cast<const char*>(src.at(r0, k0));
-    const bool ok = inside || (r0 + row0 + i * kRowStep < src.rows && src.col_ok(k0 + col0));
+    const int row = row0 + i * kRowStep, col = col0 + i * kColStep * 8;
+    const bool ok = inside || (r0 + row < src.rows && src.col_ok(k0 + col));
     const void* g = ok ? static_cast<const void*>(base + off0 + i * step)
                        : static_cast<const void*>(kZeroChunk);
     dma16(g, tile + (i * NW + wave) * kWave);
@@ -124,6 +149,21 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// Accumulators starting at zero, for epilogues with nothing to add to the product.
+struct ZeroStart {
+  template <int TM, int TN>
+  static __device__ __forceinline__ void start(floatx16 (&acc)[TM][TN], int, int, int) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  }
+  template <int TM, int TN>
+  static __device__ __forceinline__ void started(floatx16 (&)[TM][TN]) {}
+};
 
 // Identity A-fragment transform with no per-stage data (the default FX of gemm_lds). An FX
 // provides bind(row) (the A row of the calling lane's fragment 0; fragment i is row + 32 i),
@@ -154,13 +194,14 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  using L = LdsRows<BK>;
+  using LA = LdsTile<BK, SrcA::kChunkMajor, BM>;
+  using LB = LdsTile<BK, SrcB::kChunkMajor, BN>;
   constexpr int KS = BK / 16;  // MFMA substeps per stage
   static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles are multiples of 32");
   static_assert(S >= 2, "at least a double buffer");
-  constexpr int kStage = (BM + BN) * L::kRC;  // uint4 per stage
-  using TA = DmaTile<BM, NW, BK>;
-  using TB = DmaTile<BN, NW, BK>;
+  constexpr int kStage = (BM + BN) * LA::kRC;  // uint4 per stage
+  using TA = DmaTile<BM, NW, BK, SrcA::kChunkMajor>;
+  using TB = DmaTile<BN, NW, BK, SrcB::kChunkMajor>;
   constexpr int kDma = TA::kPer + TB::kPer;     // LDS-direct loads per lane per stage
   constexpr int kPart = (kDma + KS - 1) / KS;   // of them issued per substep
   constexpr int kHalf = (TM * TN) / 2;          // MFMAs before the loads of a substep
@@ -174,13 +215,10 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
   lb.init(B, wave, lane);
   epi.template prepare<TM, TN>(m0 + wm * WTM, n0 + wn * WTN, lane);
 
+  // The epilogue's start() sets the accumulators (zero, or loads issued here so that they are
+  // in flight with the first stage's loads); started() runs once the first stage has landed.
   floatx16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  epi.template start<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
 
   const int n_kt = (k_end - k_begin + BK - 1) / BK;
   // load instruction q (< kDma) of stage kt: A's instructions first, then B's
@@ -190,7 +228,7 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
     if (q < TA::kPer) {
       la.issue(A, m0, k0, st, wave, q, in_a);
     } else {
-      lb.issue(B, n0, k0, st + BM * L::kRC, wave, q - TA::kPer, in_b);
+      lb.issue(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer, in_b);
     }
   };
   auto inside_a = [&](int kt) { return A.tile_inside(m0, BM, k_begin + kt * BK); };
@@ -199,12 +237,12 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
   half8 af[2][TM], bf[2][TN];
   auto read = [&](int kt, int ks, int buf) {
     const uint4* As = lds + (kt % S) * kStage;
-    const uint4* Bs = As + BM * L::kRC;
+    const uint4* Bs = As + BM * LA::kRC;
     const int ch = ks * 2 + lane / 32;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[buf][i] = fx.apply(L::frag(As, arow + i * 32, ch), i);
+    for (int i = 0; i < TM; ++i) af[buf][i] = fx.apply(LA::frag(As, arow + i * 32, ch), i);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bf[buf][j] = L::frag(Bs, brow + j * 32, ch);
+    for (int j = 0; j < TN; ++j) bf[buf][j] = LB::frag(Bs, brow + j * 32, ch);
   };
   // Scheduling of a group "fragment reads of the next substep + first half of the MFMAs":
   // one LDS read, one MFMA, alternately (measured 1.5% faster on the LM head than all reads
@@ -235,6 +273,9 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
       for (int q = 0; q < kDma; ++q) issue(s, q, ia, ib);
     }
   }
+
+  // Waits for the prologue's loads (the first stage and whatever start() issued).
+  epi.template started<TM, TN>(acc);
 
   // The last substep of stage kt - 1 is multiplied after the barrier of stage kt: its fragments
   // are already in registers, so its MFMAs cover the latency of the first fragment reads of

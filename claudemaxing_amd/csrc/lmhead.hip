@@ -25,10 +25,10 @@
 //               + (p_t - 1) W_t): K2 zeroes the label's entry of E, so the label's coefficient
 //               is applied only here, in fp32.
 //
-// The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 1 GiB) lives in the
-// workspace. The chunk and the transposed weight are stored in 64-column panels
-// ([C/64][tokens][64], [V/64][H][64]) so that every K3 operand tile is one contiguous 16 KiB
-// read.
+// The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 128 MiB by default)
+// lives in the workspace, in 4 KiB blocks of 32 tokens x 64 columns (Tiled32), and the transposed
+// weight in 64-column panels ([V/64][H][64]), so that every K3 operand tile is one contiguous
+// span.
 #include <mutex>
 
 #include "common.h"
@@ -40,7 +40,9 @@ namespace {
 using cm::gemm::Blocked64;
 using cm::gemm::floatx16;
 using cm::gemm::half8;
+using cm::gemm::Tiled32;
 using cm::gemm::RowMajor;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int kPanel = 64;          // columns per panel of the blocked layouts
 // Logit given to vocabulary rows past a chunk's last column in K1's epilogue: below every fp16
@@ -49,6 +51,7 @@ constexpr float kNoLogit = -3.0e38f;
 constexpr float kPScale = 1024.0f;  // P16 = fp16(p * kPScale)
 constexpr int kStatThreads = 256;
 constexpr int kMaxSplit = 8;
+constexpr int kRowsPerBlock = 4;  // K2: token rows (one wavefront each) per workgroup
 
 // Tile configurations: BM, BN, wavefront grid WM x WN, stage depth BK, LDS ring stages, and the
 // minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront:
@@ -77,10 +80,11 @@ constexpr int kThreads3 = kWM3 * kWN3 * cm::kWave;
 constexpr int kGroup = kBM1 / kWM1;  // vocabulary columns per partial-statistics group
 constexpr int kEpiRows = kGroup / 2;  // group rows one lane of K1's epilogue holds per token
 static_assert(kGroup % kPanel == 0, "a statistics group is whole panels");
+// K2 holds a row's partials in registers, at most 32 per lane: a chunk has at most 64 * 32
+// statistics groups.
+constexpr int kMaxRowSlots = 32;
+constexpr int64_t kMaxChunk = int64_t{64} * kMaxRowSlots * kGroup;
 
-__device__ __forceinline__ int64_t panel_index(int64_t row, int64_t col, int64_t rows) {
-  return ((col / kPanel) * rows + row) * kPanel + col % kPanel;
-}
 
 // Partial statistics of one (token, group): group max, sum e^{z - max}, sum e^{z - max} z, first
 // argmax as a vocabulary index (-1 when the group holds no valid column).
@@ -91,13 +95,17 @@ struct Partial {
 
 // ---------------------------------------------------------------------------------------------
 // K1 epilogue: the tile is Z^T (rows = vocabulary columns of the chunk, cols = tokens). A
-// wavefront's rows are one statistics group of kGroup columns. E is staged in the LDS in the
-// output's panel layout and written with 16-byte stores, 1 KiB contiguous per wavefront
-// instruction: the tile's BM vocabulary rows are BM / 64 panels, and in each the BN tokens are one
-// contiguous span of BN x 128 bytes.
+// wavefront's rows are one statistics group of kGroup columns, and a lane holds the logits of
+// one token. E (layout Tiled32: 32 tokens x 64 columns per 4 KiB block, 8-column chunks inside)
+// is written straight from the registers: a lane's entries 4b .. 4b + 3 are rows 8b + 4h .. 8b + 4h + 3 of the group (h = the
+// lane's half of the wavefront), so after each pair of blocks (b, b + 1) trades halves across
+// the two 32-lane halves (v_permlane32_swap_b32: the first operand's upper 32 lanes swap with the
+// second operand's lower 32 lanes) lane l < 32 holds all 8 rows of block b and lane l + 32 those
+// of block b + 1. One 16-byte store each, 1 KiB contiguous per wavefront instruction, no LDS
+// staging and no barrier.
 struct EpiProbs {
   static constexpr int kTN = kBN1 / kWN1 / 32;
-  _Float16* e16;        // chunk of E = fp16(e^{z - m_g}), panels [C/64][n_tok][64]
+  _Float16* e16;        // chunk of E = fp16(e^{z - m_g}), layout Tiled32
   int n_tok;
   int n_voc;            // valid columns of the chunk
   int64_t c0;           // first vocabulary index of the chunk
@@ -106,13 +114,8 @@ struct EpiProbs {
   const int64_t* target;
   _Float16* label_z;    // [n_tok][2][64]: the label group's fp16 logits, lane by lane
   int store;            // write E (the gradient needs it)
+  int row_blocks;       // ceil(n_tok / 32), E's 32-token blocks per 64-column panel
   int64_t tgt[kTN];     // targets of the lane's tokens, loaded before the main loop
-
-  // 16-byte chunk slot of (token t, chunk c) within the staging rows of panel p: rows of 128
-  // bytes, chunk XOR-swizzled by the token so that 16 consecutive tokens hit distinct banks.
-  static __device__ __forceinline__ int stage_slot(int p, int t, int c) {
-    return (p * kBN1 + t) * 8 + (c ^ ((t >> 1) & 7));
-  }
 
   template <int TM, int TN>
   __device__ __forceinline__ void prepare(int, int nb, int lane) {
@@ -125,16 +128,19 @@ struct EpiProbs {
   }
 
   template <int TM, int TN>
+  __device__ __forceinline__ void start(floatx16 (&acc)[TM][TN], int mb, int nb, int lane) {
+    cm::gemm::ZeroStart::start<TM, TN>(acc, mb, nb, lane);
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void started(floatx16 (&)[TM][TN]) {}
+
+  template <int TM, int TN>
   __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb, int lane,
-                                        uint4* lds) {
+                                        uint4*) {
     static_assert(TM * 32 == kGroup, "a wavefront covers one statistics group");
-    static_assert(kBM1 * kBN1 * 2 <= kST1 * (kBM1 + kBN1) * kBK1 * 2,
-                  "the E tile is staged in the LDS ring");
     const int half_id = lane / 32;
-    const int m0 = mb - mb % kBM1, n0 = nb - nb % kBN1;  // tile origin
     // accumulator element e of a lane is vocabulary row mb + vrow(e)
     auto vrow = [&](int e) { return (e / 16) * 32 + ((e % 16) / 4) * 8 + half_id * 4 + e % 4; };
-    if (store) cm::gemm::lds_barrier();  // every wavefront is done reading the last stage
 #pragma unroll
     for (int nt = 0; nt < TN; ++nt) {
       const int tok = nb + nt * 32 + lane % 32;
@@ -192,22 +198,19 @@ struct EpiProbs {
       s += __shfl_xor(s, 32, cm::kWave);
       d += __shfl_xor(d, 32, cm::kWave);
       if (store) {
-        // stage: 4 consecutive vocabulary rows (8 bytes) per (mt, q)
-        const int t = tok - n0;
+        // entries 4b .. 4b + 3 = rows 8b + 4h .. 8b + 4h + 3 (vrow(4b) = 8b + 4h)
+        auto pack = [&](int e) {  // two fp16 of entries e, e + 1 as one dword
+          const half2v v{cm::from_f32<_Float16>(Z(e)), cm::from_f32<_Float16>(Z(e + 1))};
+          return __builtin_bit_cast(uint32_t, v);
+        };
 #pragma unroll
-        for (int mt = 0; mt < TM; ++mt) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            union {
-              uint2 u;
-              _Float16 h[4];
-            } pk;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) pk.h[j] = cm::from_f32<_Float16>(Z(mt * 16 + q * 4 + j));
-            const int v = mb - m0 + mt * 32 + q * 8 + half_id * 4;  // tile-local vocabulary row
-            uint2* dst = reinterpret_cast<uint2*>(lds + stage_slot(v / 64, t, (v % 64) / 8));
-            dst[half_id] = pk.u;
-          }
+        for (int b = 0; b < TM * 4; b += 2) {
+          const auto s0 = __builtin_amdgcn_permlane32_swap(pack(4 * b), pack(4 * b + 4), false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(pack(4 * b + 2), pack(4 * b + 6), false, false);
+          // lane l < 32: block b, rows 0-3 (its own) then 4-7; lane l + 32: block b + 1
+          const uint4 chunk{s0[0], s1[0], s0[1], s1[1]};
+          const int v = mb + 8 * (b + half_id);  // first vocabulary column (of the chunk)
+          if (tok_ok) *reinterpret_cast<uint4*>(e16 + Tiled32::index(tok, v, row_blocks)) = chunk;
         }
       }
 #undef Z
@@ -220,64 +223,83 @@ struct EpiProbs {
         part[static_cast<int64_t>(tok) * n_groups + mb / kGroup] = p;
       }
     }
-    if (!store) return;
-    cm::gemm::lds_barrier();
-    // copy out: slot = (p * BN + t) * 8 + physical chunk; 8 consecutive threads = one token row
-    constexpr int kSlots = kBM1 / 64 * kBN1 * 8;
-    for (int slot = threadIdx.x; slot < kSlots; slot += kThreads1) {
-      const int row = slot / 8, pc = slot % 8;
-      const int p = row / kBN1, t = row % kBN1;
-      if (n0 + t >= n_tok) continue;
-      const int c = pc ^ ((t >> 1) & 7);
-      const int64_t dst = ((static_cast<int64_t>((m0 / 64) + p) * n_tok + n0 + t) * 64) + c * 8;
-      *reinterpret_cast<uint4*>(e16 + dst) = lds[slot];
-    }
   }
 };
 
-// K3 epilogue: the tile is G (rows = tokens, cols = hidden units).
+// K3 epilogue: the tile is G (rows = tokens, cols = hidden units). On later chunks the
+// accumulators start from the slice's previous value times the row's rescale factor: start()
+// issues those loads (from clamped addresses, so without branches) ahead of the first stage's
+// loads, whose wait they share, and started() applies the factors; apply() then only stores. A
+// workgroup thus spends no round trip of its own on the read-modify-write of its slice.
 struct EpiGrad {
+  static constexpr int kMaxTM = 4;
   float* grad;          // [n_tok, hidden] fp32 accumulator of this K-slice
   int n_tok;
   int hidden;
   const float* factor;  // [n_tok]
   int first;            // first chunk: G = acc
+  float f[kMaxTM][16];  // factors of the lane's accumulator rows, loaded by start()
 
   template <int TM, int TN>
   __device__ __forceinline__ void prepare(int, int, int) {}
+
+  // token row of accumulator entry r of tile row mt, and hidden unit of tile column nt
+  static __device__ __forceinline__ int row_of(int mb, int mt, int r, int lane) {
+    return mb + mt * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
+  }
+  static __device__ __forceinline__ int col_of(int nb, int nt, int lane) {
+    return nb + nt * 32 + lane % 32;
+  }
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void start(floatx16 (&acc)[TM][TN], int mb, int nb, int lane) {
+    static_assert(TM <= kMaxTM, "factor rows of the wavefront tile");
+    if (first) {
+      cm::gemm::ZeroStart::start<TM, TN>(acc, mb, nb, lane);
+      return;
+    }
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tok = row_of(mb, mt, r, lane);
+        const int64_t row = tok < n_tok ? tok : 0;
+        f[mt][r] = factor[row];
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) {
+          const int h = col_of(nb, nt, lane);
+          acc[mt][nt][r] = grad[row * hidden + (h < hidden ? h : 0)];
+        }
+      }
+  }
+
+  template <int TM, int TN>
+  __device__ __forceinline__ void started(floatx16 (&acc)[TM][TN]) {
+    if (first) return;
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int nt = 0; nt < TN; ++nt) acc[mt][nt][r] *= f[mt][r];
+  }
 
   template <int TM, int TN>
   __device__ __forceinline__ void apply(floatx16 (&acc)[TM][TN], int mb, int nb, int lane,
                                         uint4*) const {
 #pragma unroll
-    for (int mt = 0; mt < TM; ++mt) {
+    for (int mt = 0; mt < TM; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int tok = mb + mt * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);
-        if (tok >= n_tok) continue;
-        const float f = first ? 0.0f : factor[tok];
+        const int tok = row_of(mb, mt, r, lane);
 #pragma unroll
         for (int nt = 0; nt < TN; ++nt) {
-          const int h = nb + nt * 32 + lane % 32;
-          if (h >= hidden) continue;
-          float* g = grad + static_cast<int64_t>(tok) * hidden + h;
-          *g = first ? acc[mt][nt][r] : *g * f + acc[mt][nt][r];
+          const int h = col_of(nb, nt, lane);
+          if (tok < n_tok && h < hidden) grad[static_cast<int64_t>(tok) * hidden + h] = acc[mt][nt][r];
         }
       }
-    }
   }
 };
-
-// __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD, which caps
-// the registers per wavefront accordingly.
-template <class Epi, int BM, int BN, int WM, int WN, int BK, int ST, int OCC>
-__global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm1(RowMajor A, RowMajor B,
-                                                                       int remap, Epi epi) {
-  __shared__ uint4 lds[ST * (BM + BN) * (BK / 8)];
-  int tm, tn;
-  cm::gemm::tile_of_block((B.rows + BN - 1) / BN, remap, tm, tn);
-  cm::gemm::gemm_lds<BM, BN, WM, WN, BK, ST>(A, B, 0, A.k_len, tm, tn, epi, lds);
-}
 
 // K3's A-fragment transform: E (fp16 e^{z - m_g}) times the (token, group) scale
 // s_g = e^{m_g - lse} * 1024 (0 for unlabelled tokens) gives P16 = e^{z - lse} * 1024. The
@@ -307,25 +329,68 @@ struct ScaleP {
   __device__ __forceinline__ half8 apply(half8 f, int i) const { return f * cur[i]; }
 };
 
-// K3: blockIdx.y is the K-slice; each slice accumulates into its own buffer.
+// K3: each K-slice accumulates into its own buffer.
 struct GradSlices {
   float* g[kMaxSplit];
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int ST, int OCC>
-__global__ __launch_bounds__(WM * WN * cm::kWave, OCC) void lmh_gemm3(
-    Blocked64 A, Blocked64 B, int k_slice, int remap, GradSlices out, int n_tok, int hidden,
-    const float* factor, int first, const float* scale) {
-  __shared__ uint4 lds[ST * (BM + BN) * (BK / 8)];
+// One K1 launch's arguments: Z^T = A B^T with A = the chunk's weight rows, B = the hidden rows.
+struct K1Job {
+  RowMajor A, B;
+  int count;  // workgroups (tiles)
+  int remap;  // XCD-aware tile order (count % 8 == 0)
+  EpiProbs epi;
+};
+
+// One K3 launch's arguments: G_s = G_s * factor + P W_c over K-slices of k_slice columns.
+struct K3Job {
+  Tiled32 A;    // E
+  Blocked64 B;  // W_c^T, 64-column panels
+  int tiles;  // output tiles; count = tiles * n_split workgroups
+  int count;
+  int k_slice;
+  int remap;
+  GradSlices out;
+  int n_tok, hidden;
+  const float* factor;
+  int first;
+  const float* scale;
+};
+
+constexpr int kLds1 = kST1 * (kBM1 + kBN1) * (kBK1 / 8);  // uint4 of K1's LDS ring
+constexpr int kLds3 = kST3 * (kBM3 + kBN3) * (kBK3 / 8);
+
+__device__ __forceinline__ void k1_block(const K1Job& j, int bid, uint4* lds) {
+  int tm, tn;
+  cm::gemm::tile_of(bid, j.count, (j.B.rows + kBN1 - 1) / kBN1, j.remap, tm, tn);
+  EpiProbs epi = j.epi;
+  cm::gemm::gemm_lds<kBM1, kBN1, kWM1, kWN1, kBK1, kST1>(j.A, j.B, 0, j.A.k_len, tm, tn, epi, lds);
+}
+
+__device__ __forceinline__ void k3_block(const K3Job& j, int bid, uint4* lds) {
   int tm, tn, s;
-  cm::gemm::tile_of_block_2d((B.rows + BN - 1) / BN, remap, tm, tn, s);
-  const int k_begin = s * k_slice;
+  cm::gemm::tile_of_sliced(bid, j.count, j.tiles, (j.B.rows + kBN3 - 1) / kBN3, j.remap, tm, tn,
+                           s);
+  const int k_begin = s * j.k_slice;
   // An empty slice still runs the epilogue (with zero accumulators) so that its buffer is
   // initialised on the first chunk and rescaled on later ones.
-  const int k_end = max(k_begin, min(A.k_len, k_begin + k_slice));
-  EpiGrad epi{out.g[s], n_tok, hidden, factor, first};
-  ScaleP<BM / WM / 32> xp{scale, n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
-  cm::gemm::gemm_lds<BM, BN, WM, WN, BK, ST>(A, B, k_begin, k_end, tm, tn, epi, lds, xp);
+  const int k_end = max(k_begin, min(j.A.k_len, k_begin + j.k_slice));
+  EpiGrad epi{j.out.g[s], j.n_tok, j.hidden, j.factor, j.first, {}};  // f: start()
+  ScaleP<kBM3 / kWM3 / 32> xp{j.scale, j.n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
+  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3>(j.A, j.B, k_begin, k_end, tm, tn, epi,
+                                                          lds, xp);
+}
+
+// __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD, which caps
+// the registers per wavefront accordingly.
+__global__ __launch_bounds__(kThreads1, kOcc1) void lmh_gemm1(K1Job j) {
+  __shared__ uint4 lds[kLds1];
+  k1_block(j, static_cast<int>(blockIdx.x), lds);
+}
+
+__global__ __launch_bounds__(kThreads3, kOcc3) void lmh_gemm3(K3Job j) {
+  __shared__ uint4 lds[kLds3];
+  k3_block(j, static_cast<int>(blockIdx.x), lds);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -390,21 +455,14 @@ struct OffState {
   }
 };
 
-// Merge the states of all lanes of a THREADS-lane workgroup; every lane gets the result.
-template <int THREADS>
-__device__ __forceinline__ OffState block_merge_off(OffState s, OffState* part) {
+// Merge the states of the 64 lanes of a wavefront; every lane gets the result.
+__device__ __forceinline__ OffState wave_merge_off(OffState s) {
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) {
     OffState o{cm::shfl_xor_state(s.st, d), __shfl_xor(s.off, d, cm::kWave)};
     s.merge(o);
   }
-  const int wave = threadIdx.x / cm::kWave;
-  if (threadIdx.x % cm::kWave == 0) part[wave] = s;
-  __syncthreads();
-  OffState r = part[0];
-#pragma unroll
-  for (int i = 1; i < THREADS / cm::kWave; ++i) r.merge(part[i]);
-  return r;
+  return s;
 }
 
 // K2: merge the chunk's partials into the running state; the factor; with a scale array, the
@@ -413,61 +471,77 @@ __device__ __forceinline__ OffState block_merge_off(OffState s, OffState* part) 
 // coefficient p_t - 1 is applied by K4 in fp32, so its near-1 probability never enters the
 // fp32 accumulators (a ~1024 W_t term there would cancel against -1024 W_t only at the end,
 // losing the small difference 1 - p_t of a confident label to the accumulators' rounding).
-__global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
+//
+// One wavefront per token row; lane l holds groups l, l + 64, ... (SLOTS of them, the chunk's
+// groups being at most 64 * SLOTS). Every load of the row (the running state, the SLOTS
+// partials, the label group's logits) is issued before the first merge, so a row costs one
+// memory round trip; the group maxima stay in registers for the scales.
+template <int SLOTS>
+__global__ __launch_bounds__(kRowsPerBlock * cm::kWave) void lmh_rows_kernel(
     const Partial* __restrict__ part, int n_groups, RowState rs,
     const int64_t* __restrict__ target, int n_tok, int64_t c0, int n_voc, int first,
     float* __restrict__ scale, _Float16* __restrict__ e16, const _Float16* __restrict__ label_z) {
-  const int row = blockIdx.x;
+  const int lane = threadIdx.x % cm::kWave;
+  const int row = blockIdx.x * kRowsPerBlock + static_cast<int>(threadIdx.x / cm::kWave);
+  if (row >= n_tok) return;  // the whole wavefront
   const int64_t t = target[row];
   const bool labelled = t != -100;
   // the label's statistics group in this chunk, or -1
   const int64_t g_label = t >= c0 && t < c0 + n_voc ? (t - c0) / kGroup : -1;
-  // From the label group's 128 fp16 logits (K1 copied them out lane by lane: entry e of the
-  // lane in half h is group row (e/16)*32 + ((e%16)/4)*8 + 4h + e%4): the label's logit and the
-  // group's sum of e^{z - m_g} over its other columns, relative to the group max as K1's sums
-  // are. Rows past the chunk hold -inf.
-  __shared__ float s_red[kStatThreads / cm::kWave];
-  __shared__ float s_zt;
-  float label_off = 0.0f;
-  if (g_label >= 0) {  // uniform over the workgroup
-    const int local = static_cast<int>(t - c0 - g_label * kGroup);
-    const float mg = part[static_cast<int64_t>(row) * n_groups + g_label].max;
-    float v = 0.0f;
-    if (threadIdx.x < 2 * kEpiRows) {
-      const int h = threadIdx.x / kEpiRows, e = threadIdx.x % kEpiRows;
-      const int r = (e / 16) * 32 + ((e % 16) / 4) * 8 + h * 4 + e % 4;
-      const float z = static_cast<float>(label_z[static_cast<int64_t>(row) * 2 * kEpiRows +
-                                                 threadIdx.x]);
-      if (r == local) s_zt = z;
-      else v = cm::exp_f(z - mg);
-    }
-    v = cm::wave_sum(v);
-    if (threadIdx.x % cm::kWave == 0) s_red[threadIdx.x / cm::kWave] = v;
-    __syncthreads();
-    for (int w = 0; w < kStatThreads / cm::kWave; ++w) label_off += s_red[w];
-    if (threadIdx.x == 0) rs.label_logit[row] = s_zt;
-  }
-  OffState acc = OffState::empty();
   const int n_valid = (n_voc + kGroup - 1) / kGroup;  // groups K1 wrote for this chunk
-  for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
-    const Partial p = part[static_cast<int64_t>(row) * n_groups + g];
-    if (p.best >= 0) {
-      OffState q{{p.max, p.sum, p.dot, static_cast<int64_t>(p.best)},
-                 g == g_label ? label_off : p.sum};
-      acc.merge(q);
-    }
-  }
-  __shared__ OffState s_part[kStatThreads / cm::kWave];
-  acc = block_merge_off<kStatThreads>(acc, s_part);
   OffState now = OffState::empty();
   if (!first) {
     now.st = cm::SoftmaxState{rs.max[row], rs.sum[row], rs.dot[row], rs.best[row]};
     now.off = rs.off[row];
   }
+  const uint4* prow = reinterpret_cast<const uint4*>(part + static_cast<int64_t>(row) * n_groups);
+  Partial p[SLOTS];
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) {
+    const int g = lane + i * cm::kWave;
+    p[i] = __builtin_bit_cast(Partial, prow[g < n_valid ? g : 0]);
+  }
+  // The label group's 128 fp16 logits (K1 copied them out lane by lane: entry e of the lane in
+  // half h is group row (e/16)*32 + ((e%16)/4)*8 + 4h + e%4); rows past the chunk hold the
+  // sentinel logit. They give the label's logit and the group's sum of e^{z - m_g} over its
+  // other columns, relative to the group max as K1's sums are.
+  float z0 = 0.0f, z1 = 0.0f;
+  if (g_label >= 0) {  // uniform over the wavefront
+    const _Float16* lz = label_z + static_cast<int64_t>(row) * 2 * kEpiRows;
+    z0 = static_cast<float>(lz[lane]);
+    z1 = static_cast<float>(lz[kEpiRows + lane]);
+  }
+  float label_off = 0.0f;
+  if (g_label >= 0) {
+    const int local = static_cast<int>(t - c0 - g_label * kGroup);
+    const int slot = static_cast<int>(g_label / cm::kWave), owner = static_cast<int>(g_label % cm::kWave);
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i)
+      if (i == slot) mine = p[i].max;
+    const float mg = __shfl(mine, owner, cm::kWave);
+    const int r0 = (lane / 16) * 32 + ((lane % 16) / 4) * 8 + lane % 4;  // half 0; half 1: + 4
+    const bool has0 = r0 == local, has1 = r0 + 4 == local;
+    label_off = cm::wave_sum((has0 ? 0.0f : cm::exp_f(z0 - mg)) + (has1 ? 0.0f : cm::exp_f(z1 - mg)));
+    const unsigned long long who = __ballot(has0 || has1);
+    const float zt = __shfl(has0 ? z0 : z1, static_cast<int>(__builtin_ctzll(who)), cm::kWave);
+    if (lane == 0) rs.label_logit[row] = zt;
+  }
+  OffState acc = OffState::empty();
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) {
+    const int g = lane + i * cm::kWave;
+    if (g < n_valid && p[i].best >= 0) {
+      OffState q{{p[i].max, p[i].sum, p[i].dot, static_cast<int64_t>(p[i].best)},
+                 g == g_label ? label_off : p[i].sum};
+      acc.merge(q);
+    }
+  }
+  acc = wave_merge_off(acc);
   const float lse_prev = first ? -__builtin_huge_valf() : now.st.lse();
   now.merge(acc);
   const float lse_now = now.st.lse();
-  if (threadIdx.x == 0) {
+  if (lane == 0) {
     rs.max[row] = now.st.max;
     rs.sum[row] = now.st.sum;
     rs.dot[row] = now.st.dot;
@@ -477,20 +551,26 @@ __global__ __launch_bounds__(kStatThreads) void lmh_rows_kernel(
     rs.factor[row] = first ? 0.0f : cm::exp_f(lse_prev - lse_now);
   }
   if (scale == nullptr) return;
-  for (int g = threadIdx.x; g < n_valid; g += kStatThreads) {
-    const float m = part[static_cast<int64_t>(row) * n_groups + g].max;
-    scale[static_cast<int64_t>(g) * n_tok + row] =
-        labelled ? cm::exp_f(m - lse_now) * kPScale : 0.0f;
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) {
+    const int g = lane + i * cm::kWave;
+    if (g < n_valid)
+      scale[static_cast<int64_t>(g) * n_tok + row] =
+          labelled ? cm::exp_f(p[i].max - lse_now) * kPScale : 0.0f;
   }
-  if (threadIdx.x == 0 && g_label >= 0)
-    e16[panel_index(row, t - c0, n_tok)] = static_cast<_Float16>(0.0f);
+  if (lane == 0 && g_label >= 0)
+    e16[Tiled32::index(row, t - c0, (n_tok + 31) / 32)] = static_cast<_Float16>(0.0f);
 }
 
 // K4: final per-row outputs; G = scale * (sum_s G_s / 1024 + (p_t - 1) W[t]) for labelled rows,
-// else 0.
+// else 0. NS = the number of K-slices; a thread handles kFinalPer hidden units at a time and
+// issues all their loads (NS slices and W[t]) before the first store.
+constexpr int kFinalPer = 8;
+
+template <int NS>
 __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
     RowState rs, const int64_t* __restrict__ target, int64_t vocab, float* __restrict__ loss,
-    float* __restrict__ entropy, int32_t* __restrict__ correct, GradSlices gs, int n_split,
+    float* __restrict__ entropy, int32_t* __restrict__ correct, GradSlices gs,
     const _Float16* __restrict__ weight, int64_t ld_w, int hidden, float grad_scale) {
   const int row = blockIdx.x;
   const int64_t t = target[row];
@@ -516,13 +596,50 @@ __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
   // label's whole coefficient p_t - 1 = -off / sum is applied here in fp32, with the relative
   // precision of the off-label mass however confident the label is.
   const float coef = labelled && in_range ? -rs.off[row] / rs.sum[row] : 0.0f;
-  for (int h = threadIdx.x; h < hidden; h += kStatThreads) {
-    float acc = gs.g[0][off + h];
-    for (int s = 1; s < n_split; ++s) acc += gs.g[s][off + h];
-    gs.g[0][off + h] = labelled && in_range
-                           ? grad_scale * (acc * (1.0f / kPScale) + coef * static_cast<float>(w[h]))
-                           : (labelled ? __builtin_nanf("") : 0.0f);
+  for (int h0 = threadIdx.x; h0 < hidden; h0 += kStatThreads * kFinalPer) {
+    float v[NS][kFinalPer], wv[kFinalPer];
+#pragma unroll
+    for (int j = 0; j < kFinalPer; ++j) {
+      const int h = h0 + j * kStatThreads;
+      const int hc = h < hidden ? h : 0;
+      wv[j] = static_cast<float>(w[hc]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) v[s][j] = gs.g[s][off + hc];
+    }
+#pragma unroll
+    for (int j = 0; j < kFinalPer; ++j) {
+      const int h = h0 + j * kStatThreads;
+      float acc = v[0][j];
+#pragma unroll
+      for (int s = 1; s < NS; ++s) acc += v[s][j];
+      if (h < hidden)
+        gs.g[0][off + h] = labelled && in_range
+                               ? grad_scale * (acc * (1.0f / kPScale) + coef * wv[j])
+                               : (labelled ? __builtin_nanf("") : 0.0f);
+    }
   }
+}
+
+// K4 for n_split slices (1 <= n_split <= kMaxSplit).
+int launch_final(int n_split, int n_tok, hipStream_t s, const RowState& rs, const int64_t* target,
+                 int64_t vocab, float* loss, float* entropy, int32_t* correct, const GradSlices& gs,
+                 const _Float16* w, int64_t ld_w, int hidden, float grad_scale) {
+#define CM_FINAL(NS)                                                                            \
+  hipLaunchKernelGGL(lmh_final_kernel<NS>, dim3(n_tok), dim3(kStatThreads), 0, s, rs, target,    \
+                     vocab, loss, entropy, correct, gs, w, ld_w, hidden, grad_scale)
+  switch (n_split) {
+    case 1: CM_FINAL(1); break;
+    case 2: CM_FINAL(2); break;
+    case 3: CM_FINAL(3); break;
+    case 4: CM_FINAL(4); break;
+    case 5: CM_FINAL(5); break;
+    case 6: CM_FINAL(6); break;
+    case 7: CM_FINAL(7); break;
+    case 8: CM_FINAL(8); break;
+    default: return static_cast<int>(hipErrorInvalidValue);
+  }
+#undef CM_FINAL
+  return cm::launch_status();
 }
 
 // W_c^T in panels: out[p][h][j] = W[c0 + 64 p + j][h], zero for 64 p + j >= n_voc.
@@ -551,14 +668,15 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 constexpr int64_t kChunkAlign = kBM1 > 256 ? kBM1 : 256;
 
 int64_t default_chunk(int64_t n_rows, int64_t vocab) {
-  // E chunk of at most 1 GiB (fp16, n_rows x C), whatever the vocabulary, split into equal
-  // chunks. Fewer, larger chunks pay the per-chunk costs (launch ramps, each launch's partly
-  // filled last wave of workgroups, the read-modify-write of the split-K gradient accumulators)
-  // fewer times; measured at N = 2048, V = 151936: 38016 columns (4 chunks) 2.51 ms, 50688
-  // (3) 2.51 ms, 75968 (2) 2.40 ms, one chunk 2.31 ms (a 622 MB E buffer, 0.2% of the HBM).
-  const int64_t budget = (int64_t{512} << 20) / (n_rows > 0 ? n_rows : 1);  // columns
+  // E chunk of at most 128 MiB (fp16, n_rows x C), split into equal chunks. Per extra chunk the
+  // gradient GEMM's split-K slices are read and rewritten once more (4 x 12.6 MB at N = 2048)
+  // and each kernel ramps up once more; measured at N = 2048, V = 151936 (one MI355X, same box):
+  // 8192 columns 2.58-2.63 ms, 16384 2.29-2.44 ms, 32768 2.23-2.30 ms, the whole vocabulary in
+  // one chunk (a 622 MB E) 2.28-2.35 ms.
+  const int64_t budget = (int64_t{128} << 20) / 2 / (n_rows > 0 ? n_rows : 1);  // columns
   int64_t c = budget / kChunkAlign * kChunkAlign;
   if (c < 4096) c = 4096;
+  if (c > kMaxChunk) c = kMaxChunk;
   if (c >= vocab) return round_up(vocab, kChunkAlign);
   const int64_t n_chunks = (vocab + c - 1) / c;
   return round_up((vocab + n_chunks - 1) / n_chunks, kChunkAlign);
@@ -574,7 +692,7 @@ int n_split_for(int64_t n_rows, int hidden) {
 }
 
 struct Layout {
-  int64_t chunk, n_groups;
+  int64_t chunk, n_groups, n_chunks;
   int n_split;
   int64_t off_e16, off_part, off_rows, off_labz, off_scale, off_g, off_wt, total;
 };
@@ -584,11 +702,13 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   Layout L;
   L.chunk = chunk > 0 ? round_up(chunk, kChunkAlign) : default_chunk(n_rows, vocab);
   if (L.chunk > round_up(vocab, kChunkAlign)) L.chunk = round_up(vocab, kChunkAlign);
+  if (L.chunk > kMaxChunk) L.chunk = kMaxChunk;
   L.n_groups = L.chunk / kGroup;
+  L.n_chunks = (vocab + L.chunk - 1) / L.chunk;
   L.n_split = want_grad ? n_split_for(n_rows, hidden) : 1;
   int64_t off = 0;
   L.off_e16 = off;
-  off += round_up(n_rows * L.chunk * 2, 256);
+  off += round_up(round_up(n_rows, 32) * L.chunk * 2, 256);
   L.off_part = off;
   off += round_up(n_rows * L.n_groups * static_cast<int64_t>(sizeof(Partial)), 256);
   L.off_rows = off;
@@ -637,7 +757,6 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
                int hidden_size, float* loss, float* entropy, int32_t* correct, float* grad,
                float grad_scale, char* ws, const Layout& L, hipStream_t s) {
   const bool want_grad = grad != nullptr;
-  _Float16* e16 = reinterpret_cast<_Float16*>(ws + L.off_e16);
   Partial* part = reinterpret_cast<Partial*>(ws + L.off_part);
   float* scale = want_grad ? reinterpret_cast<float*>(ws + L.off_scale) : nullptr;
   const RowState rs = row_state(ws + L.off_rows, round_up(n_rows * 4, 256));
@@ -652,65 +771,96 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
   const _Float16* W16 = static_cast<const _Float16*>(weight);
   const int n_tok = static_cast<int>(n_rows);
 
-  for (int64_t c0 = 0; c0 < vocab; c0 += L.chunk) {
-    const int n_voc = static_cast<int>(vocab - c0 < L.chunk ? vocab - c0 : L.chunk);
-    const bool first = c0 == 0;
-    // K1: Z^T tile = W_c H^T, statistics, E and the label logit
-    {
-      const int tiles_m = (n_voc + kBM1 - 1) / kBM1;
-      const int tiles_n = (n_tok + kBN1 - 1) / kBN1;
-      const int grid = tiles_m * tiles_n;
-      RowMajor A{W16 + c0 * ld_w, ld_w, n_voc, hidden_size};
-      RowMajor B{H16, ld_h, n_tok, hidden_size};
-      EpiProbs epi{e16, n_tok, n_voc, c0, part, static_cast<int>(L.n_groups), target,
-                   label_z, want_grad ? 1 : 0, {}};  // tgt: prepare()
-      hipLaunchKernelGGL((lmh_gemm1<EpiProbs, kBM1, kBN1, kWM1, kWN1, kBK1, kST1, kOcc1>), dim3(grid),
-                         dim3(kThreads1), 0, s, A, B, grid % 8 == 0 ? 1 : 0, epi);
-      int st = cm::launch_status();
-      if (st) return st;
+  auto c0_of = [&](int64_t c) { return c * L.chunk; };
+  auto n_voc_of = [&](int64_t c) {
+    return static_cast<int>(vocab - c0_of(c) < L.chunk ? vocab - c0_of(c) : L.chunk);
+  };
+  _Float16* e16 = reinterpret_cast<_Float16*>(ws + L.off_e16);
+  auto e16_of = [&](int64_t) { return e16; };
+  // K1 of chunk c: Z^T tile = W_c H^T, statistics, E and the label logit
+  auto k1_job = [&](int64_t c) {
+    const int n_voc = n_voc_of(c);
+    const int tiles = ((n_voc + kBM1 - 1) / kBM1) * ((n_tok + kBN1 - 1) / kBN1);
+    K1Job j{RowMajor{W16 + c0_of(c) * ld_w, ld_w, n_voc, hidden_size},
+            RowMajor{H16, ld_h, n_tok, hidden_size},
+            tiles,
+            tiles % 8 == 0 ? 1 : 0,
+            EpiProbs{e16_of(c), n_tok, n_voc, c0_of(c), part, static_cast<int>(L.n_groups), target,
+                     label_z, want_grad ? 1 : 0, (n_tok + 31) / 32, {}}};  // tgt: prepare()
+    return j;
+  };
+  // K2 of chunk c: running statistics and the group scales
+  auto k2 = [&](int64_t c) {
+    const dim3 grid((n_tok + kRowsPerBlock - 1) / kRowsPerBlock), block(kRowsPerBlock * cm::kWave);
+    const int ng = static_cast<int>(L.n_groups), fi = c == 0 ? 1 : 0, nv = n_voc_of(c);
+    const int64_t c0 = c0_of(c);
+    _Float16* e = e16_of(c);
+    if (L.n_groups <= cm::kWave) {
+      hipLaunchKernelGGL(lmh_rows_kernel<1>, grid, block, 0, s, part, ng, rs, target, n_tok, c0,
+                         nv, fi, scale, e, label_z);
+    } else if (L.n_groups <= 4 * cm::kWave) {
+      hipLaunchKernelGGL(lmh_rows_kernel<4>, grid, block, 0, s, part, ng, rs, target, n_tok, c0,
+                         nv, fi, scale, e, label_z);
+    } else {
+      hipLaunchKernelGGL(lmh_rows_kernel<kMaxRowSlots>, grid, block, 0, s, part, ng, rs, target,
+                         n_tok, c0, nv, fi, scale, e, label_z);
     }
-    // K2: running statistics and the group scales
-    hipLaunchKernelGGL(lmh_rows_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, part,
-                       static_cast<int>(L.n_groups), rs, target, n_tok, c0, n_voc,
-                       first ? 1 : 0, scale, e16, label_z);
-    int st = cm::launch_status();
-    if (st) return st;
-    if (!want_grad) continue;
-    // K3: G_s = G_s * factor + P W_c over K-slices, B = W_c^T in panels
+    return cm::launch_status();
+  };
+  // K3 of chunk c: G_s = G_s * factor + P W_c over K-slices, B = W_c^T in panels (the caller's
+  // cached transpose, or this chunk's transposed into the workspace first)
+  auto k3_job = [&](int64_t c, int* st) {
+    const int n_voc = n_voc_of(c);
     const _Float16* wt;
+    *st = 0;
     if (weight_t) {
-      wt = static_cast<const _Float16*>(weight_t) + (c0 / kPanel) * hidden_size * kPanel;
+      wt = static_cast<const _Float16*>(weight_t) + (c0_of(c) / kPanel) * hidden_size * kPanel;
     } else {
       dim3 tgrid((n_voc + kPanel - 1) / kPanel, (hidden_size + 63) / 64);
-      hipLaunchKernelGGL(lmh_transpose_kernel, tgrid, dim3(kStatThreads), 0, s, W16, ld_w, c0,
-                         n_voc, hidden_size, wt_ws);
-      st = cm::launch_status();
-      if (st) return st;
+      hipLaunchKernelGGL(lmh_transpose_kernel, tgrid, dim3(kStatThreads), 0, s, W16, ld_w,
+                         c0_of(c), n_voc, hidden_size, wt_ws);
+      *st = cm::launch_status();
       wt = wt_ws;
     }
-    {
-      const int tiles_m = (n_tok + kBM3 - 1) / kBM3;
-      const int tiles_n = (hidden_size + kBN3 - 1) / kBN3;
-      const int grid = tiles_m * tiles_n;
-      const int panels = (n_voc + kPanel - 1) / kPanel;
-      // slices are whole statistics groups, so a stage never straddles two group scales
-      const int groups = (panels * kPanel + kGroup - 1) / kGroup;
-      const int k_slice = ((groups + L.n_split - 1) / L.n_split) * kGroup;
-      Blocked64 A{e16, n_tok, n_voc};
-      Blocked64 B{wt, hidden_size, n_voc};
-      hipLaunchKernelGGL((lmh_gemm3<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, kOcc3>),
-                         dim3(grid, L.n_split), dim3(kThreads3), 0, s, A, B, k_slice,
-                         (grid * L.n_split) % 8 == 0 ? 1 : 0, gs, n_tok, hidden_size, rs.factor,
-                         first ? 1 : 0,
-                         scale);
-      st = cm::launch_status();
-      if (st) return st;
-    }
+    const int tiles = ((n_tok + kBM3 - 1) / kBM3) * ((hidden_size + kBN3 - 1) / kBN3);
+    const int panels = (n_voc + kPanel - 1) / kPanel;
+    // slices are whole statistics groups, so a stage never straddles two group scales
+    const int groups = (panels * kPanel + kGroup - 1) / kGroup;
+    const int k_slice = ((groups + L.n_split - 1) / L.n_split) * kGroup;
+    const int count = tiles * L.n_split;
+    K3Job j{Tiled32{e16_of(c), n_tok, n_voc, (n_tok + 31) / 32},
+            Blocked64{wt, hidden_size, n_voc},
+            tiles,
+            count,
+            k_slice,
+            count % 8 == 0 ? 1 : 0,
+            gs,
+            n_tok,
+            hidden_size,
+            rs.factor,
+            c == 0 ? 1 : 0,
+            scale};
+    return j;
+  };
+
+  // per chunk: K1, K2, and with the gradient K3
+  for (int64_t c = 0; c < L.n_chunks; ++c) {
+    const K1Job j1 = k1_job(c);
+    hipLaunchKernelGGL(lmh_gemm1, dim3(j1.count), dim3(kThreads1), 0, s, j1);
+    int st = cm::launch_status();
+    if (st) return st;
+    st = k2(c);
+    if (st) return st;
+    if (!want_grad) continue;
+    const K3Job j3 = k3_job(c, &st);
+    if (st) return st;
+    hipLaunchKernelGGL(lmh_gemm3, dim3(j3.count), dim3(kThreads3), 0, s, j3);
+    st = cm::launch_status();
+    if (st) return st;
   }
   GradSlices fin = want_grad ? gs : GradSlices{};
-  hipLaunchKernelGGL(lmh_final_kernel, dim3(n_tok), dim3(kStatThreads), 0, s, rs, target, vocab,
-                     loss, entropy, correct, fin, L.n_split, W16, ld_w, hidden_size, grad_scale);
-  return cm::launch_status();
+  return launch_final(want_grad ? L.n_split : 1, n_tok, s, rs, target, vocab, loss, entropy,
+                      correct, fin, W16, ld_w, hidden_size, grad_scale);
 }
 
 }  // namespace
