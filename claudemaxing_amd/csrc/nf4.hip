@@ -11,9 +11,9 @@
 // absmax block because blocksize >= 32. A workgroup of 256 lanes handles UNITS consecutive
 // 1 KiB slices of the packed weight, so every load and store instruction of a wavefront covers
 // one contiguous span (256 B in, 1 KiB out for fp16). The fp16 outputs go out as nontemporal
-// stores (measured on MI355X: 8.7 -> 7.5 us on the [8960,1536] weight, cold caches). The
-// 16-entry code table sits in LDS: the 16 entries fall in 16 distinct banks, so the per-lane
-// lookups never conflict.
+// stores (measured on MI355X: 8.7 -> 7.5 us on the [8960,1536] weight, cold
+// caches). The 16-entry code table sits in LDS: the 16 entries fall in 16 distinct banks, so the
+// per-lane lookups never conflict.
 #include "common.h"
 
 namespace {
@@ -23,7 +23,7 @@ namespace {
 
 constexpr int kThreads = 256;
 #ifndef CM_NF4_UNITS
-#define CM_NF4_UNITS 8
+#define CM_NF4_UNITS 4
 #endif
 #ifndef CM_NF4_WIDE
 #define CM_NF4_WIDE 0
@@ -90,32 +90,56 @@ struct Pack8<float> {
   }
 };
 
-// Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes.
+// Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes. Every
+// global load of a lane is issued at the start, independent of the others: its packed words,
+// the absmax byte (or fp32 absmax) and the absmax2 entry of each of its units, one entry of the
+// 256-entry code2 table (staged in LDS beside the 16-entry code table); after the one barrier
+// the nested scale is code2[q8] from LDS times absmax2 plus offset. (Decoding the scale from a
+// global code2[q8] made the gather a second memory round trip before the first store.)
 template <typename OutT, bool NESTED>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
     const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
     const float* __restrict__ code, const float* __restrict__ code2,
     const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
     OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
+  static_assert(kThreads >= 256, "one code2 entry per lane");
   __shared__ float s_code[16];
-  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
-  const float offset = NESTED ? *offset_ptr : 0.0f;
-  __syncthreads();
-
+  __shared__ float s_code2[NESTED ? 256 : 1];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnits) + threadIdx.x;
   uint32_t word[kUnits];
+  uint32_t q8[kUnits];   // nested: absmax byte of the unit's block
+  float a2[kUnits];      // nested: absmax2 of it; plain: the block's fp32 absmax
 #pragma unroll
   for (int j = 0; j < kUnits; ++j) {
     const int64_t u = base + j * kThreads;
-    word[j] = u < n_units ? __builtin_nontemporal_load(packed + u) : 0u;
+    const bool ok = u < n_units;
+    word[j] = ok ? __builtin_nontemporal_load(packed + u) : 0u;
+    // 8 elements of unit u start at element 8u; blocksize = 8 << unit_shift elements.
+    const uint32_t blk = ok ? static_cast<uint32_t>(u >> unit_shift) : 0u;
+    if constexpr (NESTED) {
+      q8[j] = static_cast<const uint8_t*>(absmax)[blk];
+      a2[j] = absmax2[bs2_shift >= 0 ? (blk >> bs2_shift) : (blk / bs2)];
+    } else {
+      a2[j] = static_cast<const float*>(absmax)[blk];
+    }
   }
+  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
+  if constexpr (NESTED) {
+    if (threadIdx.x < 256) s_code2[threadIdx.x] = code2[threadIdx.x];
+  }
+  const float offset = NESTED ? *offset_ptr : 0.0f;
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < kUnits; ++j) {
     const int64_t u = base + j * kThreads;
     if (u >= n_units) break;
-    // 8 elements of unit u start at element 8u; blocksize = 8 << unit_shift elements.
-    const uint32_t blk = static_cast<uint32_t>(u >> unit_shift);
-    const float s = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+    float s;
+    if constexpr (NESTED) {
+      const float prod = s_code2[q8[j]] * a2[j];  // multiply, then add (no contraction)
+      s = prod + offset;
+    } else {
+      s = a2[j];
+    }
     float v[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -266,31 +290,38 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
     uint32_t bs2) {
   constexpr int kTR = 64, kTC = 128, kCol = (kTR + 2) / 2;  // 32-bit words per LDS column
   __shared__ float s_code[16];
+  __shared__ float s_scale[kTR * (kTC / 32)];  // [row][block of the row's 128 columns]
   __shared__ uint32_t tile[kTC * kCol];  // [column][row pair]
-  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
-  const float offset = NESTED ? *offset_ptr : 0.0f;
   const int64_t tiles_c = cols / kTC;
   const int64_t r0 = (blockIdx.x / tiles_c) * kTR, c0 = (blockIdx.x % tiles_c) * kTC;
   uint32_t word[2][2];
-  int64_t unit[2][2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int p = threadIdx.x + kThreads * j, rp = p / 16, wc = p % 16;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      unit[j][h] = ((r0 + 2 * rp + h) * cols + c0) / 8 + wc;  // 8 elements per 4-byte unit
-      word[j][h] = __builtin_nontemporal_load(packed + unit[j][h]);
+      const int64_t unit = ((r0 + 2 * rp + h) * cols + c0) / 8 + wc;  // 8 elements per unit
+      word[j][h] = __builtin_nontemporal_load(packed + unit);
     }
   }
-  __syncthreads();  // s_code
+  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
+  const float offset = NESTED ? *offset_ptr : 0.0f;
+  // The tile's block scales, decoded once: a row's 128 columns start at a multiple of 128 and
+  // hold nb = max(1, 128 / blocksize) whole blocks (or lie inside one).
+  const int nb = max(1, (kTC / 8) >> unit_shift);
+  if (threadIdx.x < kTR * nb) {
+    const int r = threadIdx.x / nb, k = threadIdx.x % nb;
+    const uint32_t blk = static_cast<uint32_t>((((r0 + r) * cols + c0) / 8 >> unit_shift) + k);
+    s_scale[threadIdx.x] = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+  }
+  __syncthreads();  // s_code, s_scale
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int p = threadIdx.x + kThreads * j, rp = p / 16, wc = p % 16;
     uint32_t lo[8], hi[8];  // fp16 bits of the 8 columns, rows 2 rp and 2 rp + 1
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t blk = static_cast<uint32_t>(unit[j][h] >> unit_shift);
-      const float sc = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
+      const float sc = s_scale[(2 * rp + h) * nb + (wc >> unit_shift)];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t byte = (word[j][h] >> (8 * k)) & 0xffu;
