@@ -23,7 +23,9 @@ Every launch closure is built eagerly from its own tensors (sizes read from thos
 no closure can pick up another kernel's sizes.
 
 One JSON line is printed: the headline metric with its roofline and the CPU oracle timed on the
-host cores (a baseline, not the target), plus every kernel's numbers under "kernels".
+host cores (a baseline, not the target), plus every kernel's numbers under "kernels", and the
+board's socket power and graphics clock (amd-smi) sampled while the headline call runs back to
+back after its timed region (the matrix-core kernels run at the board's power limit).
 """
 
 import argparse
@@ -52,6 +54,8 @@ def parse():
     p.add_argument("--only", default="")
     p.add_argument("--step-steps", type=int, default=10, help="timed QLoRA steps (config 5)")
     p.add_argument("--no-step", action="store_true", help="skip the QLoRA step (config 5)")
+    p.add_argument("--no-power", action="store_true",
+                   help="skip the board power sample of the headline (profiler runs)")
     return p.parse_args()
 
 
@@ -575,6 +579,75 @@ def traffic_from_profile(name):
     return None
 
 
+def _smi_sample(smi):
+    """(socket power W, mean graphics clock MHz) from one `amd-smi metric -p -c --json`, or
+    None when the tool's output cannot be read."""
+    import subprocess
+
+    try:
+        r = subprocess.run([smi, "metric", "-p", "-c", "--json"], capture_output=True, text=True,
+                           timeout=10)
+        data = json.loads(r.stdout)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        return None
+    if isinstance(data, dict):
+        data = data.get("gpu_data", [data])
+    if not data:
+        return None
+    gpu = data[0]
+    try:
+        watts = float(gpu["power"]["socket_power"]["value"])
+        clocks = [float(v["clk"]["value"]) for k, v in gpu["clock"].items()
+                  if k.startswith("gfx_") and isinstance(v, dict) and "clk" in v]
+    except (KeyError, TypeError, ValueError):
+        return None
+    return watts, (sum(clocks) / len(clocks) if clocks else None)
+
+
+def board_power(fn, seconds=2.0):
+    """The board's socket power and graphics clock (amd-smi, about 5 samples a second) while
+    `fn` runs back to back for `seconds`, or None without a readable amd-smi. The matrix-core
+    kernels run into the board's power limit, which sets the clock they run at."""
+    import shutil
+    import threading
+
+    import torch
+
+    smi = shutil.which("amd-smi")
+    if smi is None or _smi_sample(smi) is None:
+        return None
+    samples, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            v = _smi_sample(smi)
+            if v is not None:
+                samples.append(v)
+            stop.wait(0.2)
+
+    fn()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=poll, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    steady = samples[1:] or samples  # the first sample may precede the ramp
+    if not steady:
+        return None
+    watts = sorted(w for w, _ in steady)
+    mhz = sorted(c for _, c in steady if c is not None)
+    return dict(socket_w=watts[len(watts) // 2],
+                gfx_mhz=round(mhz[len(mhz) // 2]) if mhz else None, samples=len(steady),
+                window_s=seconds,
+                note="amd-smi metric -p -c (median over the window) while the headline call runs "
+                     "back to back, after the timed region; 2.5 PFLOP/s is the 2.4 GHz peak")
+
+
 def cpu_baseline(headline):
     """The oracle of the headline kernel on the host cores, on a bounded sample."""
     import numpy as np
@@ -690,9 +763,15 @@ def main():
     kernels = build_kernels(dev, only)
     torch.cuda.synchronize()
     results = {}
+    power = None
     for kern in kernels:
         print(f"[bench] {kern.name} ...", file=sys.stderr, flush=True)
         ms = time_kernel(kern, args.steps, args.warmup)
+        if kern.name == "lmhead_ce" and not args.no_power:
+            power = board_power(kern.launches[0][0])
+            if power:
+                print(f"[bench] lmhead_ce board power: {power['socket_w']} W, graphics clock "
+                      f"{power['gfx_mhz']} MHz", file=sys.stderr, flush=True)
         if kern.bound == "hbm":
             achieved, peak, unit = kern.work / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
             if kern.name in FLOORS:
@@ -734,6 +813,7 @@ def main():
                      "unit": hr["unit"], "frac": hr["frac"],
                      "traffic": traffic_from_profile(headline)},
         "kernels": results,
+        "power": power,
         "ms_per_step_note": "one headline call (the fused LM head at config 4) per step",
         "in_step_kernel_sum_ms": round(sum(r["us"] for r in results.values()
                                            if r["in_step"]) / 1e3, 4),

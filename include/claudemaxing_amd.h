@@ -198,7 +198,8 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
 
 /* ------------------------------------------------------------------------------------------ */
 /* Fused LM head + cross-entropy with per-row loss, entropy, accuracy and the hidden-state
- * gradient, without materialising logits. Replaces the chunk loop of _FusedHeadLoss.forward
+ * gradient. The full [n_rows, V] logits are never stored: per vocabulary chunk one fp16 buffer of
+ * n_rows x chunk values lives in the workspace. Replaces the chunk loop of _FusedHeadLoss.forward
  * (solution/lm_head_loss.py:192-245: torch.mm + lm_head_vocab_chunk_kernel (108-160) + torch.mm
  * per vocabulary chunk, label fix-up 230-236).
  *   z[r,v] = fp16(sum_k hidden[r,k] * W[v,k])          (fp32 accumulation, rounded to fp16)
@@ -211,7 +212,8 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
  * weight_t[p][h][j] = W[64 p + j][h] and zeros for 64 p + j >= V; without it the gradient pass
  * transposes each weight chunk into the workspace. H, ld_h, ld_w must be multiples of 8 and the
  * bases 16-byte aligned.
- * The vocabulary is walked in chunks of chunk_cols columns (0 = the library's default); the
+ * The vocabulary is walked in chunks of chunk_cols columns (rounded up to a multiple of 256, at
+ * most 262144; 0 = the library's default, which keeps the chunk buffer at 128 MiB or less); the
  * result does not depend on the chunk size beyond fp32 rounding.
  * workspace: device memory of cm_lmhead_ce_workspace_bytes(n_rows, V, H, chunk_cols) bytes,
  * 256-B aligned.
