@@ -151,6 +151,91 @@ def k_rmsnorm(dev, c2, names):
         out.append(Kernel("rmsnorm_fwd", f"N={n_rows} H=1536 fp16", "hbm", fwd_work, fwd))
     if "rmsnorm_bwd" in names:
         out.append(Kernel("rmsnorm_bwd", f"N={n_rows} H=1536 fp16", "hbm", bwd_work, bwd))
+    if names & {"rmsnorm_fwd_w32", "rmsnorm_bwd_w32"}:
+        out += k_rmsnorm_w32(dev, c2, names)
+    if names & {"rmsnorm_fwd_qlora", "rmsnorm_bwd_qlora"}:
+        out += k_rmsnorm_qlora(dev, c2, names)
+    return out
+
+
+def k_rmsnorm_w32(dev, c2, names):
+    """Config 2's fp32-weight variant: fp16 x, the fp32 weight with its 77 tiny channels (more than
+    the save-low path's 64, so the exact path), fp32 out; backward fp32 dy -> fp16 dx."""
+    import torch
+
+    from claudemaxing_amd import _lib
+
+    n_rows, hid = c2["n"], 1536
+    fwd_work = 2 * n_rows * hid + 4 * n_rows * hid + 4 * n_rows + 4 * hid
+    bwd_work = (4 + 2 + 2) * n_rows * hid + 4 * n_rows + 4 * hid
+    fwd, bwd = [], []
+    for _ in range(copies_for(fwd_work + bwd_work)):
+        xd, wd = c2["x"].to(dev), c2["w"].to(torch.float32).to(dev)
+        out = torch.empty(n_rows, hid, dtype=torch.float32, device=dev)
+        rstd = torch.empty(n_rows, dtype=torch.float32, device=dev)
+        dy = c2["dy"].to(torch.float32).to(dev)
+        dx = torch.empty(n_rows, hid, dtype=torch.float16, device=dev)
+        assert xd.dtype == torch.float16 and xd.shape == out.shape == dy.shape == dx.shape
+        keep = (xd, wd, out, rstd, dy, dx)
+        f = bound("cm_rmsnorm_fwd", xd.data_ptr(), _lib.F16, hid, wd.data_ptr(), _lib.F32,
+                  out.data_ptr(), _lib.F32, rstd.data_ptr(), None, None, None, 1, n_rows, hid,
+                  1e-6, _stream(dev))
+        b = bound("cm_rmsnorm_bwd", dy.data_ptr(), _lib.F32, xd.data_ptr(), _lib.F16,
+                  wd.data_ptr(), _lib.F32, rstd.data_ptr(), dx.data_ptr(), _lib.F16, None, None,
+                  None, 1, 0, n_rows, hid, _stream(dev))
+        f()
+        fwd.append((f, keep))
+        bwd.append((b, keep))
+    out = []
+    if "rmsnorm_fwd_w32" in names:
+        out.append(Kernel("rmsnorm_fwd_w32", f"N={n_rows} H=1536 fp16 x, fp32 w -> fp32", "hbm",
+                          fwd_work, fwd, step=False))
+    if "rmsnorm_bwd_w32" in names:
+        out.append(Kernel("rmsnorm_bwd_w32", f"N={n_rows} H=1536 fp32 dy -> fp16 dx", "hbm",
+                          bwd_work, bwd, step=False))
+    return out
+
+
+def k_rmsnorm_qlora(dev, c2, names):
+    """The training step's norms: fp32 residual x, frozen fp32 weight with no tiny channel
+    (n_small = 0), fp32 out plus the fp16 copy of the output that the NF4 linears read (the
+    save-low path); backward from that copy: fp32 dy -> fp32 dx."""
+    import torch
+
+    from claudemaxing_amd import _lib
+
+    n_rows, hid = c2["n"], 1536
+    fwd_work = (4 + 4 + 2) * n_rows * hid + 4 * n_rows + 4 * hid
+    bwd_work = (4 + 2 + 4) * n_rows * hid + 4 * n_rows + 4 * hid
+    w1 = torch.rand(hid, generator=torch.Generator().manual_seed(2)) + 0.5  # no |w| < 2^-10
+    fwd, bwd = [], []
+    for _ in range(copies_for(fwd_work + bwd_work)):
+        xd, wd = c2["x"].to(torch.float32).to(dev), w1.to(dev)
+        out = torch.empty(n_rows, hid, dtype=torch.float32, device=dev)
+        low = torch.empty(n_rows, hid, dtype=torch.float16, device=dev)
+        side = torch.empty(n_rows, 1, dtype=torch.float16, device=dev)
+        slot = torch.full((hid,), -1, dtype=torch.int32, device=dev)  # no tiny column
+        rstd = torch.empty(n_rows, dtype=torch.float32, device=dev)
+        dy = c2["dy"].to(torch.float32).to(dev)
+        dx = torch.empty(n_rows, hid, dtype=torch.float32, device=dev)
+        assert xd.shape == out.shape == low.shape == dy.shape == dx.shape == (n_rows, hid)
+        keep = (xd, wd, out, low, side, slot, rstd, dy, dx)
+        f = bound("cm_rmsnorm_fwd", xd.data_ptr(), _lib.F32, hid, wd.data_ptr(), _lib.F32,
+                  out.data_ptr(), _lib.F32, rstd.data_ptr(), low.data_ptr(), slot.data_ptr(),
+                  side.data_ptr(), 0, n_rows, hid, 1e-6, _stream(dev))
+        b = bound("cm_rmsnorm_bwd", dy.data_ptr(), _lib.F32, low.data_ptr(), _lib.F16,
+                  wd.data_ptr(), _lib.F32, rstd.data_ptr(), dx.data_ptr(), _lib.F32, None,
+                  slot.data_ptr(), side.data_ptr(), 0, 1, n_rows, hid, _stream(dev))
+        f()  # the fp16 copy and rstd hold real values before backward is timed
+        fwd.append((f, keep))
+        bwd.append((b, keep))
+    out = []
+    if "rmsnorm_fwd_qlora" in names:
+        out.append(Kernel("rmsnorm_fwd_qlora", f"N={n_rows} H=1536 fp32 x and w -> fp32 + fp16 "
+                          "copy (the training step's save-low path)", "hbm", fwd_work, fwd))
+    if "rmsnorm_bwd_qlora" in names:
+        out.append(Kernel("rmsnorm_bwd_qlora", f"N={n_rows} H=1536 from the fp16 copy, fp32 dy "
+                          "-> fp32 dx", "hbm", bwd_work, bwd))
     return out
 
 
@@ -502,7 +587,8 @@ def k_lmhead(dev):
                    step=False)]
 
 
-ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd", "swiglu_fwd",
+ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_fwd_w32", "rmsnorm_bwd_w32",
+       "rmsnorm_fwd_qlora", "rmsnorm_bwd_qlora", "rope_fwd", "rope_bwd", "swiglu_fwd",
        "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "floor_empty", "floor_one_wave",
        "floor_copy_1mib", "nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw",
        "rope_bwd_bw", "lora_pack_bw", "lora_unpack_bw", "nf4_linear_fwd", "nf4_linear_bwd",
@@ -520,7 +606,8 @@ def build_kernels(dev, only):
     if "nf4_dequant" in names:
         kernels += k_nf4(dev)
     c2 = inputs.rmsnorm_rope(0)
-    if names & {"rmsnorm_fwd", "rmsnorm_bwd"}:
+    if names & {"rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_fwd_w32", "rmsnorm_bwd_w32",
+                 "rmsnorm_fwd_qlora", "rmsnorm_bwd_qlora"}:
         kernels += k_rmsnorm(dev, c2, names)
     if names & {"rope_fwd", "rope_bwd"}:
         kernels += k_rope(dev, c2, names)

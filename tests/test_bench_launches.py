@@ -33,12 +33,18 @@ def ranges(args_by_name):
         x, xdt, stride, w, wdt, o, odt, rstd, low, slot, small, n_small, rows, cols, _, _ = a
         out += [(x, ((rows - 1) * stride + cols) * NBYTES[xdt], "x"), (w, cols * NBYTES[wdt], "w"),
                 (o, rows * cols * NBYTES[odt], "out"), (rstd, 4 * rows, "rstd")]
+        if low:
+            out += [(low, rows * cols * 2, "low16")]
+            if n_small:
+                out += [(small, rows * n_small * 2, "small16"), (slot, 4 * cols, "slot")]
     elif name == "cm_rmsnorm_bwd":
         dy, dydt, xs, xsdt, w, wdt, rstd, dx, dxdt, dwp, slot, small, n_small, saved, rows, cols, \
             _ = a
         out += [(dy, rows * cols * NBYTES[dydt], "dy"), (xs, rows * cols * NBYTES[xsdt], "xs"),
                 (w, cols * NBYTES[wdt], "w"), (rstd, 4 * rows, "rstd"),
                 (dx, rows * cols * NBYTES[dxdt], "dx")]
+        if saved and n_small:
+            out += [(small, rows * n_small * 2, "small16"), (slot, 4 * cols, "slot")]
     elif name == "cm_rope":
         (x0, d0, sb0, sh0, st0, h0, o0, od0, x1, d1, sb1, sh1, st1, h1, o1, od1, cos, sin, cdt,
          csb, cst, b, t, d, _, _) = a
