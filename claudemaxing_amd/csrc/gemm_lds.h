@@ -23,6 +23,8 @@
 // after a barrier. ZeroStart is the plain start (zero accumulators).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "gemm_nt.h"
 
@@ -128,6 +130,15 @@ struct DmaTile {
     off0 = src.tile_offset(row0, col0);
   }
 
+  // Instruction i of the stage whose origin is (r0, k0), for a tile known to lie wholly inside
+  // the operand: no bounds selection.
+  template <class Src>
+  __device__ __forceinline__ void issue_inside(const Src& src, int r0, int k0, uint4* tile,
+                                               int wave, int i) const {
+    const char* base = reinterpret_cast<const char*>(src.at(r0, k0));
+    dma16(base + off0 + i * step, tile + (i * NW + wave) * kWave);
+  }
+
   // Instruction i of the stage whose origin is (r0, k0); `inside` = the tile is wholly inside
   // the operand (one wave-uniform test per stage).
   template <class Src>
@@ -187,8 +198,14 @@ struct PlainA {
 // short, so a wavefront never stalls in issue with the matrix core idle (issued as one burst
 // after the barrier, the loads of a 256 x 256 x 64 stage held every wavefront for ~1000
 // cycles). sched_barrier pins that order.
+// Bounds handling of the operand loads (EDGE): kEdgeEither picks per workgroup (a second copy of
+// the main loop without bounds selection, taken when every stage lies inside both operands),
+// kEdgeAlways always selects, kEdgeNever never does (the caller guarantees every tile of the
+// launch lies inside: one loop, for kernels where two copies would not fit the registers).
+enum EdgeMode { kEdgeEither = 0, kEdgeAlways = 1, kEdgeNever = 2 };
+
 template <int BM, int BN, int WM, int WN, int BK, int S, class SrcA, class SrcB, class Epi,
-          class FX = PlainA>
+          class FX = PlainA, int EDGE = kEdgeEither>
 __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_begin, int k_end,
                                          int tm, int tn, Epi& epi, uint4* lds, FX fx = FX()) {
   constexpr int NW = WM * WN;
@@ -221,18 +238,24 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
   epi.template start<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
 
   const int n_kt = (k_end - k_begin + BK - 1) / BK;
+  auto inside_a = [&](int kt) { return A.tile_inside(m0, BM, k_begin + kt * BK); };
+  auto inside_b = [&](int kt) { return B.tile_inside(n0, BN, k_begin + kt * BK); };
+  // Every stage of the workgroup's tiles lies inside both operands (the common case: the
+  // bounds tests are monotonic in the stage, so the last stage decides); the main loop then
+  // issues its loads with no bounds selection.
+  const bool all_inside = n_kt > 0 && inside_a(n_kt - 1) && inside_b(n_kt - 1);
   // load instruction q (< kDma) of stage kt: A's instructions first, then B's
-  auto issue = [&](int kt, int q, bool in_a, bool in_b) {
+  auto issue = [&](int kt, int q, bool in_a, bool in_b, auto edge) {
     uint4* st = lds + (kt % S) * kStage;
     const int k0 = k_begin + kt * BK;
     if (q < TA::kPer) {
-      la.issue(A, m0, k0, st, wave, q, in_a);
+      if constexpr (decltype(edge)::value) la.issue(A, m0, k0, st, wave, q, in_a);
+      else la.issue_inside(A, m0, k0, st, wave, q);
     } else {
-      lb.issue(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer, in_b);
+      if constexpr (decltype(edge)::value) lb.issue(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer, in_b);
+      else lb.issue_inside(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer);
     }
   };
-  auto inside_a = [&](int kt) { return A.tile_inside(m0, BM, k_begin + kt * BK); };
-  auto inside_b = [&](int kt) { return B.tile_inside(n0, BN, k_begin + kt * BK); };
   const int arow = wm * WTM + lane % 32, brow = wn * WTN + lane % 32;
   half8 af[2][TM], bf[2][TN];
   auto read = [&](int kt, int ks, int buf) {
@@ -270,61 +293,80 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
     if (s < n_kt) {
       const bool ia = inside_a(s), ib = inside_b(s);
 #pragma unroll
-      for (int q = 0; q < kDma; ++q) issue(s, q, ia, ib);
+      for (int q = 0; q < kDma; ++q) issue(s, q, ia, ib, std::true_type{});
     }
   }
 
   // Waits for the prologue's loads (the first stage and whatever start() issued).
   epi.template started<TM, TN>(acc);
 
-  // The last substep of stage kt - 1 is multiplied after the barrier of stage kt: its fragments
-  // are already in registers, so its MFMAs cover the latency of the first fragment reads of
-  // stage kt. Before the barrier each wavefront waits for its own reads (the buffer they read
-  // from is refilled after it).
+  // Stage kt. The last substep of stage kt - 1 is multiplied after the barrier of stage kt: its
+  // fragments are already in registers, so its MFMAs cover the latency of the first fragment
+  // reads of stage kt. Before the barrier each wavefront waits for its own reads (the buffer they
+  // read from is refilled after it). The bounds selection on the loads is compile-time (EDGE):
+  // with kEdgeEither a workgroup whose every stage lies inside both operands runs a copy of the
+  // loop without it. (Peeling the first stage and the load-free last stages as well, or two loop
+  // copies in the LM head's gradient GEMM, pushed it past 256 registers.)
   static_assert(KS % 2 == 0, "substep buffers alternate within a stage");
-  for (int kt = 0; kt < n_kt; ++kt) {
-    if (kt + S - 2 < n_kt) {
-      wait_vmcnt<(S - 2) * kDma>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own fragment reads have landed
-    lds_barrier();
-    fx.advance();
-    if (kt + 1 < n_kt) fx.prefetch(k_begin + (kt + 1) * BK);
-    const int kl = kt + S - 1;
-    const bool load = kl < n_kt;
-    const bool ia = load && inside_a(kl), ib = load && inside_b(kl);
-    read(kt, 0, 0);
-    if (kt > 0) {
-      mfma(1, 0, kHalf);
-      interleave_reads();
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (load) {
-#pragma unroll
-      for (int q = 0; q < kPart; ++q)
-        if (q < kDma) issue(kl, q, ia, ib);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt > 0) mfma(1, kHalf, TM * TN);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      const int b = ks & 1;
-      read(kt, ks + 1, b ^ 1);
-      mfma(b, 0, kHalf);
-      interleave_reads();
+  auto run = [&](auto edge) {
+    for (int kt = 0; kt < n_kt; ++kt) {
+      if (kt + S - 2 < n_kt) {
+        wait_vmcnt<(S - 2) * kDma>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own fragment reads have landed
+      lds_barrier();
+      fx.advance();
+      if (kt + 1 < n_kt) fx.prefetch(k_begin + (kt + 1) * BK);
+      const int kl = kt + S - 1;
+      const bool load = kl < n_kt;
+      bool ia = true, ib = true;
+      if constexpr (decltype(edge)::value) {
+        ia = load && inside_a(kl);
+        ib = load && inside_b(kl);
+      }
+      read(kt, 0, 0);
+      if (kt > 0) {
+        mfma(1, 0, kHalf);
+        interleave_reads();
+      }
       __builtin_amdgcn_sched_barrier(0);
       if (load) {
 #pragma unroll
-        for (int q = (ks + 1) * kPart; q < (ks + 2) * kPart; ++q)
-          if (q < kDma) issue(kl, q, ia, ib);
+        for (int q = 0; q < kPart; ++q)
+          if (q < kDma) issue(kl, q, ia, ib, edge);
       }
       __builtin_amdgcn_sched_barrier(0);
-      mfma(b, kHalf, TM * TN);
+      if (kt > 0) mfma(1, kHalf, TM * TN);
       __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ks = 0; ks + 1 < KS; ++ks) {
+        const int b = ks & 1;
+        read(kt, ks + 1, b ^ 1);
+        mfma(b, 0, kHalf);
+        interleave_reads();
+        __builtin_amdgcn_sched_barrier(0);
+        if (load) {
+#pragma unroll
+          for (int q = (ks + 1) * kPart; q < (ks + 2) * kPart; ++q)
+            if (q < kDma) issue(kl, q, ia, ib, edge);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(b, kHalf, TM * TN);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+  };
+  if constexpr (EDGE == kEdgeEither) {
+    if (all_inside) {
+      run(std::false_type{});
+    } else {
+      run(std::true_type{});
+    }
+  } else {
+    (void)all_inside;
+    run(std::bool_constant<EDGE == kEdgeAlways>{});
   }
   if (n_kt > 0) mfma(1, 0, TM * TN);
   epi.template apply<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds);

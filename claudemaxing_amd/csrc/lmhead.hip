@@ -367,6 +367,7 @@ __device__ __forceinline__ void k1_block(const K1Job& j, int bid, uint4* lds) {
   cm::gemm::gemm_lds<kBM1, kBN1, kWM1, kWN1, kBK1, kST1>(j.A, j.B, 0, j.A.k_len, tm, tn, epi, lds);
 }
 
+template <int EDGE>
 __device__ __forceinline__ void k3_block(const K3Job& j, int bid, uint4* lds) {
   int tm, tn, s;
   cm::gemm::tile_of_sliced(bid, j.count, j.tiles, (j.B.rows + kBN3 - 1) / kBN3, j.remap, tm, tn,
@@ -377,8 +378,9 @@ __device__ __forceinline__ void k3_block(const K3Job& j, int bid, uint4* lds) {
   const int k_end = max(k_begin, min(j.A.k_len, k_begin + j.k_slice));
   EpiGrad epi{j.out.g[s], j.n_tok, j.hidden, j.factor, j.first, {}};  // f: start()
   ScaleP<kBM3 / kWM3 / 32> xp{j.scale, j.n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
-  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3>(j.A, j.B, k_begin, k_end, tm, tn, epi,
-                                                          lds, xp);
+  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, Tiled32, Blocked64, EpiGrad,
+                     ScaleP<kBM3 / kWM3 / 32>, EDGE>(j.A, j.B, k_begin, k_end, tm, tn, epi, lds,
+                                                     xp);
 }
 
 // __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD, which caps
@@ -388,9 +390,13 @@ __global__ __launch_bounds__(kThreads1, kOcc1) void lmh_gemm1(K1Job j) {
   k1_block(j, static_cast<int>(blockIdx.x), lds);
 }
 
+// EDGE: cm::gemm::kEdgeNever when every output tile lies inside G (n_tok a multiple of kBM3,
+// hidden of kBN3; the contraction runs over whole 64-column panels), else kEdgeAlways. One loop
+// copy per kernel: two in one did not fit the registers.
+template <int EDGE>
 __global__ __launch_bounds__(kThreads3, kOcc3) void lmh_gemm3(K3Job j) {
   __shared__ uint4 lds[kLds3];
-  k3_block(j, static_cast<int>(blockIdx.x), lds);
+  k3_block<EDGE>(j, static_cast<int>(blockIdx.x), lds);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -854,7 +860,12 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     if (!want_grad) continue;
     const K3Job j3 = k3_job(c, &st);
     if (st) return st;
-    hipLaunchKernelGGL(lmh_gemm3, dim3(j3.count), dim3(kThreads3), 0, s, j3);
+    if (n_tok % kBM3 == 0 && hidden_size % kBN3 == 0) {
+      hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeNever>, dim3(j3.count), dim3(kThreads3), 0, s, j3);
+    } else {
+      hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeAlways>, dim3(j3.count), dim3(kThreads3), 0, s,
+                         j3);
+    }
     st = cm::launch_status();
     if (st) return st;
   }
