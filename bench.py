@@ -569,14 +569,14 @@ def k_lmhead(dev):
     h, w, t = inputs.lm_head(0)
     hd, wd, td = h.to(dev), w.to(dev), t.to(dev)
     flops = 4 * h.shape[0] * w.shape[0] * h.shape[1]
-    w16, wt16 = lm_head_loss.fp16_head_weights(wd, True)  # the host's cached W^T, as in training
-    keep = (hd, wd, td, w16, wt16)
+    w16 = lm_head_loss.fp16_head_weight(wd)  # the host's cached fp16 weight, as in training
+    keep = (hd, wd, td, w16)
 
-    def launch(hd=hd, w16=w16, td=td, wt16=wt16):
-        return lm_head_loss._fused_rows(hd, w16, td, True, None, wt16)
+    def launch(hd=hd, w16=w16, td=td):
+        return lm_head_loss._fused_rows(hd, w16, td, True, None)
 
-    def launch_8192(hd=hd, w16=w16, td=td, wt16=wt16):
-        return lm_head_loss._fused_rows(hd, w16, td, True, 8192, wt16)
+    def launch_8192(hd=hd, w16=w16, td=td):
+        return lm_head_loss._fused_rows(hd, w16, td, True, 8192)
 
     launch()
     launch_8192()

@@ -4,7 +4,8 @@
 //   Blocked64 element (r, k) at p[((k / 64) * rows + r) * 64 + k % 64], i.e. 64-column panels,
 //             so a (rows x 64) tile of one panel is a single contiguous span. Panels are padded
 //             to 64 columns (the padding must hold finite values; the LM head keeps zeros there).
-//   Tiled32   32-row x 64-column blocks of 8-column chunks (below).
+//   Tiled32   32-row x 64-column blocks of 8-column chunks (below);
+//   KMajor    the operand stored transposed, [K][N] with N contiguous (below).
 // The main loop that consumes them is in gemm_lds.h.
 #pragma once
 
@@ -21,6 +22,7 @@ constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per tile row
 
 struct RowMajor {
   static constexpr bool kChunkMajor = false;  // LDS tile layout (gemm_lds.h)
+  static constexpr bool kKMajor = false;
   const _Float16* p;
   int64_t ld;
   int rows;   // valid rows
@@ -40,6 +42,7 @@ struct RowMajor {
 
 struct Blocked64 {
   static constexpr bool kChunkMajor = false;
+  static constexpr bool kKMajor = false;
   const _Float16* p;
   int rows;   // valid rows (= rows of a panel)
   int k_len;  // columns, padded panels beyond it hold finite values
@@ -67,6 +70,7 @@ struct Blocked64 {
 // finite values.
 struct Tiled32 {
   static constexpr bool kChunkMajor = true;
+  static constexpr bool kKMajor = false;
   const _Float16* p;
   int rows;        // valid rows
   int k_len;       // columns
@@ -85,6 +89,26 @@ struct Tiled32 {
   // k < 64 a multiple of 8)
   __device__ __forceinline__ uint32_t tile_offset(int r, int k) const {
     return static_cast<uint32_t>(((r / 32) * 8 + k / 8) * 512 + (r % 32) * 16);
+  }
+};
+
+// An NT operand stored transposed, [K][N] with N contiguous: element (row n, column k) of the
+// operand at p[k * ld + n]. The LM head reads its weight W [V][H] this way as the gradient GEMM's
+// B operand (rows = hidden units, K = vocabulary), so that no transposed copy of W is needed.
+// Its LDS tiles are k-major and its MFMA fragments are assembled by transposing LDS reads
+// (gemm_lds.h, DmaTileK and frag_kmajor).
+struct KMajor {
+  static constexpr bool kChunkMajor = false;
+  static constexpr bool kKMajor = true;
+  const _Float16* p;
+  int64_t ld;  // elements between consecutive k
+  int rows;    // valid n
+  int k_len;   // valid k
+  __device__ __forceinline__ const _Float16* at(int n, int k) const {
+    return p + static_cast<int64_t>(k) * ld + n;
+  }
+  __device__ __forceinline__ bool tile_inside(int n0, int n_rows, int k0) const {
+    return n0 + n_rows <= rows && k0 + kBK <= k_len;
   }
 };
 

@@ -37,7 +37,7 @@
 
 namespace {
 
-using cm::gemm::Blocked64;
+using cm::gemm::KMajor;
 using cm::gemm::floatx16;
 using cm::gemm::half8;
 using cm::gemm::Tiled32;
@@ -187,10 +187,13 @@ struct EpiProbs {
         }
       }
       // E = e^{z - m_g} (in place of z) and the sums, relative to the group max
+      // e^{z - m_g} = 2^(z log2e - m_g log2e): one fused multiply-add for the argument
+      const float mg2 = mg * cm::kLog2e;
       float s = 0.0f, d = 0.0f;
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e) {
-        const float x = cm::exp_f(Z(e) - mg);  // 0 for kNoLogit rows, so x z = -0 there
+        // 0 for kNoLogit rows (the argument rounds to -inf), so x z = -0 there
+        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(Z(e), cm::kLog2e, -mg2));
         s += x;
         d += x * Z(e);
         Z(e) = x;
@@ -344,8 +347,8 @@ struct K1Job {
 
 // One K3 launch's arguments: G_s = G_s * factor + P W_c over K-slices of k_slice columns.
 struct K3Job {
-  Tiled32 A;    // E
-  Blocked64 B;  // W_c^T, 64-column panels
+  Tiled32 A;  // E
+  KMajor B;   // W_c as stored ([C][H], hidden contiguous), read as the operand W_c^T
   int tiles;  // output tiles; count = tiles * n_split workgroups
   int count;
   int k_slice;
@@ -378,7 +381,7 @@ __device__ __forceinline__ void k3_block(const K3Job& j, int bid, uint4* lds) {
   const int k_end = max(k_begin, min(j.A.k_len, k_begin + j.k_slice));
   EpiGrad epi{j.out.g[s], j.n_tok, j.hidden, j.factor, j.first, {}};  // f: start()
   ScaleP<kBM3 / kWM3 / 32> xp{j.scale, j.n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
-  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, Tiled32, Blocked64, EpiGrad,
+  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, Tiled32, KMajor, EpiGrad,
                      ScaleP<kBM3 / kWM3 / 32>, EDGE>(j.A, j.B, k_begin, k_end, tm, tn, epi, lds,
                                                      xp);
 }
@@ -648,25 +651,6 @@ int launch_final(int n_split, int n_tok, hipStream_t s, const RowState& rs, cons
   return cm::launch_status();
 }
 
-// W_c^T in panels: out[p][h][j] = W[c0 + 64 p + j][h], zero for 64 p + j >= n_voc.
-__global__ __launch_bounds__(kStatThreads) void lmh_transpose_kernel(
-    const _Float16* __restrict__ w, int64_t ld_w, int64_t c0, int n_voc, int hidden,
-    _Float16* __restrict__ wt) {
-  __shared__ _Float16 tile[64][66];
-  const int p = blockIdx.x, h0 = blockIdx.y * 64;
-  for (int i = threadIdx.x; i < 64 * 64; i += kStatThreads) {
-    const int r = i / 64, c = i % 64;  // r: vocabulary within the panel, c: hidden
-    const int v = p * 64 + r, h = h0 + c;
-    tile[r][c] = (v < n_voc && h < hidden) ? w[(c0 + v) * ld_w + h] : _Float16(0);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < 64 * 64; i += kStatThreads) {
-    const int r = i / 64, c = i % 64;  // r: hidden, c: vocabulary
-    const int h = h0 + r;
-    if (h < hidden) wt[(static_cast<int64_t>(p) * hidden + h) * 64 + c] = tile[c][r];
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
 // Workspace layout.
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
@@ -700,11 +684,10 @@ int n_split_for(int64_t n_rows, int hidden) {
 struct Layout {
   int64_t chunk, n_groups, n_chunks;
   int n_split;
-  int64_t off_e16, off_part, off_rows, off_labz, off_scale, off_g, off_wt, total;
+  int64_t off_e16, off_part, off_rows, off_labz, off_scale, off_g, total;
 };
 
-Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad,
-              bool need_wt) {
+Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad) {
   Layout L;
   L.chunk = chunk > 0 ? round_up(chunk, kChunkAlign) : default_chunk(n_rows, vocab);
   if (L.chunk > round_up(vocab, kChunkAlign)) L.chunk = round_up(vocab, kChunkAlign);
@@ -725,8 +708,6 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   off += round_up(n_rows * L.n_groups * 4, 256);
   L.off_g = off;
   off += (L.n_split - 1) * round_up(n_rows * hidden * 4, 256);
-  L.off_wt = off;
-  if (need_wt) off += round_up(static_cast<int64_t>(hidden) * L.chunk * 2, 256);
   L.total = off;
   return L;
 }
@@ -736,30 +717,28 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
 extern "C" int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_size,
                                                 int64_t chunk_cols) {
   if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0) return 0;
-  return layout(n_rows, vocab, hidden_size, chunk_cols, true, true).total;
+  return layout(n_rows, vocab, hidden_size, chunk_cols, true).total;
 }
 
 namespace {
 
 // Argument checks shared by both entry points (everything but the workspace).
 bool args_ok(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-             const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
+             const int64_t* target, int64_t n_rows, int64_t vocab,
              int hidden_size, int64_t chunk_cols, const float* loss, const float* entropy,
              const int32_t* correct) {
   if (!(n_rows > 0 && vocab > 0 && hidden_size > 0 && chunk_cols >= 0)) return false;
   if (!(hidden && weight && target && loss && entropy && correct)) return false;
   if (!(n_rows < (int64_t{1} << 31) && vocab < (int64_t{1} << 31))) return false;
   // 16-byte tile rows: hidden size, leading dimensions and bases multiples of 8 fp16.
-  if (!(hidden_size % 8 == 0 && ld_h % 8 == 0 && ld_w % 8 == 0 && ld_h >= hidden_size &&
-        ld_w >= hidden_size && cm::aligned(hidden, 16) && cm::aligned(weight, 16)))
-    return false;
-  return weight_t == nullptr || cm::aligned(weight_t, 16);
+  return hidden_size % 8 == 0 && ld_h % 8 == 0 && ld_w % 8 == 0 && ld_h >= hidden_size &&
+         ld_w >= hidden_size && cm::aligned(hidden, 16) && cm::aligned(weight, 16);
 }
 
 // The launches of one call (K1..K4 per chunk), on `ws` laid out as L; the arguments and the
 // workspace's size and alignment have been checked.
 int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-               const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
+               const int64_t* target, int64_t n_rows, int64_t vocab,
                int hidden_size, float* loss, float* entropy, int32_t* correct, float* grad,
                float grad_scale, char* ws, const Layout& L, hipStream_t s) {
   const bool want_grad = grad != nullptr;
@@ -772,7 +751,6 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
   gs.g[0] = grad;
   for (int i = 1; i < L.n_split; ++i)
     gs.g[i] = reinterpret_cast<float*>(ws + L.off_g + (i - 1) * round_up(n_rows * hidden_size * 4, 256));
-  _Float16* wt_ws = reinterpret_cast<_Float16*>(ws + L.off_wt);
   const _Float16* H16 = static_cast<const _Float16*>(hidden);
   const _Float16* W16 = static_cast<const _Float16*>(weight);
   const int n_tok = static_cast<int>(n_rows);
@@ -813,21 +791,9 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     }
     return cm::launch_status();
   };
-  // K3 of chunk c: G_s = G_s * factor + P W_c over K-slices, B = W_c^T in panels (the caller's
-  // cached transpose, or this chunk's transposed into the workspace first)
-  auto k3_job = [&](int64_t c, int* st) {
+  // K3 of chunk c: G_s = G_s * factor + P W_c over K-slices; B = W_c read as stored (k-major)
+  auto k3_job = [&](int64_t c) {
     const int n_voc = n_voc_of(c);
-    const _Float16* wt;
-    *st = 0;
-    if (weight_t) {
-      wt = static_cast<const _Float16*>(weight_t) + (c0_of(c) / kPanel) * hidden_size * kPanel;
-    } else {
-      dim3 tgrid((n_voc + kPanel - 1) / kPanel, (hidden_size + 63) / 64);
-      hipLaunchKernelGGL(lmh_transpose_kernel, tgrid, dim3(kStatThreads), 0, s, W16, ld_w,
-                         c0_of(c), n_voc, hidden_size, wt_ws);
-      *st = cm::launch_status();
-      wt = wt_ws;
-    }
     const int tiles = ((n_tok + kBM3 - 1) / kBM3) * ((hidden_size + kBN3 - 1) / kBN3);
     const int panels = (n_voc + kPanel - 1) / kPanel;
     // slices are whole statistics groups, so a stage never straddles two group scales
@@ -835,7 +801,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     const int k_slice = ((groups + L.n_split - 1) / L.n_split) * kGroup;
     const int count = tiles * L.n_split;
     K3Job j{Tiled32{e16_of(c), n_tok, n_voc, (n_tok + 31) / 32},
-            Blocked64{wt, hidden_size, n_voc},
+            KMajor{W16 + c0_of(c) * ld_w, ld_w, hidden_size, n_voc},
             tiles,
             count,
             k_slice,
@@ -858,9 +824,8 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     st = k2(c);
     if (st) return st;
     if (!want_grad) continue;
-    const K3Job j3 = k3_job(c, &st);
-    if (st) return st;
-    if (n_tok % kBM3 == 0 && hidden_size % kBN3 == 0) {
+    const K3Job j3 = k3_job(c);
+    if (n_tok % kBM3 == 0 && hidden_size % kBN3 == 0 && j3.A.k_len % kBK3 == 0) {
       hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeNever>, dim3(j3.count), dim3(kThreads3), 0, s, j3);
     } else {
       hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeAlways>, dim3(j3.count), dim3(kThreads3), 0, s,
@@ -883,13 +848,14 @@ extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight
                             void* workspace, int64_t workspace_bytes, void* stream) {
   CM_CHECK_ARG(n_rows >= 0);
   if (n_rows == 0) return 0;
-  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+  (void)weight_t;  // accepted for compatibility; the gradient GEMM reads the weight as stored
+  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                        chunk_cols, loss, entropy, correct));
   CM_CHECK_ARG(workspace != nullptr);
   const bool want_grad = grad != nullptr;
-  const Layout L = layout(n_rows, vocab, hidden_size, chunk_cols, want_grad, want_grad && !weight_t);
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk_cols, want_grad);
   CM_CHECK_ARG(workspace_bytes >= L.total && cm::aligned(workspace, 256));
-  return run_lmhead(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+  return run_lmhead(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                     loss, entropy, correct, grad, grad_scale, static_cast<char*>(workspace), L,
                     static_cast<hipStream_t>(stream));
 }
@@ -930,9 +896,9 @@ int scratch_of_current_device(char** out) {
 // The chunk the scratch can hold: chunk_cols itself when given (0 when it does not fit), else
 // the largest multiple of 256 columns (at most the whole vocabulary) whose layout fits.
 int64_t scratch_chunk(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_cols,
-                      bool want_grad, bool need_wt) {
+                      bool want_grad) {
   auto fits = [&](int64_t c) {
-    return layout(n_rows, vocab, hidden, c, want_grad, need_wt).total <= kScratchBytes;
+    return layout(n_rows, vocab, hidden, c, want_grad).total <= kScratchBytes;
   };
   if (chunk_cols > 0) return fits(chunk_cols) ? chunk_cols : 0;
   int64_t lo = 0, hi = round_up(vocab, kChunkAlign) / kChunkAlign;  // in units of 256 columns
@@ -953,18 +919,18 @@ extern "C" int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void
                                     void* stream) {
   CM_CHECK_ARG(n_rows >= 0);
   if (n_rows == 0) return 0;
-  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+  (void)weight_t;  // accepted for compatibility; the gradient GEMM reads the weight as stored
+  CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                        chunk_cols, loss, entropy, correct));
   const bool want_grad = grad != nullptr;
-  const bool need_wt = want_grad && !weight_t;
-  const int64_t chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad, need_wt);
+  const int64_t chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad);
   if (chunk == 0) return CM_ERROR_SCRATCH_TOO_SMALL;
-  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad, need_wt);
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad);
   if (L.total > kScratchBytes) return CM_ERROR_SCRATCH_TOO_SMALL;
   char* ws = nullptr;
   const int st = scratch_of_current_device(&ws);
   if (st) return st;
-  return run_lmhead(hidden, ld_h, weight, ld_w, weight_t, target, n_rows, vocab, hidden_size,
+  return run_lmhead(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                     loss, entropy, correct, grad, grad_scale, ws, L,
                     static_cast<hipStream_t>(stream));
 }

@@ -208,10 +208,9 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
  *   grad (if not NULL) [n_rows, H] fp32 = grad_scale * sum_v (softmax_v - [v == t_r]) W[v,:]
  *     (zero rows for unlabelled targets)
  * hidden fp16 [n_rows, H] (row stride ld_h), W fp16 [V, H] (row stride ld_w), target int64.
- * weight_t (may be NULL) is W transposed in 64-row panels: fp16 [ceil(V/64), H, 64] with
- * weight_t[p][h][j] = W[64 p + j][h] and zeros for 64 p + j >= V; without it the gradient pass
- * transposes each weight chunk into the workspace. H, ld_h, ld_w must be multiples of 8 and the
- * bases 16-byte aligned.
+ * weight_t is not read (any value, NULL included): the gradient pass reads W itself, through
+ * transposing LDS reads, so no transposed copy of the weight exists. H, ld_h, ld_w must be
+ * multiples of 8 and the bases 16-byte aligned.
  * The vocabulary is walked in chunks of chunk_cols columns (rounded up to a multiple of 256, at
  * most 262144; 0 = the library's default, which keeps the chunk buffer at 128 MiB or less); the
  * result does not depend on the chunk size beyond fp32 rounding.
@@ -236,8 +235,8 @@ int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_s
  * held by that GPU until the process ends; its device address is looked up once per device on
  * the first call with that device current, so call it with the stream's device current. The
  * vocabulary chunk is chunk_cols when given, else the largest multiple of 256 columns whose
- * workspace (cm_lmhead_ce_workspace_bytes with that chunk; less without a gradient or with
- * weight_t) fits the scratch: with the same chunk the results are bit-identical to
+ * workspace (cm_lmhead_ce_workspace_bytes with that chunk; less without a gradient) fits the
+ * scratch: with the same chunk the results are bit-identical to
  * cm_lmhead_ce's. Sizes whose smallest layout (or the given chunk's) does not fit return
  * CM_ERROR_SCRATCH_TOO_SMALL before anything is launched. Every call on one GPU uses that GPU's
  * one array: calls that overlap on one GPU (other streams, other threads) race; nothing in the

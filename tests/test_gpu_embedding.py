@@ -122,7 +122,7 @@ def test_fused_head_reads_the_fp16_weight(dev):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
     from claudemaxing_amd import apply
-    from claudemaxing_amd.lm_head_loss import _REQUEST_ATTR, fp16_head_weights
+    from claudemaxing_amd.lm_head_loss import _REQUEST_ATTR, fp16_head_weight
 
     apply()
     cfg = Qwen2Config(vocab_size=1000, hidden_size=64, intermediate_size=128,
@@ -143,5 +143,5 @@ def test_fused_head_reads_the_fp16_weight(dev):
     assert torch.isfinite(out.loss)
     w = model.get_input_embeddings().weight
     assert w.dtype == torch.float16
-    w16, _ = fp16_head_weights(w, False)
+    w16 = fp16_head_weight(w)
     assert w16.data_ptr() == w.data_ptr()

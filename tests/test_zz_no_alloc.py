@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 F16 = torch.float16
 
 
-def _noalloc(h16, w16, wt16, tgt, chunk, want_grad=True):
+def _noalloc(h16, w16, tgt, chunk, want_grad=True):
     n, hidden = h16.shape
     dev = h16.device
     loss = torch.full((n,), -7.0, device=dev)
@@ -29,7 +29,7 @@ def _noalloc(h16, w16, wt16, tgt, chunk, want_grad=True):
     grad = torch.full((n, hidden), -7.0, device=dev) if want_grad else None
     before = torch.cuda.memory_allocated(dev)
     rc = _lib.load().cm_lmhead_ce_noalloc(
-        h16.data_ptr(), h16.stride(0), w16.data_ptr(), w16.stride(0), _lib.ptr(wt16),
+        h16.data_ptr(), h16.stride(0), w16.data_ptr(), w16.stride(0), None,
         tgt.data_ptr(), n, w16.shape[0], hidden, chunk, loss.data_ptr(), ent.data_ptr(),
         corr.data_ptr(), _lib.ptr(grad), 1.0, _lib.stream(dev))
     assert torch.cuda.memory_allocated(dev) == before  # no allocation through torch either
@@ -45,33 +45,32 @@ def _same_bits(a, b, what):
 
 def test_noalloc_equals_workspace_entry_two_calls(dev):
     banner("lmhead noalloc: two calls, explicit chunks")
-    # call 1: 1100 rows, H 512, the full Qwen vocabulary in 4096-column chunks, W^T given
+    # call 1: 1100 rows, H 512, the full Qwen vocabulary in 4096-column chunks
     h, w, t = inputs.lm_head(5, n=1100, hidden=512)
     h16, w16, td = h.to(dev), w.to(dev), t.to(dev)
-    wt16 = LH.transpose_panels(w16)
-    rc, got = _noalloc(h16, w16, wt16, td, 4096)
+    rc, got = _noalloc(h16, w16, td, 4096)
     assert rc == 0, _lib.load().cm_error_string(rc)
-    ref = LH._fused_rows(h16, w16, td, True, 4096, wt16)
+    ref = LH._fused_rows(h16, w16, td, True, 4096)
     torch.cuda.synchronize()
     _same_bits(got, ref, "call 1")
     rows = torch.arange(0, 1100, 37)
     o = O.head(h[rows], w, t[rows])
     assert_close(got[0][rows.to(dev)], o[0], 1e-4, "call 1 loss vs oracle")
     assert_close(got[3][rows.to(dev)], o[3], 1e-2, "call 1 grad vs oracle")
-    # call 2, smaller: 300 rows, H 256, a 50,000-column vocabulary in 2048-column chunks, the
-    # kernel transposing each weight chunk itself (no W^T), on the scratch call 1 filled
+    # call 2, smaller: 300 rows, H 256, a 50,000-column vocabulary in 2048-column chunks, on
+    # the scratch call 1 filled
     h, w, t = inputs.lm_head(6, n=300, vocab=50000, hidden=256)
     h16, w16, td = h.to(dev), w.to(dev), t.to(dev)
-    rc, got = _noalloc(h16, w16, None, td, 2048)
+    rc, got = _noalloc(h16, w16, td, 2048)
     assert rc == 0, _lib.load().cm_error_string(rc)
-    ref = LH._fused_rows(h16, w16, td, True, 2048, None)
+    ref = LH._fused_rows(h16, w16, td, True, 2048)
     torch.cuda.synchronize()
     _same_bits(got, ref, "call 2")
     o = O.head(h, w, t)
     assert_close(got[0], o[0], 1e-4, "call 2 loss vs oracle")
     assert_close(got[3], o[3], 1e-2, "call 2 grad vs oracle")
     # and without a gradient (forward terms only)
-    rc, fwd = _noalloc(h16, w16, None, td, 2048, want_grad=False)
+    rc, fwd = _noalloc(h16, w16, td, 2048, want_grad=False)
     assert rc == 0
     torch.cuda.synchronize()
     _same_bits(fwd[:3], ref[:3], "call 3, no gradient")
@@ -81,10 +80,10 @@ def test_noalloc_own_chunk_and_refusal(dev):
     banner("lmhead noalloc: own chunk at config 4, refusal")
     h, w, t = inputs.lm_head(0)
     hd, wd, td = h.to(dev), w.to(dev), t.to(dev)
-    w16, wt16 = LH.fp16_head_weights(wd, True)
-    rc, got = _noalloc(hd, w16, wt16, td, 0)
+    w16 = LH.fp16_head_weight(wd)
+    rc, got = _noalloc(hd, w16, td, 0)
     assert rc == 0, _lib.load().cm_error_string(rc)
-    ref = LH._fused_rows(hd, w16, td, True, None, wt16)
+    ref = LH._fused_rows(hd, w16, td, True, None)
     torch.cuda.synchronize()
     assert_close(got[0], ref[0], 1e-5, "loss")
     assert_close(got[1], ref[1], 1e-5, "entropy")
@@ -94,7 +93,7 @@ def test_noalloc_own_chunk_and_refusal(dev):
         gaps, ulps = O.top2_gap(h[diff], w)
         assert torch.all(gaps <= ulps)
     # a whole-vocabulary chunk at this size needs ~650 MB: refused, nothing written
-    rc, out = _noalloc(hd, w16, wt16, td, 151936)
+    rc, out = _noalloc(hd, w16, td, 151936)
     assert rc == 20001  # CM_ERROR_SCRATCH_TOO_SMALL
     assert b"scratch" in _lib.load().cm_error_string(rc)
     torch.cuda.synchronize()
