@@ -26,10 +26,12 @@
 //               is applied only here, in fp32.
 //
 // The full [tokens, vocab] logits never exist: one fp16 chunk of E (at most 128 MiB by default)
-// lives in the workspace, in 4 KiB blocks of 32 tokens x 64 columns (Tiled32), and the transposed
-// weight in 64-column panels ([V/64][H][64]), so that every K3 operand tile is one contiguous
-// span.
+// lives in the workspace, in 4 KiB blocks of 32 tokens x 64 columns (Tiled32), so that every K3
+// A tile is one contiguous span. Both GEMMs read the weight [V][H] as stored: K1 as a row-major
+// operand, K3 as a k-major one (vocabulary = K), whose LDS tiles are transposed into MFMA
+// fragments by ds_read_b64_tr_b16.
 #include <mutex>
+#include <numeric>
 
 #include "common.h"
 #include "gemm_lds.h"
@@ -43,6 +45,7 @@ using cm::gemm::half8;
 using cm::gemm::Tiled32;
 using cm::gemm::RowMajor;
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPanel = 64;          // columns per panel of the blocked layouts
 // Logit given to vocabulary rows past a chunk's last column in K1's epilogue: below every fp16
@@ -97,9 +100,9 @@ struct Partial {
 // K1 epilogue: the tile is Z^T (rows = vocabulary columns of the chunk, cols = tokens). A
 // wavefront's rows are one statistics group of kGroup columns, and a lane holds the logits of
 // one token. E (layout Tiled32: 32 tokens x 64 columns per 4 KiB block, 8-column chunks inside)
-// is written straight from the registers: a lane's entries 4b .. 4b + 3 are rows 8b + 4h .. 8b + 4h + 3 of the group (h = the
-// lane's half of the wavefront), so after each pair of blocks (b, b + 1) trades halves across
-// the two 32-lane halves (v_permlane32_swap_b32: the first operand's upper 32 lanes swap with the
+// is written straight from the registers: a lane's entries 4b .. 4b + 3 are rows
+// 8b + 4h .. 8b + 4h + 3 of the group (h = the lane's half of the wavefront), so after each pair
+// of blocks (b, b + 1) trades halves across the two 32-lane halves (v_permlane32_swap_b32: the first operand's upper 32 lanes swap with the
 // second operand's lower 32 lanes) lane l < 32 holds all 8 rows of block b and lane l + 32 those
 // of block b + 1. One 16-byte store each, 1 KiB contiguous per wavefront instruction, no LDS
 // staging and no barrier.
@@ -211,9 +214,13 @@ struct EpiProbs {
           const auto s0 = __builtin_amdgcn_permlane32_swap(pack(4 * b), pack(4 * b + 4), false, false);
           const auto s1 = __builtin_amdgcn_permlane32_swap(pack(4 * b + 2), pack(4 * b + 6), false, false);
           // lane l < 32: block b, rows 0-3 (its own) then 4-7; lane l + 32: block b + 1
-          const uint4 chunk{s0[0], s1[0], s0[1], s1[1]};
+          const u32x4 chunk{s0[0], s1[0], s0[1], s1[1]};
           const int v = mb + 8 * (b + half_id);  // first vocabulary column (of the chunk)
-          if (tok_ok) *reinterpret_cast<uint4*>(e16 + Tiled32::index(tok, v, row_blocks)) = chunk;
+          // streamed past the caches: K3 reads E only after K1 has finished every tile
+          // (1.7% off the call against plain stores, same-process A/B)
+          if (tok_ok)
+            __builtin_nontemporal_store(
+                chunk, reinterpret_cast<u32x4*>(e16 + Tiled32::index(tok, v, row_blocks)));
         }
       }
 #undef Z
@@ -656,18 +663,24 @@ int launch_final(int n_split, int n_tok, hipStream_t s, const RowState& rs, cons
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 constexpr int64_t kChunkAlign = kBM1 > 256 ? kBM1 : 256;
+constexpr int64_t kCUs = 256;  // MI355X compute units (8 XCDs x 32)
 
 int64_t default_chunk(int64_t n_rows, int64_t vocab) {
-  // E chunk of at most 128 MiB (fp16, n_rows x C), split into equal chunks. Per extra chunk the
-  // gradient GEMM's split-K slices are read and rewritten once more (4 x 12.6 MB at N = 2048)
-  // and each kernel ramps up once more; measured at N = 2048, V = 151936 (one MI355X, same box):
-  // 8192 columns 2.58-2.63 ms, 16384 2.29-2.44 ms, 32768 2.23-2.30 ms, the whole vocabulary in
-  // one chunk (a 622 MB E) 2.28-2.35 ms.
+  // E chunk of at most 128 MiB (fp16, n_rows x C). Per extra chunk the gradient GEMM's split-K
+  // slices are read and rewritten once more (4 x 12.6 MB at N = 2048) and each kernel ramps up
+  // once more. K1 runs one 256 x 256 workgroup per CU, so a chunk whose vocabulary tiles times
+  // token tiles is a multiple of 256 fills whole waves of the chip; the largest such chunk within
+  // the budget is taken (the last chunk takes the remainder), else the vocabulary is split into
+  // equal chunks. Measured at N = 2048, V = 151936 (one MI355X, one process, interleaved):
+  // 4 x 32768 + 20864 columns 2092 us, 5 x 30464 2105 us, 24576 2115 us, 16384 2171 us.
   const int64_t budget = (int64_t{128} << 20) / 2 / (n_rows > 0 ? n_rows : 1);  // columns
   int64_t c = budget / kChunkAlign * kChunkAlign;
   if (c < 4096) c = 4096;
   if (c > kMaxChunk) c = kMaxChunk;
   if (c >= vocab) return round_up(vocab, kChunkAlign);
+  const int64_t token_tiles = (n_rows + kBN1 - 1) / kBN1;
+  const int64_t wave_cols = kBM1 * (kCUs / std::gcd(token_tiles, kCUs));
+  if (wave_cols <= c) return c / wave_cols * wave_cols;
   const int64_t n_chunks = (vocab + c - 1) / c;
   return round_up((vocab + n_chunks - 1) / n_chunks, kChunkAlign);
 }
@@ -675,7 +688,7 @@ int64_t default_chunk(int64_t n_rows, int64_t vocab) {
 // K-slices of the gradient GEMM: as many as keep the grid within one workgroup per CU (256).
 int n_split_for(int64_t n_rows, int hidden) {
   const int64_t tiles = ((n_rows + kBM3 - 1) / kBM3) * ((hidden + kBN3 - 1) / kBN3);
-  int64_t s = 256 / (tiles > 0 ? tiles : 1);
+  int64_t s = kCUs / (tiles > 0 ? tiles : 1);
   if (s < 1) s = 1;
   if (s > kMaxSplit) s = kMaxSplit;
   return static_cast<int>(s);

@@ -204,3 +204,28 @@ def test_nf4_linear_argument_checks(lib):
     # 2 int64, 1 pointer
     assert _lib.NF4Weight.rows.offset == 64 and _lib.NF4Weight.scale_map.offset == 80
     assert ctypes.sizeof(_lib.NF4Weight) == 88
+
+
+
+def test_lmhead_default_chunk(lib):
+    """The LM head's default vocabulary chunk keeps E (fp16, tokens x chunk) within 128 MiB and,
+    where the chip's 256 CUs allow it, fills whole waves of K1's 256 x 256 workgroups: at 2048
+    tokens (8 token tiles) a multiple of 32 vocabulary tiles, i.e. 4 chunks of 32768 columns and
+    the remainder; at 1193 tokens (5 token tiles, no whole-wave chunk within the budget) equal
+    chunks. The workspace grows with the chunk, so the default is the chunk whose workspace
+    matches chunk_cols = 0."""
+    ws = lib.cm_lmhead_ce_workspace_bytes
+    V, H = 151936, 1536
+
+    def default_chunk(n):
+        target = ws(n, V, H, 0)
+        hits = [c for c in range(256, V + 256, 256) if ws(n, V, H, c) == target]
+        assert len(hits) == 1, (n, hits)
+        return hits[0]
+
+    assert default_chunk(2048) == 32768
+    assert default_chunk(4096) == 16384
+    assert default_chunk(1193) == 50688  # 3 equal chunks, 256-aligned
+    assert default_chunk(16) == V // 256 * 256 + 256  # the whole vocabulary in one chunk
+    for n in (64, 1193, 2048, 4096, 16384):
+        assert (n + 31) // 32 * 32 * default_chunk(n) * 2 <= 128 << 20, n
