@@ -147,6 +147,19 @@ def train_step(model, opt, scaler, batch, fused=True, metrics=None):
     return out.loss.detach()
 
 
+_CAPTURE_STREAMS = {}
+
+
+def _capture_stream(device):
+    """The one side stream of `device` on which every GraphedStep warms up and captures. torch
+    keeps a hipBLAS and a hipBLASLt workspace per stream (76 MiB each on this stack) for as long
+    as the process lives, so a fresh stream per capture would pin another pair every time."""
+    s = _CAPTURE_STREAMS.get(device)
+    if s is None:
+        s = _CAPTURE_STREAMS[device] = torch.cuda.Stream(device)
+    return s
+
+
 class GraphedStep:
     """The same training step with the packed forward and the scaled backward replayed from one
     HIP graph. The step issues ~5000 kernels, and in eager mode the host's launch cost exceeds
@@ -171,7 +184,7 @@ class GraphedStep:
         self.packed = _pack_batch(model, kwargs, batch["labels"])
         if self.packed is None:
             raise ValueError("GraphedStep needs a padded batch with pads to pack out")
-        side = torch.cuda.Stream()
+        side = _capture_stream(next(model.parameters()).device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(warmup):
@@ -180,7 +193,7 @@ class GraphedStep:
         torch.cuda.current_stream().wait_stream(side)
         self._zero()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=side):
             self.loss = self._forward_backward()
 
     def _zero(self):
@@ -205,6 +218,14 @@ class GraphedStep:
         for name in ("ids", "pos", "mask", "target", "index"):
             getattr(self.packed, name).copy_(getattr(packed, name))
 
+    def pool_bytes(self):
+        """Bytes of the segments of the graph's private memory pool: the activations and
+        temporaries of the captured pass, which replays reuse. torch counts them as allocated
+        only while the capture runs, so a replay's allocated bytes leave them out."""
+        pool = tuple(self.graph.pool())
+        return sum(seg["total_size"] for seg in torch.cuda.memory_snapshot()
+                   if tuple(seg.get("segment_pool_id", ())) == pool)
+
     def step(self):
         """Replay forward + backward, then the GradScaler step with AdamW; the loss tensor."""
         self.graph.replay()
@@ -216,7 +237,9 @@ class GraphedStep:
 def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
     """Median and all per-step wall times (ms), each step between two device syncs as the
     reference's harness probe times them; peak HBM over the timed steps. With graphed, the
-    steps replay a GraphedStep captured first (the capture and its warm-up are not timed)."""
+    steps replay a GraphedStep captured first (the capture and its warm-up are not timed), and
+    graph_pool_gb is the size of its private pool, which the replay's allocated bytes leave
+    out."""
     if graphed:
         gstep = GraphedStep(model, opt, scaler, batch)
         run = gstep.step
@@ -235,10 +258,13 @@ def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
     ordered = sorted(times)
-    return dict(median_ms=ordered[len(ordered) // 2], step_ms=times,
-                peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
-                peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30,
-                losses=[float(x) for x in losses])
+    out = dict(median_ms=ordered[len(ordered) // 2], step_ms=times,
+               peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
+               peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30,
+               losses=[float(x) for x in losses])
+    if graphed:
+        out["graph_pool_gb"] = gstep.pool_bytes() / 2 ** 30
+    return out
 
 
 def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, graphed=False):

@@ -122,6 +122,25 @@ def test_graphed_step_matches_eager(dev):
 
 
 @pytest.mark.gpu
+def test_graph_captures_do_not_accumulate_memory(dev):
+    """A new GraphedStep per batch (packed shapes change every step in SFT) keeps the HBM in use
+    flat: every capture warms up and records on the one side stream of the device, so torch's
+    per-stream BLAS workspaces are made once, and each graph's pool is released with the graph.
+    Five captures after the first two may not raise the allocated bytes by more than 4 MiB."""
+    banner("qlora step: 7 graph captures over distinct batches, 2 layers")
+    model = qlora_step.build_model(dev, seed=0, **TWO_LAYERS)
+    opt = qlora_step.make_optimizer(model)
+    scaler = torch.amp.GradScaler("cuda")
+    held = []
+    for i in range(7):
+        batch, _ = qlora_step.make_batch(dev, seed=100 + i)
+        float(qlora_step.GraphedStep(model, opt, scaler, batch, warmup=1).step())
+        torch.cuda.synchronize()
+        held.append(torch.cuda.memory_allocated())
+    assert held[-1] - held[1] <= 4 << 20, [h / 2 ** 20 for h in held]
+
+
+@pytest.mark.gpu
 def test_graphed_step_trains_with_dropout(dev):
     banner("qlora step: graphed with dropout, 2 layers, 4 steps")
     model = qlora_step.build_model(dev, seed=0, **TWO_LAYERS)
