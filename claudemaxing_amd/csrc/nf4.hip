@@ -32,6 +32,7 @@ constexpr int kThreads = 256;
 #define CM_NF4_NT_STORE 1
 #endif
 constexpr int kUnits = CM_NF4_UNITS;  // 4-byte units per lane
+constexpr int64_t kResidentBlocks = 2048;  // 256-lane workgroups the chip holds at once
 
 template <bool NESTED>
 __device__ __forceinline__ float block_scale(const void* absmax, const float* code2,
@@ -90,55 +91,77 @@ struct Pack8<float> {
   }
 };
 
-// Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes. Every
-// global load of a lane is issued at the start, independent of the others: its packed words,
-// the absmax byte (or fp32 absmax) and the absmax2 entry of each of its units, one entry of the
-// 256-entry code2 table (staged in LDS beside the 16-entry code table); after the one barrier
-// the nested scale is code2[q8] from LDS times absmax2 plus offset. (Decoding the scale from a
-// global code2[q8] made the gather a second memory round trip before the first store.)
-template <typename OutT, bool NESTED>
+// Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes. A
+// workgroup's 1024 units span at most 256 absmax blocks (blocksize >= 32 elements = 4 units), and
+// lane t stages block blk0 + t in LDS: its absmax byte and absmax2 entry (or its fp32 absmax),
+// with one entry of the 256-entry code2 table per lane and the 16-entry code table. Those loads
+// are issued first, then the lane's packed words; one barrier, after which a unit's scale is
+// code2[q8] * absmax2 + offset from LDS. A lane thus issues its 4 word loads and at most 3
+// coalesced others (loading the absmax byte and absmax2 entry per unit took 12, and the kernel
+// 7.2 us at [8960,1536] against 6.0 us for the same loads and stores without the decode; now
+// 6.7 us). SCALES_FIRST issues the block loads before the packed words: faster when every
+// workgroup of the launch is resident at once (the barrier waits on the earliest loads), slower
+// by ~3% for a streaming launch of many waves of workgroups, which issues the words first.
+// Both orders compute the same values.
+template <typename OutT, bool NESTED, bool SCALES_FIRST>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
     const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
     const float* __restrict__ code, const float* __restrict__ code2,
     const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
     OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
   static_assert(kThreads >= 256, "one code2 entry per lane");
+  static_assert(kThreads * kUnits / 4 <= kThreads, "one absmax block of the range per lane");
   __shared__ float s_code[16];
   __shared__ float s_code2[NESTED ? 256 : 1];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnits) + threadIdx.x;
+  __shared__ uint2 s_blk[kThreads];  // block blk0 + t: {absmax byte, absmax2 bits} or {-, absmax}
+  const int t = threadIdx.x;
+  const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnits);
+  const uint32_t blk0 = static_cast<uint32_t>(u0 >> unit_shift);
+  // blocks in the workgroup's range (1 when the range lies inside one block)
+  const int nb = unit_shift < 30 && ((kThreads * kUnits) >> unit_shift) > 0
+                     ? (kThreads * kUnits) >> unit_shift
+                     : 1;
+  uint32_t q8 = 0;
+  float a2 = 0.0f, c = 0.0f, c2 = 0.0f;
   uint32_t word[kUnits];
-  uint32_t q8[kUnits];   // nested: absmax byte of the unit's block
-  float a2[kUnits];      // nested: absmax2 of it; plain: the block's fp32 absmax
+  auto load_words = [&] {
 #pragma unroll
-  for (int j = 0; j < kUnits; ++j) {
-    const int64_t u = base + j * kThreads;
-    const bool ok = u < n_units;
-    word[j] = ok ? __builtin_nontemporal_load(packed + u) : 0u;
-    // 8 elements of unit u start at element 8u; blocksize = 8 << unit_shift elements.
-    const uint32_t blk = ok ? static_cast<uint32_t>(u >> unit_shift) : 0u;
-    if constexpr (NESTED) {
-      q8[j] = static_cast<const uint8_t*>(absmax)[blk];
-      a2[j] = absmax2[bs2_shift >= 0 ? (blk >> bs2_shift) : (blk / bs2)];
-    } else {
-      a2[j] = static_cast<const float*>(absmax)[blk];
+    for (int j = 0; j < kUnits; ++j) {
+      const int64_t u = u0 + t + j * kThreads;
+      word[j] = u < n_units ? __builtin_nontemporal_load(packed + u) : 0u;
+    }
+  };
+  if constexpr (!SCALES_FIRST) load_words();
+  if (t < nb) {
+    const uint32_t blk = blk0 + t;
+    if ((static_cast<int64_t>(blk) << unit_shift) < n_units) {
+      if constexpr (NESTED) {
+        q8 = static_cast<const uint8_t*>(absmax)[blk];
+        a2 = absmax2[bs2_shift >= 0 ? (blk >> bs2_shift) : (blk / bs2)];
+      } else {
+        a2 = static_cast<const float*>(absmax)[blk];
+      }
     }
   }
-  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
-  if constexpr (NESTED) {
-    if (threadIdx.x < 256) s_code2[threadIdx.x] = code2[threadIdx.x];
-  }
+  if (t < 16) c = code[t];
+  if constexpr (NESTED) c2 = code2[t];
+  if constexpr (SCALES_FIRST) load_words();
+  if (t < nb) s_blk[t] = uint2{q8, __builtin_bit_cast(uint32_t, a2)};
+  if (t < 16) s_code[t] = c;
+  if constexpr (NESTED) s_code2[t] = c2;
   const float offset = NESTED ? *offset_ptr : 0.0f;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kUnits; ++j) {
-    const int64_t u = base + j * kThreads;
+    const int64_t u = u0 + t + j * kThreads;
     if (u >= n_units) break;
+    const uint2 e = s_blk[static_cast<uint32_t>(u >> unit_shift) - blk0];
     float s;
     if constexpr (NESTED) {
-      const float prod = s_code2[q8[j]] * a2[j];  // multiply, then add (no contraction)
+      const float prod = s_code2[e.x] * __builtin_bit_cast(float, e.y);  // multiply, then add
       s = prod + offset;
     } else {
-      s = a2[j];
+      s = __builtin_bit_cast(float, e.y);
     }
     float v[8];
 #pragma unroll
@@ -242,10 +265,13 @@ int launch(const uint8_t* packed, const void* absmax, const float* code, const f
       const int64_t blocks = (n_units + per_block - 1) / per_block;
       if (blocks > 0x7fffffff) return static_cast<int>(hipErrorInvalidValue);
       // unit u covers elements [8u, 8u+8): block index = 8u / blocksize = u >> (bs_shift - 3)
-      hipLaunchKernelGGL((nf4_dequant_vec<OutT, NESTED>), dim3(static_cast<uint32_t>(blocks)),
-                         dim3(kThreads), 0, stream, reinterpret_cast<const uint32_t*>(packed),
-                         absmax, code, code2, absmax2, offset, out, n_units, bs_shift - 3,
-                         bs2_shift, static_cast<uint32_t>(blocksize2));
+      // one wave of resident workgroups (256 CUs x 8) or fewer: latency-bound, block loads first
+      auto kern = blocks <= kResidentBlocks ? nf4_dequant_vec<OutT, NESTED, true>
+                                            : nf4_dequant_vec<OutT, NESTED, false>;
+      hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
+                         reinterpret_cast<const uint32_t*>(packed), absmax, code, code2,
+                         absmax2, offset, out, n_units, bs_shift - 3, bs2_shift,
+                         static_cast<uint32_t>(blocksize2));
       int st = cm::launch_status();
       if (st) return st;
     }

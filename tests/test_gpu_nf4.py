@@ -53,6 +53,20 @@ def test_config1_gate_proj(dev):
     assert err < 0.02, err
 
 
+@pytest.mark.parametrize("blocksize", [32, 64, 4096])
+def test_streaming_launch_matches_oracle(blocksize, dev):
+    """A weight large enough that the launch holds more workgroups than the chip keeps resident
+    (one layer's NF4 weights, 46.6M elements: 5688 workgroups of 1024 packed words): that launch
+    issues its packed words before the block loads, the resident-sized ones the other way round,
+    and both must give the oracle's bits."""
+    banner(f"nf4 streaming launch, one layer's weights, blocksize {blocksize}")
+    w = torch.randn(30336, 1536, generator=torch.Generator().manual_seed(3)) * 0.02
+    packed, state = quantize_nf4(w, blocksize, True)
+    out = dequantize_nf4(packed.to(dev), state.to(dev), torch.float16)
+    torch.cuda.synchronize()
+    assert_bits_equal(out, oracle_of(packed, state, torch.float16), f"streaming bs {blocksize}")
+
+
 def test_every_byte_with_every_q8_code(dev):
     banner("nf4 exhaustive bytes x q8")
     code2 = torch.from_numpy(O.dynamic_map())
