@@ -142,6 +142,22 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
+# torch's C accessor of the current stream's raw handle (what torch.cuda.current_stream(d)
+# .cuda_stream returns, without building a Stream object: 0.07 us against 1.9 us per call on the
+# MI355X box's host, and every launch asks for it); the public call where it is absent
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device=None):
     """Handle of torch's current stream on `device`, for the stream argument."""
-    return torch.cuda.current_stream(device).cuda_stream
+    if _RAW_STREAM is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, torch.device):
+        index = device.index
+    elif device is None:
+        index = None
+    else:
+        index = torch.device(device).index if isinstance(device, str) else int(device)
+    if index is None:
+        index = torch.cuda.current_device()
+    return _RAW_STREAM(index)
