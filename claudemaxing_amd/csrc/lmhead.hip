@@ -153,9 +153,12 @@ struct EpiProbs {
       // no fp16 logit reaches and whose e^{z - m} is 0, so the loops below need no validity
       // test per element
 #define Z(e) acc[(e) / 16][nt][(e) % 16]
+      // A plain conversion (an accumulator, not a product, so there is no multiply for the
+      // compiler to fuse it with): it can be computed for every element and selected, where
+      // cm::from_f32's register pin made the compiler branch around each conversion.
 #pragma unroll
       for (int e = 0; e < TM * 16; ++e)
-        Z(e) = mb + vrow(e) < n_voc ? static_cast<float>(cm::from_f32<_Float16>(Z(e))) : kNoLogit;
+        Z(e) = mb + vrow(e) < n_voc ? static_cast<float>(static_cast<_Float16>(Z(e))) : kNoLogit;
       // group max and first argmax over both halves of the wavefront (branch-free)
       float m = kNoLogit;
       int best = -1;
@@ -206,7 +209,7 @@ struct EpiProbs {
       if (store) {
         // entries 4b .. 4b + 3 = rows 8b + 4h .. 8b + 4h + 3 (vrow(4b) = 8b + 4h)
         auto pack = [&](int e) {  // two fp16 of entries e, e + 1 as one dword
-          const half2v v{cm::from_f32<_Float16>(Z(e)), cm::from_f32<_Float16>(Z(e + 1))};
+          const half2v v{static_cast<_Float16>(Z(e)), static_cast<_Float16>(Z(e + 1))};
           return __builtin_bit_cast(uint32_t, v);
         };
 #pragma unroll
