@@ -453,166 +453,3 @@ __device__ __forceinline__ void gemm_lds(const SrcA& A, const SrcB& B, int k_beg
 
 }  // namespace gemm
 }  // namespace cm
-
-namespace cm {
-namespace gemm {
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-// The same NT GEMM on four wavefronts (2 x 2), one per SIMD, each holding a 128 x 128 sub-tile
-// of a 256 x 256 tile as 8 x 8 v_mfma_f32_16x16x32_f16 tiles (256 fp32 accumulators per lane,
-// which the compiler keeps in the accumulation registers). Per 32-column substep a wavefront
-// reads 8 + 8 fragments (16 ds_read_b128) for 64 MFMAs: a third less LDS read traffic per MFMA
-// than eight wavefronts of 128 x 64. Operand layouts, direct loads, LDS tiles and the stage ring
-// are those of gemm_lds. MFMA lane layout (checked on the box): A lane l holds row l % 16,
-// columns 8 (l / 16) .. + 7; B likewise (row = output column); D lane l, register r holds row
-// 4 (l / 16) + r, column l % 16.
-// The epilogue receives floatx4 acc[8][8] (tile (i, j) = rows mb + 16 i .., columns nb + 16 j ..).
-template <int BK, int S, class SrcA, class SrcB, class Epi, class FX = PlainA,
-          int EDGE = kEdgeEither>
-__device__ __forceinline__ void gemm_lds_w4(const SrcA& A, const SrcB& B, int k_begin, int k_end,
-                                            int tm, int tn, Epi& epi, uint4* lds, FX fx = FX()) {
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, NW = WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 16, TN = WTN / 16;  // 8 x 8 MFMA tiles per wavefront
-  using LA = LdsTile<BK, SrcA::kChunkMajor, BM>;
-  using LB = LdsTile<BK, SrcB::kChunkMajor, BN>;
-  constexpr int KS = BK / 32;  // MFMA substeps per stage
-  static_assert(S >= 2, "at least a double buffer");
-  static_assert(KS == 2, "two substeps per stage (BK = 64)");
-  constexpr int kStage = (BM + BN) * LA::kRC;  // uint4 per stage
-  using TA = DmaTile<BM, NW, BK, SrcA::kChunkMajor>;
-  using TB = DmaTile<BN, NW, BK, SrcB::kChunkMajor>;
-  constexpr int kDma = TA::kPer + TB::kPer;  // 16 direct loads per lane per stage
-  constexpr int kQuarters = 4;               // MFMA groups per substep
-  constexpr int kDmaQ = kDma / (KS * kQuarters);
-  static_assert(kDmaQ * KS * kQuarters == kDma, "loads split evenly over the quarters");
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int wm = wave / WN, wn = wave % WN;
-  TA la;
-  TB lb;
-  la.init(A, wave, lane);
-  lb.init(B, wave, lane);
-  epi.template prepare<TM, TN>(m0 + wm * WTM, n0 + wn * WTN, lane);
-
-  floatx4 acc[TM][TN];
-  epi.template start<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
-
-  const int n_kt = (k_end - k_begin + BK - 1) / BK;
-  auto inside_a = [&](int kt) { return A.tile_inside(m0, BM, k_begin + kt * BK); };
-  auto inside_b = [&](int kt) { return B.tile_inside(n0, BN, k_begin + kt * BK); };
-  const bool all_inside = n_kt > 0 && inside_a(n_kt - 1) && inside_b(n_kt - 1);
-  auto issue = [&](int kt, int q, bool in_a, bool in_b, auto edge) {
-    uint4* st = lds + (kt % S) * kStage;
-    const int k0 = k_begin + kt * BK;
-    if (q < TA::kPer) {
-      if constexpr (decltype(edge)::value) la.issue(A, m0, k0, st, wave, q, in_a);
-      else la.issue_inside(A, m0, k0, st, wave, q);
-    } else {
-      if constexpr (decltype(edge)::value) lb.issue(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer, in_b);
-      else lb.issue_inside(B, n0, k0, st + BM * LA::kRC, wave, q - TA::kPer);
-    }
-  };
-  const int arow = wm * WTM + lane % 16, brow = wn * WTN + lane % 16;
-  half8 af[2][TM], bf[2][TN];
-  // fragments of quarter qq (A tiles 2 qq, 2 qq + 1 and B tiles 2 qq, 2 qq + 1) of substep ks
-  auto read_q = [&](int kt, int ks, int buf, int qq) {
-    const uint4* As = lds + (kt % S) * kStage;
-    const uint4* Bs = As + BM * LA::kRC;
-    const int ch = ks * 4 + lane / 16;
-#pragma unroll
-    for (int i = 2 * qq; i < 2 * qq + 2; ++i) af[buf][i] = fx.apply(LA::frag(As, arow + i * 16, ch), i);
-#pragma unroll
-    for (int j = 2 * qq; j < 2 * qq + 2; ++j) bf[buf][j] = LB::frag(Bs, brow + j * 16, ch);
-  };
-  // the 16 MFMAs of quarter qq: A tiles 2 qq and 2 qq + 1 against all 8 B tiles, on fragments
-  // of the previous substep (all read during its four quarters)
-  auto mfma_q = [&](int b, int qq) {
-#pragma unroll
-    for (int i = 2 * qq; i < 2 * qq + 2; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[b][i], bf[b][j], acc[i][j], 0, 0, 0);
-  };
-  auto interleave = [] {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-    }
-  };
-
-  fx.bind(m0 + wm * WTM + lane % 16);
-  if (n_kt > 0) fx.prefetch(k_begin);
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s) {
-    if (s < n_kt) {
-      const bool ia = inside_a(s), ib = inside_b(s);
-#pragma unroll
-      for (int q = 0; q < kDma; ++q) issue(s, q, ia, ib, std::true_type{});
-    }
-  }
-  epi.template started<TM, TN>(acc);
-
-  // Stage kt: after the barrier, the quarters of substep 1 of stage kt - 1 (deferred) are
-  // multiplied while substep 0's fragments of stage kt are read, then substep 0 is multiplied
-  // while substep 1's fragments are read. Each quarter also issues its share of stage
-  // kt + S - 1's direct loads.
-  auto run = [&](auto edge) {
-    for (int kt = 0; kt < n_kt; ++kt) {
-      if (kt + S - 2 < n_kt) {
-        wait_vmcnt<(S - 2) * kDma>();
-      } else {
-        wait_vmcnt<0>();
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      lds_barrier();
-      fx.advance();
-      if (kt + 1 < n_kt) fx.prefetch(k_begin + (kt + 1) * BK);
-      const int kl = kt + S - 1;
-      const bool load = kl < n_kt;
-      bool ia = true, ib = true;
-      if constexpr (decltype(edge)::value) {
-        ia = load && inside_a(kl);
-        ib = load && inside_b(kl);
-      }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int b_read = ks & 1;        // buffer of the fragments read now (substep ks)
-        const int b_mul = b_read ^ 1;     // buffer multiplied now (the previous substep)
-        const bool mul = ks > 0 || kt > 0;
-#pragma unroll
-        for (int qq = 0; qq < kQuarters; ++qq) {
-          read_q(kt, ks, b_read, qq);
-          if (mul) {
-            mfma_q(b_mul, qq);
-            interleave();
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          if (load) {
-#pragma unroll
-            for (int q = (ks * kQuarters + qq) * kDmaQ; q < (ks * kQuarters + qq + 1) * kDmaQ; ++q)
-              issue(kl, q, ia, ib, edge);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
-  };
-  if constexpr (EDGE == kEdgeEither) {
-    if (all_inside) run(std::false_type{}); else run(std::true_type{});
-  } else {
-    (void)all_inside;
-    run(std::bool_constant<EDGE == kEdgeAlways>{});
-  }
-  if (n_kt > 0) {
-#pragma unroll
-    for (int qq = 0; qq < kQuarters; ++qq) mfma_q(1, qq);
-  }
-  epi.template apply<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds);
-}
-
-}  // namespace gemm
-}  // namespace cm

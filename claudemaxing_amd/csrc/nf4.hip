@@ -25,9 +25,6 @@ constexpr int kThreads = 256;
 #ifndef CM_NF4_UNITS
 #define CM_NF4_UNITS 4
 #endif
-#ifndef CM_NF4_WIDE
-#define CM_NF4_WIDE 0
-#endif
 #ifndef CM_NF4_NT_STORE
 #define CM_NF4_NT_STORE 1
 #endif
@@ -174,37 +171,6 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
   }
 }
 
-// Wide path: a lane handles 16 packed bytes (one 16-byte load, 32 outputs, one block scale
-// because blocksize >= 32), written as four 16-byte stores. Units [0, n_units) of 16 bytes.
-template <typename OutT, bool NESTED>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_wide(
-    const uint4* __restrict__ packed, const void* __restrict__ absmax,
-    const float* __restrict__ code, const float* __restrict__ code2,
-    const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
-    OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
-  __shared__ float s_code[16];
-  if (threadIdx.x < 16) s_code[threadIdx.x] = code[threadIdx.x];
-  const float offset = NESTED ? *offset_ptr : 0.0f;
-  __syncthreads();
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (u >= n_units) return;
-  const uint4 word = packed[u];
-  const uint32_t blk = static_cast<uint32_t>(u >> unit_shift);
-  const float s = block_scale<NESTED>(absmax, code2, absmax2, offset, blk, bs2_shift, bs2);
-  const uint32_t w4[4] = {word.x, word.y, word.z, word.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float v[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t byte = (w4[q] >> (8 * k)) & 0xffu;
-      v[2 * k] = s_code[byte >> 4] * s;
-      v[2 * k + 1] = s_code[byte & 0xfu] * s;
-    }
-    Pack8<OutT>::store(out + 32 * u + 8 * q, v);
-  }
-}
-
 // Scalar path: one packed byte per lane, any alignment; bytes [first, n_bytes).
 template <typename OutT, bool NESTED>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_bytes(
@@ -238,26 +204,7 @@ int launch(const uint8_t* packed, const void* absmax, const float* code, const f
   const int bs_shift = log2_exact(blocksize);
   const int bs2_shift = log2_exact(blocksize2);
   int64_t done = 0;
-#if CM_NF4_WIDE
-  if (cm::aligned(packed, 16) && cm::aligned(out, 16)) {
-    const int64_t n_units = n_bytes / 16;
-    if (n_units > 0) {
-      const int64_t blocks = (n_units + kThreads - 1) / kThreads;
-      if (blocks > 0x7fffffff) return static_cast<int>(hipErrorInvalidValue);
-      // unit u covers elements [32u, 32u+32): block index = u >> (bs_shift - 5)
-      hipLaunchKernelGGL((nf4_dequant_wide<OutT, NESTED>), dim3(static_cast<uint32_t>(blocks)),
-                         dim3(kThreads), 0, stream, reinterpret_cast<const uint4*>(packed),
-                         absmax, code, code2, absmax2, offset, out, n_units, bs_shift - 5,
-                         bs2_shift, static_cast<uint32_t>(blocksize2));
-      int st = cm::launch_status();
-      if (st) return st;
-    }
-    done = n_units * 16;
-  }
-  const bool vec = false;
-#else
   const bool vec = cm::aligned(packed, 4) && cm::aligned(out, 16);
-#endif
   if (vec) {
     const int64_t n_units = n_bytes / 4;
     if (n_units > 0) {
