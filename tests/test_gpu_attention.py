@@ -125,6 +125,44 @@ def test_packed_attention_matches_fp32(dev, lengths):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv", [(14, 2), (16, 2), (28, 4), (40, 8)],
+                         ids=lambda x: str(x))
+def test_qwen_head_layouts(dev, heads, kv):
+    """The query/key-value head counts of the other Qwen2.5 models (0.5B 14/2, 3B 16/2, 7B 28/4,
+    14B 40/8: groups of 7, 8, 7 and 5 query heads per key-value head), on config 5's rows."""
+    banner(f"packed causal attention heads={heads} kv={kv}")
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward as stock
+    from transformers.modeling_utils import AttentionInterface
+
+    from claudemaxing_amd import attention
+
+    attention.patch_qwen2_grouped_sdpa()
+    ours = AttentionInterface._global_mapping["sdpa"]
+    lengths = [154, 284, 482, 356]
+    n = sum(lengths)
+    q, k, v, do = _inputs(dev, n, 9, heads=heads, groups=kv)
+    mask = _packed_mask(lengths, dev)
+    o_ref, g_ref = _reference(q, k, v, lengths, do, 128 ** -0.5)
+
+    class Mod(_Module):
+        num_key_value_groups = heads // kv
+
+    def run(fn):
+        for t in (q, k, v):
+            t.grad = None
+        out, _ = fn(Mod(), q, k, v, mask, dropout=0.0, scaling=128 ** -0.5)
+        out.backward(do)
+        return out.detach(), [t.grad.detach() for t in (q, k, v)]
+
+    o_st, g_st = run(stock)
+    o, g = run(ours)
+    assert o.shape == (1, n, heads, 128)
+    _check("out", o, o_st, o_ref)
+    for a, b, c, name in zip(g, g_st, g_ref, "qkv"):
+        _check(f"d{name}", a, b, c)
+
+
+@pytest.mark.gpu
 def test_fp32_inputs_under_autocast(dev):
     """The training step's case: fp32 q/k/v (after RoPE) inside fp16 autocast; gradients fp32."""
     banner("packed causal attention, fp32 inputs under fp16 autocast")
