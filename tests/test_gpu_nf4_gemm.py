@@ -144,6 +144,27 @@ def test_backward_matches_exact_product(m, n, k, dev):
     assert_bits_equal(dx32.half(), dx, "fp32 dx = the fp16 dx widened")
 
 
+# the projections of Qwen2.5-0.5B (hidden 896, kv 128, intermediate 4864) and 7B (3584, 512,
+# 18944): weight extents that are multiples of 128 but not of 256, and long contractions
+OTHER_QWEN = [(896, 896), (128, 896), (4864, 896), (896, 4864),
+              (3584, 3584), (512, 3584), (18944, 3584), (3584, 18944)]
+
+
+@pytest.mark.parametrize("m", [37, 300])
+@pytest.mark.parametrize("n,k", OTHER_QWEN)
+def test_other_qwen_shapes(m, n, k, dev):
+    banner(f"nf4_gemm fwd+bwd m={m} n={n} k={k}")
+    packed, state, w16 = make_weight(n, k, 14)
+    pd = to_dev(packed, state, dev)
+    x16 = torch.randn(m, k, generator=torch.Generator().manual_seed(15)).half()
+    (y,) = nf4_linear_fwd(x16.to(dev), [pd], [None])
+    g = torch.randn(m, n, generator=torch.Generator().manual_seed(16)).half()
+    dx = nf4_linear_bwd([g.to(dev)], [pd])
+    torch.cuda.synchronize()
+    check_product(y, x16, w16, f"fwd {m}x{n}x{k}")
+    check_product(dx, None, [w16], f"bwd {m}x{n}x{k}", trans=True, grads=[g])
+
+
 def test_mlp_shapes_two_weights(dev):
     banner("nf4_gemm gate+up fwd, dgate Wg + dup Wu bwd, m=1276")
     m, f, h = 1276, 8960, 1536
