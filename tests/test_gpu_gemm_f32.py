@@ -25,7 +25,9 @@ def _check(out, ref, name):
 
 
 @pytest.mark.parametrize("m,n,k", [(1276, 1536, 8960), (37, 1536, 8960), (300, 200, 1032),
-                                   (8, 8, 8), (2048, 1536, 4096)])
+                                   (8, 8, 8), (2048, 1536, 4096),
+                                   # down projections of Qwen2.5-0.5B and 7B
+                                   (300, 896, 4864), (300, 3584, 18944)])
 def test_one_pair_matches_fp64(m, n, k, dev):
     banner(f"gemm_f32 m={m} n={n} k={k}")
     a, b = _pair(m, n, k, dev, 1)

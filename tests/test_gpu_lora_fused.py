@@ -12,12 +12,12 @@ import torch
 from tests.conftest import banner
 
 
-def _layer(dev, out_f, seed):
+def _layer(dev, out_f, seed, in_f=1536):
     from claudemaxing_amd.lora import LoRALinear
     from claudemaxing_amd.nf4_linear import NF4Linear
 
     g = torch.Generator().manual_seed(seed)
-    w = torch.randn(out_f, 1536, generator=g) * 0.02
+    w = torch.randn(out_f, in_f, generator=g) * 0.02
     b = torch.randn(out_f, generator=g) * 0.1
     base = NF4Linear.from_weight(w.half().float(), bias=b.half().float()).to(dev)
     lin = LoRALinear(base, r=16, alpha=32, dropout=0.05).to(dev)
@@ -87,6 +87,22 @@ def test_fused_adapter_matches(dev, rows, out_f):
     same = float((fused[0] == unfused[0]).float().mean())
     print(f"  identical outputs: {100 * same:.1f}%")
     assert same > 0.9
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("in_f,out_f", [(896, 896), (896, 128), (2048, 2048), (2048, 256)])
+def test_fused_adapter_other_qwen_widths(dev, in_f, out_f):
+    """The q and v adapters of Qwen2.5-0.5B (896 -> 896, 128) and 3B (2048 -> 2048, 256)."""
+    banner(f"fused LoRA adapter in={in_f} out={out_f}")
+    lin = _layer(dev, out_f, seed=in_f + out_f, in_f=in_f)
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn(1, 300, in_f, generator=g, device=dev)
+    gout = torch.randn(1, 300, out_f, generator=g, device=dev)
+    fused = _run(lin, x, gout, True, seed=6)
+    unfused = _run(lin, x, gout, False, seed=6)
+    ref = _reference(lin, x, gout, seed=6)
+    for name, a, b, c in zip(("out", "dx", "dA", "dB"), fused, unfused, ref):
+        _check(name, a, b, c)
 
 
 @pytest.mark.gpu

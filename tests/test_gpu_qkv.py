@@ -75,15 +75,17 @@ def reference(block, x, grads, seed):
     return [o.detach() for o in outs] + [xx.grad] + [p.grad for p in params]
 
 
-@pytest.mark.parametrize("tokens", [1276, 37])
-def test_fused_qkv_matches_separate_layers(tokens, dev):
-    banner(f"NF4QKV tokens={tokens}")
-    block = make_block(dev)
-    x = torch.randn(1, tokens, 1536, device=dev)
+@pytest.mark.parametrize("tokens,h,nq,nkv", [(1276, 1536, 1536, 256), (37, 1536, 1536, 256),
+                                             (300, 896, 896, 128), (300, 2048, 2048, 256)],
+                         ids=["1.5B-1276", "1.5B-37", "0.5B-300", "3B-300"])
+def test_fused_qkv_matches_separate_layers(tokens, h, nq, nkv, dev):
+    banner(f"NF4QKV tokens={tokens} hidden={h} q={nq} kv={nkv}")
+    block = make_block(dev, h=h, nq=nq, nkv=nkv)
+    x = torch.randn(1, tokens, h, device=dev)
     assert _fused_layout(block, x.requires_grad_(True)) is False  # outside fp16 autocast
     with torch.autocast("cuda", dtype=torch.float16):
         assert _fused_layout(block, x)
-    grads = [torch.randn(1, tokens, n, device=dev) for n in (1536, 256, 256)]
+    grads = [torch.randn(1, tokens, n, device=dev) for n in (nq, nkv, nkv)]
     fused = run(block, x, grads, True, 7)
     sep = run(block, x, grads, False, 7)
     ref = reference(block, x, grads, 7)
