@@ -42,15 +42,29 @@ def _loss_and_grads(model, batch, fused, autocast=True):
     return float(out.loss.detach()), grads
 
 
+# Two-layer models of the Qwen2.5 shapes: 1.5B (the benchmark's), 0.5B, 3B, and 7B, whose head
+# weight is not tied to the embedding.
+SHAPES = {
+    "1.5B": TWO_LAYERS,
+    "0.5B": dict(TWO_LAYERS, hidden_size=896, intermediate_size=4864, num_attention_heads=14,
+                 num_key_value_heads=2),
+    "3B": dict(TWO_LAYERS, hidden_size=2048, intermediate_size=11008, num_attention_heads=16,
+               num_key_value_heads=2),
+    "7B": dict(TWO_LAYERS, hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
+               num_key_value_heads=4, tie_word_embeddings=False),
+}
+
+
 @pytest.mark.gpu
-def test_fused_step_matches_stock(dev):
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_fused_step_matches_stock(dev, shape):
     """Both fp16 paths against the fp32 evaluation of the same model (stock code, no autocast,
     NF4 weights expanded to fp32): the fused path must be about as close as the stock fp16 path
     (within 2x its error, or within tol)."""
-    banner("qlora step: fused vs stock transformers vs fp32, 2 layers")
+    banner(f"qlora step: fused vs stock transformers vs fp32, 2 layers, Qwen2.5-{shape} shape")
     from claudemaxing_amd.nf4_linear import NF4Linear
 
-    model = qlora_step.build_model(dev, seed=0, dropout=0.0, **TWO_LAYERS)
+    model = qlora_step.build_model(dev, seed=0, dropout=0.0, **SHAPES[shape])
     g = torch.Generator(device=dev).manual_seed(1)
     for n, p in model.named_parameters():
         if "lora_B" in n:  # nonzero, so the LoRA branch changes the forward
@@ -64,7 +78,8 @@ def test_fused_step_matches_stock(dev):
             m.compute_dtype = torch.float32
         # the fused step stored the tied weight in fp16 (lossless); fp32 products need fp32
         emb = model.get_input_embeddings()
-        assert emb.weight.dtype == torch.float16
+        tied = model.config.tie_word_embeddings
+        assert emb.weight.dtype == (torch.float16 if tied else torch.float32)
         w16 = emb.weight.data
         emb.weight.data = w16.float()
         try:
