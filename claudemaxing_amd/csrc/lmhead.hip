@@ -30,6 +30,7 @@
 // A tile is one contiguous span. Both GEMMs read the weight [V][H] as stored: K1 as a row-major
 // operand, K3 as a k-major one (vocabulary = K), whose LDS tiles are transposed into MFMA
 // fragments by ds_read_b64_tr_b16.
+#include <algorithm>
 #include <mutex>
 #include <numeric>
 
@@ -58,28 +59,32 @@ constexpr int kRowsPerBlock = 4;  // K2: token rows (one wavefront each) per wor
 
 // Tile configurations: BM, BN, wavefront grid WM x WN, stage depth BK, LDS ring stages, and the
 // minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront:
-// 2 gives 256, 1 gives 512). Variant 0 is the default; variant 1 of each is the alternative
-// measured beside it (a deeper ring of 32-column stages; for K3 four wavefronts of 128 x 96).
+// 2 gives 256, 1 gives 512). K1's variant 0 is the default; variant 1 is the alternative
+// measured beside it (a deeper ring of 32-column stages).
 #ifndef CM_LMH_K1
 #define CM_LMH_K1 0
-#endif
-#ifndef CM_LMH_K3
-#define CM_LMH_K3 0
 #endif
 #if CM_LMH_K1 == 1
 constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 32, kST1 = 4, kOcc1 = 2;
 #else
 constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 64, kST1 = 2, kOcc1 = 2;
 #endif
-#if CM_LMH_K3 == 1
-constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 2, kWN3 = 2, kBK3 = 32, kST3 = 4, kOcc3 = 1;
-#elif CM_LMH_K3 == 2
-constexpr int kBM3 = 256, kBN3 = 256, kWM3 = 2, kWN3 = 4, kBK3 = 64, kST3 = 2, kOcc3 = 2;
-#else
-constexpr int kBM3 = 256, kBN3 = 192, kWM3 = 4, kWN3 = 2, kBK3 = 64, kST3 = 2, kOcc3 = 2;
-#endif
 constexpr int kThreads1 = kWM1 * kWN1 * cm::kWave;
-constexpr int kThreads3 = kWM3 * kWN3 * cm::kWave;
+// K3's tile configurations, one per kind of hidden size (the tile's columns): 256 tokens x 192
+// hidden units on 4 x 2 wavefronts of 64 x 96 where the hidden size is a multiple of 192
+// (Qwen2.5-1.5B's 1536: 8 tiles per 256 tokens, no partial tile), else 256 x 256 on 2 x 4 of
+// 128 x 64 where it is a multiple of 256 (2048, 3584, 5120, 8192), else the first.
+template <int BM, int BN, int WM, int WN, int BK, int ST, int OCC>
+struct K3Cfg {
+  static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kBK = BK, kST = ST, kOcc = OCC;
+  static constexpr int kThreads = WM * WN * cm::kWave;
+  static constexpr int kLds = ST * (BM + BN) * (BK / 8);  // uint4 of the LDS ring
+};
+using K3Tall = K3Cfg<256, 192, 4, 2, 64, 2, 2>;
+using K3Square = K3Cfg<256, 256, 2, 4, 64, 2, 2>;
+__host__ __device__ constexpr bool k3_square(int hidden) {
+  return hidden % 192 != 0 && hidden % 256 == 0;
+}
 constexpr int kGroup = kBM1 / kWM1;  // vocabulary columns per partial-statistics group
 constexpr int kEpiRows = kGroup / 2;  // group rows one lane of K1's epilogue holds per token
 static_assert(kGroup % kPanel == 0, "a statistics group is whole panels");
@@ -371,7 +376,6 @@ struct K3Job {
 };
 
 constexpr int kLds1 = kST1 * (kBM1 + kBN1) * (kBK1 / 8);  // uint4 of K1's LDS ring
-constexpr int kLds3 = kST3 * (kBM3 + kBN3) * (kBK3 / 8);
 
 __device__ __forceinline__ void k1_block(const K1Job& j, int bid, uint4* lds) {
   int tm, tn;
@@ -380,20 +384,20 @@ __device__ __forceinline__ void k1_block(const K1Job& j, int bid, uint4* lds) {
   cm::gemm::gemm_lds<kBM1, kBN1, kWM1, kWN1, kBK1, kST1>(j.A, j.B, 0, j.A.k_len, tm, tn, epi, lds);
 }
 
-template <int EDGE>
+template <class CFG, int EDGE>
 __device__ __forceinline__ void k3_block(const K3Job& j, int bid, uint4* lds) {
   int tm, tn, s;
-  cm::gemm::tile_of_sliced(bid, j.count, j.tiles, (j.B.rows + kBN3 - 1) / kBN3, j.remap, tm, tn,
-                           s);
+  cm::gemm::tile_of_sliced(bid, j.count, j.tiles, (j.B.rows + CFG::kBN - 1) / CFG::kBN, j.remap,
+                           tm, tn, s);
   const int k_begin = s * j.k_slice;
   // An empty slice still runs the epilogue (with zero accumulators) so that its buffer is
   // initialised on the first chunk and rescaled on later ones.
   const int k_end = max(k_begin, min(j.A.k_len, k_begin + j.k_slice));
   EpiGrad epi{j.out.g[s], j.n_tok, j.hidden, j.factor, j.first, {}};  // f: start()
-  ScaleP<kBM3 / kWM3 / 32> xp{j.scale, j.n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
-  cm::gemm::gemm_lds<kBM3, kBN3, kWM3, kWN3, kBK3, kST3, Tiled32, KMajor, EpiGrad,
-                     ScaleP<kBM3 / kWM3 / 32>, EDGE>(j.A, j.B, k_begin, k_end, tm, tn, epi, lds,
-                                                     xp);
+  using FX = ScaleP<CFG::kBM / CFG::kWM / 32>;
+  FX xp{j.scale, j.n_tok, 0, {}, {}};  // nxt / cur are filled by prefetch
+  cm::gemm::gemm_lds<CFG::kBM, CFG::kBN, CFG::kWM, CFG::kWN, CFG::kBK, CFG::kST, Tiled32, KMajor,
+                     EpiGrad, FX, EDGE>(j.A, j.B, k_begin, k_end, tm, tn, epi, lds, xp);
 }
 
 // __launch_bounds__'s second argument is the minimum number of wavefronts per SIMD, which caps
@@ -403,13 +407,13 @@ __global__ __launch_bounds__(kThreads1, kOcc1) void lmh_gemm1(K1Job j) {
   k1_block(j, static_cast<int>(blockIdx.x), lds);
 }
 
-// EDGE: cm::gemm::kEdgeNever when every output tile lies inside G (n_tok a multiple of kBM3,
-// hidden of kBN3; the contraction runs over whole 64-column panels), else kEdgeAlways. One loop
-// copy per kernel: two in one did not fit the registers.
-template <int EDGE>
-__global__ __launch_bounds__(kThreads3, kOcc3) void lmh_gemm3(K3Job j) {
-  __shared__ uint4 lds[kLds3];
-  k3_block<EDGE>(j, static_cast<int>(blockIdx.x), lds);
+// EDGE: cm::gemm::kEdgeNever when every output tile lies inside G (n_tok a multiple of the
+// tile's rows, hidden of its columns; the contraction runs over whole 64-column panels), else
+// kEdgeAlways. One loop copy per kernel: two in one did not fit the registers.
+template <class CFG, int EDGE>
+__global__ __launch_bounds__(CFG::kThreads, CFG::kOcc) void lmh_gemm3(K3Job j) {
+  __shared__ uint4 lds[CFG::kLds];
+  k3_block<CFG, EDGE>(j, static_cast<int>(blockIdx.x), lds);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -689,12 +693,28 @@ int64_t default_chunk(int64_t n_rows, int64_t vocab) {
 }
 
 // K-slices of the gradient GEMM: as many as keep the grid within one workgroup per CU (256).
+// Output tiles of the gradient GEMM (K3) for this hidden size's tile configuration.
+int64_t k3_tiles(int64_t n_rows, int hidden) {
+  const int bm = k3_square(hidden) ? K3Square::kBM : K3Tall::kBM;
+  const int bn = k3_square(hidden) ? K3Square::kBN : K3Tall::kBN;
+  return ((n_rows + bm - 1) / bm) * ((hidden + bn - 1) / bn);
+}
+
+// K-slices of the gradient GEMM: the grid of tiles x slices should fill whole waves of the 256
+// CUs (one workgroup each), but every slice is one more fp32 accumulator to read and rewrite
+// per chunk. Take the fewest slices whose wave fill is within 7% of the best one up to
+// kMaxSplit (N = 2048: 64 tiles x 4 at hidden 1536, 112 x 2 at 3584, 160 x 3 at 5120).
 int n_split_for(int64_t n_rows, int hidden) {
-  const int64_t tiles = ((n_rows + kBM3 - 1) / kBM3) * ((hidden + kBN3 - 1) / kBN3);
-  int64_t s = kCUs / (tiles > 0 ? tiles : 1);
-  if (s < 1) s = 1;
-  if (s > kMaxSplit) s = kMaxSplit;
-  return static_cast<int>(s);
+  const int64_t tiles = k3_tiles(n_rows, hidden);
+  auto fill = [&](int64_t sp) {
+    const int64_t wg = tiles * sp;
+    return static_cast<double>(wg) / static_cast<double>((wg + kCUs - 1) / kCUs * kCUs);
+  };
+  double best = 0.0;
+  for (int sp = 1; sp <= kMaxSplit; ++sp) best = fill(sp) > best ? fill(sp) : best;
+  for (int sp = 1; sp <= kMaxSplit; ++sp)
+    if (fill(sp) >= best - 0.07) return sp;
+  return 1;
 }
 
 struct Layout {
@@ -703,14 +723,15 @@ struct Layout {
   int64_t off_e16, off_part, off_rows, off_labz, off_scale, off_g, total;
 };
 
-Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad) {
+Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool want_grad,
+              int max_split = kMaxSplit) {
   Layout L;
   L.chunk = chunk > 0 ? round_up(chunk, kChunkAlign) : default_chunk(n_rows, vocab);
   if (L.chunk > round_up(vocab, kChunkAlign)) L.chunk = round_up(vocab, kChunkAlign);
   if (L.chunk > kMaxChunk) L.chunk = kMaxChunk;
   L.n_groups = L.chunk / kGroup;
   L.n_chunks = (vocab + L.chunk - 1) / L.chunk;
-  L.n_split = want_grad ? n_split_for(n_rows, hidden) : 1;
+  L.n_split = want_grad ? std::min(n_split_for(n_rows, hidden), max_split) : 1;
   int64_t off = 0;
   L.off_e16 = off;
   off += round_up(round_up(n_rows, 32) * L.chunk * 2, 256);
@@ -810,7 +831,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
   // K3 of chunk c: G_s = G_s * factor + P W_c over K-slices; B = W_c read as stored (k-major)
   auto k3_job = [&](int64_t c) {
     const int n_voc = n_voc_of(c);
-    const int tiles = ((n_tok + kBM3 - 1) / kBM3) * ((hidden_size + kBN3 - 1) / kBN3);
+    const int tiles = static_cast<int>(k3_tiles(n_tok, hidden_size));
     const int panels = (n_voc + kPanel - 1) / kPanel;
     // slices are whole statistics groups, so a stage never straddles two group scales
     const int groups = (panels * kPanel + kGroup - 1) / kGroup;
@@ -841,11 +862,20 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     if (st) return st;
     if (!want_grad) continue;
     const K3Job j3 = k3_job(c);
-    if (n_tok % kBM3 == 0 && hidden_size % kBN3 == 0 && j3.A.k_len % kBK3 == 0) {
-      hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeNever>, dim3(j3.count), dim3(kThreads3), 0, s, j3);
+    auto launch3 = [&](auto cfg) {
+      using CFG = decltype(cfg);
+      if (n_tok % CFG::kBM == 0 && hidden_size % CFG::kBN == 0 && j3.A.k_len % CFG::kBK == 0) {
+        hipLaunchKernelGGL((lmh_gemm3<CFG, cm::gemm::kEdgeNever>), dim3(j3.count),
+                           dim3(CFG::kThreads), 0, s, j3);
+      } else {
+        hipLaunchKernelGGL((lmh_gemm3<CFG, cm::gemm::kEdgeAlways>), dim3(j3.count),
+                           dim3(CFG::kThreads), 0, s, j3);
+      }
+    };
+    if (k3_square(hidden_size)) {
+      launch3(K3Square{});
     } else {
-      hipLaunchKernelGGL(lmh_gemm3<cm::gemm::kEdgeAlways>, dim3(j3.count), dim3(kThreads3), 0, s,
-                         j3);
+      launch3(K3Tall{});
     }
     st = cm::launch_status();
     if (st) return st;
@@ -912,9 +942,9 @@ int scratch_of_current_device(char** out) {
 // The chunk the scratch can hold: chunk_cols itself when given (0 when it does not fit), else
 // the largest multiple of 256 columns (at most the whole vocabulary) whose layout fits.
 int64_t scratch_chunk(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_cols,
-                      bool want_grad) {
+                      bool want_grad, int max_split) {
   auto fits = [&](int64_t c) {
-    return layout(n_rows, vocab, hidden, c, want_grad).total <= kScratchBytes;
+    return layout(n_rows, vocab, hidden, c, want_grad, max_split).total <= kScratchBytes;
   };
   if (chunk_cols > 0) return fits(chunk_cols) ? chunk_cols : 0;
   int64_t lo = 0, hi = round_up(vocab, kChunkAlign) / kChunkAlign;  // in units of 256 columns
@@ -939,9 +969,16 @@ extern "C" int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void
   CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                        chunk_cols, loss, entropy, correct));
   const bool want_grad = grad != nullptr;
-  const int64_t chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad);
+  // the workspace entry's K-slices where they fit the scratch, else fewer (each is an fp32
+  // [n_rows, hidden] accumulator)
+  int max_split = kMaxSplit;
+  int64_t chunk = 0;
+  for (; max_split >= 1; --max_split) {
+    chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad, max_split);
+    if (chunk != 0) break;
+  }
   if (chunk == 0) return CM_ERROR_SCRATCH_TOO_SMALL;
-  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad);
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad, max_split);
   if (L.total > kScratchBytes) return CM_ERROR_SCRATCH_TOO_SMALL;
   char* ws = nullptr;
   const int st = scratch_of_current_device(&ws);
