@@ -503,7 +503,8 @@ template <int SLOTS>
 __global__ __launch_bounds__(kRowsPerBlock * cm::kWave) void lmh_rows_kernel(
     const Partial* __restrict__ part, int n_groups, RowState rs,
     const int64_t* __restrict__ target, int n_tok, int64_t c0, int n_voc, int first,
-    float* __restrict__ scale, _Float16* __restrict__ e16, const _Float16* __restrict__ label_z) {
+    float* __restrict__ scale, _Float16* __restrict__ e16, const _Float16* __restrict__ label_z,
+    int row_blocks) {
   const int lane = threadIdx.x % cm::kWave;
   const int row = blockIdx.x * kRowsPerBlock + static_cast<int>(threadIdx.x / cm::kWave);
   if (row >= n_tok) return;  // the whole wavefront
@@ -582,7 +583,7 @@ __global__ __launch_bounds__(kRowsPerBlock * cm::kWave) void lmh_rows_kernel(
           labelled ? cm::exp_f(p[i].max - lse_now) * kPScale : 0.0f;
   }
   if (lane == 0 && g_label >= 0)
-    e16[Tiled32::index(row, t - c0, (n_tok + 31) / 32)] = static_cast<_Float16>(0.0f);
+    e16[Tiled32::index(row, t - c0, row_blocks)] = static_cast<_Float16>(0.0f);
 }
 
 // K4: final per-row outputs; G = scale * (sum_s G_s / 1024 + (p_t - 1) W[t]) for labelled rows,
@@ -672,27 +673,48 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 constexpr int64_t kChunkAlign = kBM1 > 256 ? kBM1 : 256;
 constexpr int64_t kCUs = 256;  // MI355X compute units (8 XCDs x 32)
 
+// E's token rows: padded to the gradient GEMM's 256-row tiles, so that its loads of a partial
+// tile stay inside E and need no bounds selection (the padding rows feed only output rows that
+// are never stored).
+constexpr int64_t kERowAlign = 256;
+static_assert(K3Tall::kBM == kERowAlign && K3Square::kBM == kERowAlign,
+              "a K3 tile's rows are one padded block of E rows");
+int64_t e_rows(int64_t n_rows) { return round_up(n_rows > 0 ? n_rows : 1, kERowAlign); }
+int e_row_blocks(int64_t n_rows) { return static_cast<int>(e_rows(n_rows) / 32); }
+
 int64_t default_chunk(int64_t n_rows, int64_t vocab) {
-  // E chunk of at most 128 MiB (fp16, n_rows x C). Per extra chunk the gradient GEMM's split-K
-  // slices are read and rewritten once more (4 x 12.6 MB at N = 2048) and each kernel ramps up
-  // once more. K1 runs one 256 x 256 workgroup per CU, so a chunk whose vocabulary tiles times
-  // token tiles is a multiple of 256 fills whole waves of the chip; the largest such chunk within
-  // the budget is taken (the last chunk takes the remainder), else the vocabulary is split into
-  // equal chunks. Measured at N = 2048, V = 151936 (one MI355X, one process, interleaved):
-  // 4 x 32768 + 20864 columns 2092 us, 5 x 30464 2105 us, 24576 2115 us, 16384 2171 us.
-  const int64_t budget = (int64_t{128} << 20) / 2 / (n_rows > 0 ? n_rows : 1);  // columns
+  // E chunk of at most 128 MiB (fp16, padded rows x C). Per extra chunk the gradient GEMM's
+  // split-K slices are read and rewritten once more (4 x 12.6 MB at N = 2048) and each kernel
+  // ramps up once more. K1 runs one 256 x 256 workgroup per CU, so the chunk is chosen by the
+  // waves of workgroups the whole vocabulary takes: the number of 256-column vocabulary tiles
+  // per chunk (from the budget down to half of it) that needs the fewest waves over all chunks,
+  // then the fewest chunks. At N = 2048 (8 token tiles) that is 4 chunks of 128 tiles (32768
+  // columns, 1024 workgroups each) and the rest, 19 waves; at 1792 (7 token tiles) 4 chunks of
+  // 146 tiles (1022 workgroups) and the rest, 17 waves where equal chunks of 119 took 20.
+  // Measured at N = 2048, V = 151936 (one MI355X, one process, interleaved): 4 x 32768 + 20864
+  // columns 2092 us, 5 x 30464 2105 us, 24576 2115 us, 16384 2171 us.
+  const int64_t budget = (int64_t{128} << 20) / 2 / e_rows(n_rows);  // columns
   int64_t c = budget / kChunkAlign * kChunkAlign;
   if (c < 4096) c = 4096;
   if (c > kMaxChunk) c = kMaxChunk;
   if (c >= vocab) return round_up(vocab, kChunkAlign);
   const int64_t token_tiles = (n_rows + kBN1 - 1) / kBN1;
-  const int64_t wave_cols = kBM1 * (kCUs / std::gcd(token_tiles, kCUs));
-  if (wave_cols <= c) return c / wave_cols * wave_cols;
-  const int64_t n_chunks = (vocab + c - 1) / c;
-  return round_up((vocab + n_chunks - 1) / n_chunks, kChunkAlign);
+  const int64_t vocab_tiles = (vocab + kBM1 - 1) / kBM1;
+  auto waves = [&](int64_t tiles) { return (tiles * token_tiles + kCUs - 1) / kCUs; };
+  int64_t best_vt = c / kBM1, best_waves = -1, best_chunks = 0;
+  for (int64_t vt = c / kBM1; vt >= 1 && vt * 2 >= c / kBM1; --vt) {
+    const int64_t full = vocab_tiles / vt, rest = vocab_tiles % vt;
+    const int64_t w = full * waves(vt) + (rest ? waves(rest) : 0);
+    const int64_t n = full + (rest ? 1 : 0);
+    if (best_waves < 0 || w < best_waves || (w == best_waves && n < best_chunks)) {
+      best_vt = vt;
+      best_waves = w;
+      best_chunks = n;
+    }
+  }
+  return best_vt * kBM1;
 }
 
-// K-slices of the gradient GEMM: as many as keep the grid within one workgroup per CU (256).
 // Output tiles of the gradient GEMM (K3) for this hidden size's tile configuration.
 int64_t k3_tiles(int64_t n_rows, int hidden) {
   const int bm = k3_square(hidden) ? K3Square::kBM : K3Tall::kBM;
@@ -734,7 +756,7 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   L.n_split = want_grad ? std::min(n_split_for(n_rows, hidden), max_split) : 1;
   int64_t off = 0;
   L.off_e16 = off;
-  off += round_up(round_up(n_rows, 32) * L.chunk * 2, 256);
+  off += round_up(e_rows(n_rows) * L.chunk * 2, 256);
   L.off_part = off;
   off += round_up(n_rows * L.n_groups * static_cast<int64_t>(sizeof(Partial)), 256);
   L.off_rows = off;
@@ -807,7 +829,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
             tiles,
             tiles % 8 == 0 ? 1 : 0,
             EpiProbs{e16_of(c), n_tok, n_voc, c0_of(c), part, static_cast<int>(L.n_groups), target,
-                     label_z, want_grad ? 1 : 0, (n_tok + 31) / 32, {}}};  // tgt: prepare()
+                     label_z, want_grad ? 1 : 0, e_row_blocks(n_tok), {}}};  // tgt: prepare()
     return j;
   };
   // K2 of chunk c: running statistics and the group scales
@@ -816,15 +838,16 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     const int ng = static_cast<int>(L.n_groups), fi = c == 0 ? 1 : 0, nv = n_voc_of(c);
     const int64_t c0 = c0_of(c);
     _Float16* e = e16_of(c);
+    const int rb = e_row_blocks(n_tok);
     if (L.n_groups <= cm::kWave) {
       hipLaunchKernelGGL(lmh_rows_kernel<1>, grid, block, 0, s, part, ng, rs, target, n_tok, c0,
-                         nv, fi, scale, e, label_z);
+                         nv, fi, scale, e, label_z, rb);
     } else if (L.n_groups <= 4 * cm::kWave) {
       hipLaunchKernelGGL(lmh_rows_kernel<4>, grid, block, 0, s, part, ng, rs, target, n_tok, c0,
-                         nv, fi, scale, e, label_z);
+                         nv, fi, scale, e, label_z, rb);
     } else {
       hipLaunchKernelGGL(lmh_rows_kernel<kMaxRowSlots>, grid, block, 0, s, part, ng, rs, target,
-                         n_tok, c0, nv, fi, scale, e, label_z);
+                         n_tok, c0, nv, fi, scale, e, label_z, rb);
     }
     return cm::launch_status();
   };
@@ -837,7 +860,7 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     const int groups = (panels * kPanel + kGroup - 1) / kGroup;
     const int k_slice = ((groups + L.n_split - 1) / L.n_split) * kGroup;
     const int count = tiles * L.n_split;
-    K3Job j{Tiled32{e16_of(c), n_tok, n_voc, (n_tok + 31) / 32},
+    K3Job j{Tiled32{e16_of(c), n_tok, n_voc, e_row_blocks(n_tok)},
             KMajor{W16 + c0_of(c) * ld_w, ld_w, hidden_size, n_voc},
             tiles,
             count,
@@ -864,7 +887,9 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
     const K3Job j3 = k3_job(c);
     auto launch3 = [&](auto cfg) {
       using CFG = decltype(cfg);
-      if (n_tok % CFG::kBM == 0 && hidden_size % CFG::kBN == 0 && j3.A.k_len % CFG::kBK == 0) {
+      // E's rows are padded to whole tiles (kERowAlign), so only the hidden size and the
+      // chunk's columns decide whether every load lies inside its operand
+      if (hidden_size % CFG::kBN == 0 && j3.A.k_len % CFG::kBK == 0) {
         hipLaunchKernelGGL((lmh_gemm3<CFG, cm::gemm::kEdgeNever>), dim3(j3.count),
                            dim3(CFG::kThreads), 0, s, j3);
       } else {

@@ -208,11 +208,12 @@ def test_nf4_linear_argument_checks(lib):
 
 
 def test_lmhead_default_chunk(lib):
-    """The LM head's default vocabulary chunk keeps E (fp16, tokens x chunk) within 128 MiB and,
-    where the chip's 256 CUs allow it, fills whole waves of K1's 256 x 256 workgroups: at 2048
-    tokens (8 token tiles) a multiple of 32 vocabulary tiles, i.e. 4 chunks of 32768 columns and
-    the remainder; at 1193 tokens (5 token tiles, no whole-wave chunk within the budget) equal
-    chunks. The workspace grows with the chunk, so the default is the chunk whose workspace
+    """The LM head's default vocabulary chunk keeps E (fp16, tokens padded to 256 x chunk) within
+    128 MiB and needs the fewest waves of K1's 256 x 256 workgroups over the whole vocabulary
+    (594 vocabulary tiles), then the fewest chunks: at 2048 tokens (8 token tiles) 4 chunks of
+    32768 columns and the remainder, 19 waves; at 1792 (7 token tiles) 4 of 146 tiles (1022
+    workgroups) and the remainder, 17 waves; at 1193 (5 token tiles) 204-tile chunks, 12 waves
+    in 3 chunks. The workspace grows with the chunk, so the default is the chunk whose workspace
     matches chunk_cols = 0."""
     ws = lib.cm_lmhead_ce_workspace_bytes
     V, H = 151936, 1536
@@ -225,7 +226,8 @@ def test_lmhead_default_chunk(lib):
 
     assert default_chunk(2048) == 32768
     assert default_chunk(4096) == 16384
-    assert default_chunk(1193) == 50688  # 3 equal chunks, 256-aligned
+    assert default_chunk(1792) == 146 * 256
+    assert default_chunk(1193) == 204 * 256
     assert default_chunk(16) == V // 256 * 256 + 256  # the whole vocabulary in one chunk
-    for n in (64, 1193, 2048, 4096, 16384):
-        assert (n + 31) // 32 * 32 * default_chunk(n) * 2 <= 128 << 20, n
+    for n in (64, 1193, 1792, 2048, 4096, 16384):
+        assert (n + 255) // 256 * 256 * default_chunk(n) * 2 <= 128 << 20, n
