@@ -54,7 +54,8 @@ constexpr int kPanel = 64;          // columns per panel of the blocked layouts
 constexpr float kNoLogit = -3.0e38f;
 constexpr float kPScale = 1024.0f;  // P16 = fp16(p * kPScale)
 constexpr int kStatThreads = 256;
-constexpr int kMaxSplit = 8;
+constexpr int kMaxSplit = 32;      // K-slices of the gradient GEMM (small batches take many)
+constexpr int kFinalUnrolled = 8;  // K4 slice counts with their own instantiation
 constexpr int kRowsPerBlock = 4;  // K2: token rows (one wavefront each) per workgroup
 
 // Tile configurations: BM, BN, wavefront grid WM x WN, stage depth BK, LDS ring stages, and the
@@ -595,7 +596,7 @@ template <int NS>
 __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
     RowState rs, const int64_t* __restrict__ target, int64_t vocab, float* __restrict__ loss,
     float* __restrict__ entropy, int32_t* __restrict__ correct, GradSlices gs,
-    const _Float16* __restrict__ weight, int64_t ld_w, int hidden, float grad_scale) {
+    const _Float16* __restrict__ weight, int64_t ld_w, int hidden, float grad_scale, int ns) {
   const int row = blockIdx.x;
   const int64_t t = target[row];
   const bool labelled = t != -100;
@@ -620,22 +621,46 @@ __global__ __launch_bounds__(kStatThreads) void lmh_final_kernel(
   // label's whole coefficient p_t - 1 = -off / sum is applied here in fp32, with the relative
   // precision of the off-label mass however confident the label is.
   const float coef = labelled && in_range ? -rs.off[row] / rs.sum[row] : 0.0f;
+  // NS > 0: NS slices, every load issued before the first add; NS == 0: ns slices (more than
+  // kFinalUnrolled), loaded kFinalUnrolled at a time. Either way the slices are added in order.
+  constexpr int kV = NS > 0 ? NS : kFinalUnrolled;
   for (int h0 = threadIdx.x; h0 < hidden; h0 += kStatThreads * kFinalPer) {
-    float v[NS][kFinalPer], wv[kFinalPer];
+    float v[kV][kFinalPer], wv[kFinalPer], accs[kFinalPer];
 #pragma unroll
     for (int j = 0; j < kFinalPer; ++j) {
       const int h = h0 + j * kStatThreads;
       const int hc = h < hidden ? h : 0;
       wv[j] = static_cast<float>(w[hc]);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) v[s][j] = gs.g[s][off + hc];
+      for (int s = 0; s < kV; ++s) v[s][j] = gs.g[s][off + hc];
+    }
+#pragma unroll
+    for (int j = 0; j < kFinalPer; ++j) {
+      accs[j] = v[0][j];
+#pragma unroll
+      for (int s = 1; s < kV; ++s) accs[j] += v[s][j];
+    }
+    if constexpr (NS == 0) {
+      for (int s0 = kFinalUnrolled; s0 < ns; s0 += kFinalUnrolled) {
+#pragma unroll
+        for (int j = 0; j < kFinalPer; ++j) {
+          const int h = h0 + j * kStatThreads;
+          const int hc = h < hidden ? h : 0;
+#pragma unroll
+          for (int s = 0; s < kFinalUnrolled; ++s)
+            v[s][j] = s0 + s < ns ? gs.g[s0 + s][off + hc] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kFinalPer; ++j)
+#pragma unroll
+          for (int s = 0; s < kFinalUnrolled; ++s)
+            if (s0 + s < ns) accs[j] += v[s][j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < kFinalPer; ++j) {
       const int h = h0 + j * kStatThreads;
-      float acc = v[0][j];
-#pragma unroll
-      for (int s = 1; s < NS; ++s) acc += v[s][j];
+      const float acc = accs[j];
       if (h < hidden)
         gs.g[0][off + h] = labelled && in_range
                                ? grad_scale * (acc * (1.0f / kPScale) + coef * wv[j])
@@ -650,7 +675,11 @@ int launch_final(int n_split, int n_tok, hipStream_t s, const RowState& rs, cons
                  const _Float16* w, int64_t ld_w, int hidden, float grad_scale) {
 #define CM_FINAL(NS)                                                                            \
   hipLaunchKernelGGL(lmh_final_kernel<NS>, dim3(n_tok), dim3(kStatThreads), 0, s, rs, target,    \
-                     vocab, loss, entropy, correct, gs, w, ld_w, hidden, grad_scale)
+                     vocab, loss, entropy, correct, gs, w, ld_w, hidden, grad_scale, n_split)
+  if (n_split > kFinalUnrolled && n_split <= kMaxSplit) {
+    CM_FINAL(0);
+    return cm::launch_status();
+  }
   switch (n_split) {
     case 1: CM_FINAL(1); break;
     case 2: CM_FINAL(2); break;
@@ -725,16 +754,22 @@ int64_t k3_tiles(int64_t n_rows, int hidden) {
 // K-slices of the gradient GEMM: the grid of tiles x slices should fill whole waves of the 256
 // CUs (one workgroup each), but every slice is one more fp32 accumulator to read and rewrite
 // per chunk. Take the fewest slices whose wave fill is within 7% of the best one up to
-// kMaxSplit (N = 2048: 64 tiles x 4 at hidden 1536, 112 x 2 at 3584, 160 x 3 at 5120).
+// kMaxSplit (N = 2048: 64 tiles x 4 at hidden 1536, 112 x 2 at 3584, 160 x 3 at 5120; N = 256:
+// 8 x 30).
 int n_split_for(int64_t n_rows, int hidden) {
   const int64_t tiles = k3_tiles(n_rows, hidden);
   auto fill = [&](int64_t sp) {
     const int64_t wg = tiles * sp;
     return static_cast<double>(wg) / static_cast<double>((wg + kCUs - 1) / kCUs * kCUs);
   };
+  // the extra slices' accumulators within 128 MiB (a small batch can afford many: 1.5 MB each
+  // at 256 tokens x 1536)
+  const int64_t slice_bytes = round_up(n_rows * hidden * 4, 256);
+  int64_t cap = 1 + (int64_t{128} << 20) / (slice_bytes > 0 ? slice_bytes : 1);
+  if (cap > kMaxSplit) cap = kMaxSplit;
   double best = 0.0;
-  for (int sp = 1; sp <= kMaxSplit; ++sp) best = fill(sp) > best ? fill(sp) : best;
-  for (int sp = 1; sp <= kMaxSplit; ++sp)
+  for (int sp = 1; sp <= cap; ++sp) best = fill(sp) > best ? fill(sp) : best;
+  for (int sp = 1; sp <= cap; ++sp)
     if (fill(sp) >= best - 0.07) return sp;
   return 1;
 }
