@@ -514,7 +514,7 @@ def k_nf4_linear(dev, names):
         xd, gd = x.to(dev), g.to(dev)
         ys = [torch.empty(m, f, dtype=torch.float16, device=dev) for _ in range(2)]
         dx = torch.empty(m, h, dtype=torch.float16, device=dev)
-        w_arr, keep = _weights(pairs)
+        w_arr, keep = _weights(pairs)[:2]
         out_arr = (ctypes.c_void_p * 2)(*[y.data_ptr() for y in ys])
         ldo = (ctypes.c_int64 * 2)(f, f)
         g_arr = (ctypes.c_void_p * 2)(gd.data_ptr(), gd.data_ptr())

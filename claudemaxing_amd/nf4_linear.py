@@ -11,6 +11,7 @@ input's dtype, as Linear4bit does).
 """
 
 import ctypes
+import weakref
 
 import torch
 
@@ -44,8 +45,27 @@ def fused_supported(packed, state):
     return state.absmax.dtype == torch.float32
 
 
+def _weight_key(packed, state):
+    """What a weight's descriptor is built from: the addresses and versions of its tensors and
+    its sizes. Equal keys of one QuantState give the same descriptor."""
+    s2 = state.state2 if state.nested else None
+    off = state.offset
+    return (packed.data_ptr(), state.absmax.data_ptr(), state.absmax._version,
+            None if state.code is None else state.code.data_ptr(),
+            None if s2 is None else (s2.code.data_ptr(), s2.absmax.data_ptr(),
+                                     s2.absmax._version, int(s2.blocksize)),
+            (off.data_ptr(), off._version) if torch.is_tensor(off) else off,
+            int(state.blocksize), tuple(state.shape))
+
+
 def _descriptor(packed, state, scale_map=True):
-    """(cm_nf4_weight, tensors it points into that must stay alive for the call)."""
+    """(cm_nf4_weight, tensors it points into that must stay alive for the call). With the
+    scale map, the descriptor is kept on the QuantState for the next call with the same key
+    (the host cost of building one, ~8 us, is paid once per weight version)."""
+    key = _weight_key(packed, state) if scale_map else None
+    cached = getattr(state, "_cm_descriptor", None) if scale_map else None
+    if cached is not None and cached[0] == key:
+        return cached[1], cached[2]
     nested = bool(state.nested)
     s2 = state.state2 if nested else None
     code = _nf4_code(packed.device) if state.code is None else state.code
@@ -56,7 +76,10 @@ def _descriptor(packed, state, scale_map=True):
                        _lib.ptr(s2.absmax if nested else None), _lib.ptr(offset),
                        int(state.blocksize), int(s2.blocksize) if nested else 1,
                        int(state.shape[0]), int(state.shape[1]), _lib.ptr(smap))
-    return d, (code, offset, smap)
+    keep = (code, offset, smap)
+    if scale_map:
+        state._cm_descriptor = (key, d, keep)
+    return d, keep
 
 
 def _scale_map(packed, state):
@@ -82,12 +105,28 @@ def _scale_map(packed, state):
 
 
 def _weights(pairs):
+    """(cm_nf4_weight array of the pairs, tensors it points into, {(m, backward): workspace
+    bytes}, the pairs' QuantStates as weak references). Kept on the first pair's QuantState,
+    keyed by every pair's weight key and checked against the pairs' QuantState objects
+    themselves, so a cached array never outlives or mixes up the weights it describes."""
+    keys = tuple(_weight_key(p, s) for p, s in pairs)
+    cache = getattr(pairs[0][1], "_cm_arrays", None)
+    if cache is None:
+        cache = pairs[0][1]._cm_arrays = {}
+    got = cache.get(keys)
+    if got is not None and all(r() is s for r, (_, s) in zip(got[3], pairs)):
+        return got
     descs, keep = [], []
     for packed, state in pairs:
         d, k = _descriptor(packed, state)
         descs.append(d)
         keep.append(k)
-    return (_lib.NF4Weight * len(descs))(*descs), keep
+    got = ((_lib.NF4Weight * len(descs))(*descs), keep, {},
+           tuple(weakref.ref(s) for _, s in pairs))
+    if len(cache) > 16:  # a few groupings per weight at most; stale versions drop out
+        cache.clear()
+    cache[keys] = got
+    return got
 
 
 # Products below this many FLOPs take the fused kernel; larger ones expand the weight with the
@@ -115,12 +154,19 @@ def _rows16(t, k):
     return t2
 
 
-def _workspace(m, w, n, backward, device):
+def _workspace(m, weights, n, backward, device):
     """The fp32 partial-sum buffer a split contraction needs (None when the call does not split),
-    from torch's caching allocator on the current stream."""
-    nbytes = _lib.load().cm_nf4_linear_workspace_bytes(m, w, n, backward)
-    if nbytes < 0:
-        raise RuntimeError("cm_nf4_linear_workspace_bytes: invalid weights")
+    from torch's caching allocator on the current stream; `weights` is what _weights returned,
+    whose dict keeps the byte count per (m, backward)."""
+    w, sizes = weights[0], weights[2]
+    nbytes = sizes.get((m, backward))
+    if nbytes is None:
+        nbytes = _lib.load().cm_nf4_linear_workspace_bytes(m, w, n, backward)
+        if nbytes < 0:
+            raise RuntimeError("cm_nf4_linear_workspace_bytes: invalid weights")
+        if len(sizes) > 64:
+            sizes.clear()
+        sizes[(m, backward)] = nbytes
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
 
 
@@ -132,7 +178,8 @@ def nf4_linear_fwd(x16, pairs, biases=None, out_dtype=torch.float16):
     x2 = _rows16(x16, k)
     m = x2.shape[0]
     outs = [torch.empty(m, st.shape[0], dtype=out_dtype, device=x2.device) for _, st in pairs]
-    w, keep = _weights(pairs)
+    weights = _weights(pairs)
+    w = weights[0]
     n = len(pairs)
     bias_arr = None
     if biases is not None and any(b is not None for b in biases):
@@ -140,11 +187,10 @@ def nf4_linear_fwd(x16, pairs, biases=None, out_dtype=torch.float16):
         bias_arr = (ctypes.c_void_p * n)(*[_lib.ptr(b) for b in biases])
     out_arr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     ldo = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
-    ws = _workspace(m, w, n, 0, x2.device)
+    ws = _workspace(m, weights, n, 0, x2.device)
     _lib.call("cm_nf4_linear_fwd", x2.data_ptr(), x2.stride(0), m, w, n, bias_arr, out_arr, ldo,
               _lib.dtype_code(out_dtype), _lib.ptr(ws), 0 if ws is None else ws.numel(),
               _lib.stream(x2.device))
-    del keep
     lead = x16.shape[:-1]
     return [o.view(*lead, o.shape[1]) for o in outs]
 
@@ -156,15 +202,15 @@ def nf4_linear_bwd(grads, pairs, dx_dtype=torch.float16):
     g2 = [_rows16(g, st.shape[0]) for g, (_, st) in zip(grads, pairs)]
     m = g2[0].shape[0]
     dx = torch.empty(m, k, dtype=dx_dtype, device=g2[0].device)
-    w, keep = _weights(pairs)
+    weights = _weights(pairs)
+    w = weights[0]
     n = len(pairs)
     g_arr = (ctypes.c_void_p * n)(*[g.data_ptr() for g in g2])
     ldg = (ctypes.c_int64 * n)(*[g.stride(0) for g in g2])
-    ws = _workspace(m, w, n, 1, dx.device)
+    ws = _workspace(m, weights, n, 1, dx.device)
     _lib.call("cm_nf4_linear_bwd", g_arr, ldg, m, w, n, dx.data_ptr(), dx.stride(0),
               _lib.dtype_code(dx_dtype), _lib.ptr(ws), 0 if ws is None else ws.numel(),
               _lib.stream(dx.device))
-    del keep
     return dx.view(*grads[0].shape[:-1], k)
 
 
