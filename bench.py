@@ -25,7 +25,10 @@ no closure can pick up another kernel's sizes.
 One JSON line is printed: the headline metric with its roofline and the CPU oracle timed on the
 host cores (a baseline, not the target), plus every kernel's numbers under "kernels", and the
 board's socket power and graphics clock (amd-smi) sampled while the headline call runs back to
-back after its timed region (the matrix-core kernels run at the board's power limit).
+back after its timed region (the matrix-core kernels run at the board's power limit), and the
+two roofline denominators as the board attains them ("measured_peaks": a 2 GiB HBM stream and
+the fp16 MFMA issue rate on register operands), each kernel's fraction of them beside its
+fraction of the published peaks.
 """
 
 import argparse
@@ -54,6 +57,8 @@ def parse():
     p.add_argument("--only", default="")
     p.add_argument("--step-steps", type=int, default=10, help="timed QLoRA steps (config 5)")
     p.add_argument("--no-step", action="store_true", help="skip the QLoRA step (config 5)")
+    p.add_argument("--no-peaks", action="store_true",
+                   help="skip the on-box HBM and matrix-core peak probes")
     p.add_argument("--no-power", action="store_true",
                    help="skip the board power sample of the headline (profiler runs)")
     return p.parse_args()
@@ -691,6 +696,81 @@ def _smi_sample(smi):
     return watts, (sum(clocks) / len(clocks) if clocks else None)
 
 
+def measured_peaks(dev, power=True):
+    """The two roofline denominators as this board attains them (cm_probe_hbm,
+    cm_probe_mfma_f16): a 16-byte stream over 2 GiB, read only and copied (GB/s of bytes read +
+    written; the best of 1, 4, 16 words per lane with plain or nontemporal loads), and
+    v_mfma_f32_32x32x16_f16 on register operands of N(0,1) fp16 data (TFLOP/s; the best of 2, 4,
+    8 accumulator chains per wavefront); median of 5 launches after 2 warm-ups, HIP events around
+    each launch on the launch stream. With power, the board's power and clock while the MFMA
+    probe runs back to back."""
+    import torch
+
+    from claudemaxing_amd import _lib
+
+    lib = _lib.load()
+    stream = _lib.stream(dev)
+    cur = torch.cuda.current_stream(dev)
+
+    def median_s(fn, n=5, warm=2):
+        for _ in range(warm):
+            fn()
+        times = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(cur)
+            fn()
+            b.record(cur)
+            b.synchronize()
+            times.append(a.elapsed_time(b) * 1e-3)
+        return sorted(times)[n // 2]
+
+    nbytes = 2 << 30
+    src = torch.randint(0, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    read, copy = {}, {}
+    for per_lane in (1, 4, 16):
+        for nt in (0, 1):
+            key = f"{per_lane}{'nt' if nt else ''}"
+            read[key] = nbytes / median_s(
+                lambda q=per_lane, t=nt: _lib.call("cm_probe_hbm", src.data_ptr(), None, nbytes,
+                                                   q, t, sink.data_ptr(), stream)) / 1e9
+            copy[key] = 2 * nbytes / median_s(
+                lambda q=per_lane, t=nt: _lib.call("cm_probe_hbm", src.data_ptr(), dst.data_ptr(),
+                                                   nbytes, q, t, sink.data_ptr(), stream)) / 1e9
+    del src, dst
+    gen = torch.Generator().manual_seed(0)
+    ops = torch.randn(512 * 8, generator=gen).half().to(dev)
+    iters = 2000
+    rates = {}
+    for chains in (2, 4, 8):
+        flops = int(lib.cm_probe_mfma_f16_flops(iters, chains))
+        sec = median_s(lambda c=chains: _lib.call("cm_probe_mfma_f16", ops.data_ptr(), iters, c,
+                                                  sink.data_ptr(), stream))
+        rates[chains] = flops / sec / 1e12
+    best = max(rates, key=rates.get)
+
+    def mfma():
+        _lib.call("cm_probe_mfma_f16", ops.data_ptr(), iters, best, sink.data_ptr(), stream)
+
+    out = dict(hbm_read_GBs=round(max(read.values()), 1),
+               hbm_copy_GBs=round(max(copy.values()), 1),
+               hbm_GBs_by_variant={q: dict(read=round(read[q], 1), copy=round(copy[q], 1))
+                                   for q in read},
+               mfma_f16_TFLOPs=round(rates[best], 1),
+               mfma_f16_TFLOPs_by_chains={c: round(r, 1) for c, r in rates.items()},
+               spec=dict(hbm_GBs=HBM_PEAK_GBS, mfma_f16_TFLOPs=MFMA_FP16_PEAK_TFLOPS),
+               note="cm_probe_hbm over 2 GiB (read only; copied, bytes read + written; 1, 4 or "
+                    "16 16-byte words per lane, plain or nontemporal (nt) loads: the best) and "
+                    "cm_probe_mfma_f16 (2048 x 4 wavefronts x 2000 x 2 x chains MFMAs 32x32x16 "
+                    "on N(0,1) fp16 register operands, chains 2, 4, 8 accumulators per "
+                    "wavefront: the best), median of 5")
+    if power:
+        out["mfma_power"] = board_power(mfma)
+    return out
+
+
 def board_power(fn, seconds=2.0):
     """The board's socket power and graphics clock (amd-smi, about 5 samples a second) while
     `fn` runs back to back for `seconds`, or None without a readable amd-smi. The matrix-core
@@ -886,6 +966,20 @@ def main():
     torch.cuda.empty_cache()
     headline = "lmhead_ce" if "lmhead_ce" in results else next(iter(results))
     hr = results[headline]
+    peaks = None
+    if not args.no_peaks:
+        print("[bench] measured peaks ...", file=sys.stderr, flush=True)
+        peaks = measured_peaks(dev, power=not args.no_power)
+        print(f"[bench] measured peaks: HBM {peaks['hbm_read_GBs']} GB/s read, "
+              f"{peaks['hbm_copy_GBs']} GB/s copy; fp16 MFMA {peaks['mfma_f16_TFLOPs']} TFLOP/s",
+              file=sys.stderr, flush=True)
+        # the matrix-core probe bounds every MFMA kernel; the single-stream HBM probe does not
+        # bound the elementwise kernels that stream several arrays at once (LoRA pack/unpack
+        # and RMSNorm forward at bandwidth scale exceed its copy rate), so HBM fractions stay
+        # against the published 8 TB/s
+        for r in results.values():
+            if r["bound"] == "mfma":
+                r["frac_of_measured"] = round(r["achieved"] / peaks["mfma_f16_TFLOPs"], 4)
     line = {
         "metric": METRIC,
         "value": hr["achieved"],
@@ -904,9 +998,11 @@ def main():
         "roofline": {"bound": hr["bound"], "achieved": hr["achieved"],
                      "peak": HBM_PEAK_GBS if hr["bound"] == "hbm" else MFMA_FP16_PEAK_TFLOPS,
                      "unit": hr["unit"], "frac": hr["frac"],
-                     "traffic": traffic_from_profile(headline)},
+                     "traffic": traffic_from_profile(headline),
+                     "frac_of_measured_peak": hr.get("frac_of_measured")},
         "kernels": results,
         "power": power,
+        "measured_peaks": peaks,
         "ms_per_step_note": "one headline call (the fused LM head at config 4) per step",
         "in_step_kernel_sum_ms": round(sum(r["us"] for r in results.values()
                                            if r["in_step"]) / 1e3, 4),

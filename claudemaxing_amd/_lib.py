@@ -88,6 +88,9 @@ SIGNATURES = {
     "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P, _L, _P]),
     "cm_nf4_linear_bwd": (_I, [_PP, _PL, _L, _PW, _I, _P, _L, _I, _P, _L, _P]),
     "cm_nf4_linear_workspace_bytes": (_L, [_L, _PW, _I, _I]),
+    "cm_probe_hbm": (_I, [_P, _P, _L, _I, _I, _P, _P]),
+    "cm_probe_mfma_f16": (_I, [_P, _I, _I, _P, _P]),
+    "cm_probe_mfma_f16_flops": (_L, [_I, _I]),
     "cm_nf4_scale_map": (_I, [_PW, _P, _P]),
 }
 

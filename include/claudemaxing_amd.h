@@ -410,6 +410,25 @@ int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
  * these sizes (0: the call does not split its contraction), -1 for invalid weights. */
 int64_t cm_nf4_linear_workspace_bytes(int64_t m, const cm_nf4_weight* w, int n_w, int backward);
 
+/* ---- On-box peak probes (measurement only; no counterpart in the reference) ----------------
+ * The roofline denominators as this board attains them, which bench.py reports beside the
+ * published 8 TB/s and 2.5 PFLOP/s. Neither is part of the training step. */
+
+/* Streams `bytes` (a multiple of 16, 16-byte aligned) from src: read only when dst is NULL
+ * (sink: 4 bytes of device memory the kernel may write), else copied to dst (nontemporal
+ * stores). One pass of 256-lane workgroups, each over per_lane (1, 4 or 16) x 4 KiB, with 16-byte
+ * loads, nontemporal when nt_loads is non-zero. */
+int cm_probe_hbm(const void* src, void* dst, int64_t bytes, int per_lane, int nt_loads,
+                 uint32_t* sink, void* stream);
+
+/* fp16 matrix-core rate: 2048 workgroups of 4 wavefronts, each issuing iters x 2 x chains
+ * v_mfma_f32_32x32x16_f16 on `chains` (2, 4 or 8) independent accumulators, operands taken from
+ * `operands` (512 x 8 fp16 = 8 KiB, 16-byte aligned; use non-zero data). sink: 4 bytes of
+ * device memory. */
+int cm_probe_mfma_f16(const void* operands, int iters, int chains, float* sink, void* stream);
+/* Matrix-core FLOPs of one cm_probe_mfma_f16 call (0 for invalid arguments). */
+int64_t cm_probe_mfma_f16_flops(int iters, int chains);
+
 #ifdef __cplusplus
 }
 #endif

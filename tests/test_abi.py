@@ -231,3 +231,11 @@ def test_lmhead_default_chunk(lib):
     assert default_chunk(16) == V // 256 * 256 + 256  # the whole vocabulary in one chunk
     for n in (64, 1193, 1792, 2048, 4096, 16384):
         assert (n + 255) // 256 * 256 * default_chunk(n) * 2 <= 128 << 20, n
+
+
+def test_peak_probes_refuse_bad_arguments(lib):
+    # checked before any launch: no GPU needed
+    assert lib.cm_probe_hbm(1 << 40, None, 4096, 3, 1, 1 << 40, None) != 0  # 3 words per lane
+    assert lib.cm_probe_hbm(1 << 40, None, 4100, 1, 1, 1 << 40, None) != 0  # not 16-byte words
+    assert lib.cm_probe_mfma_f16(1 << 40, 10, 3, 1 << 40, None) != 0  # 3 accumulator chains
+    assert lib.cm_probe_mfma_f16_flops(10, 3) == 0
