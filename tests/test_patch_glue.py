@@ -16,6 +16,7 @@ import torch
 
 from claudemaxing_amd import lm_head_loss as LH
 from claudemaxing_amd import lora, nf4, rmsnorm, rope
+from claudemaxing_amd._patching import install, tagged
 
 
 class _FakeCuda(torch.Tensor):
@@ -145,8 +146,13 @@ def test_peft_forward_falls_back_to_peft(monkeypatch):
         seen.append((args, kwargs))
         return "peft"
 
-    forward = lora._peft_forward(original)
-    assert forward._lora_branch and forward._original is original
+    class Layer:
+        pass
+
+    Layer.forward = original
+    forward = install(Layer, "forward", "lora_branch", lora._peft_forward)
+    assert tagged(forward, "lora_branch") and forward._original is original
+    assert install(Layer, "forward", "lora_branch", lora._peft_forward) is None  # idempotent
     assert forward(_peft_layer(), torch.zeros(2, 16), 3, scale=1) == "peft"
     assert seen == [((3,), {"scale": 1})]
 
@@ -174,7 +180,7 @@ class _FusedLM(torch.nn.Module):
         return SimpleNamespace(loss=torch.tensor(2.5), logits=None, asked=asked)
 
 
-_FusedLM.forward._fused_head = True
+_FusedLM.forward._cm_patch = LH._HEAD_TAG
 
 
 def _trainer(model, **args):
@@ -229,7 +235,7 @@ def test_trl_compute_loss_end_to_end(monkeypatch):
     sys.modules["trl.trainer"].sft_trainer = sft
     LH.patch_sft_compute_loss()
     LH.patch_sft_compute_loss()  # idempotent
-    assert SFTTrainer.compute_loss._fused_head
+    assert tagged(SFTTrainer.compute_loss, LH._HEAD_TAG)
     model = _FusedLM()
     model.train()
     monkeypatch.setattr(type(model.head.weight), "is_cuda", property(lambda self: True))
@@ -283,3 +289,19 @@ def test_rmsnorm_guard():
     assert not rmsnorm._kernel_covers(_cuda(torch.zeros(3, 256, dtype=torch.float64)), w)
     wide = _cuda(torch.zeros(1, rmsnorm.MAX_COLS + 8))
     assert not rmsnorm._kernel_covers(wide, _cuda(torch.ones(rmsnorm.MAX_COLS + 8)))
+
+
+def test_install_is_idempotent_and_records_the_original():
+    def stock(x):
+        return x + 1
+
+    table = {"f": stock}
+    new = install(table, "f", "demo", lambda orig: (lambda x: orig(x) * 10))
+    assert table["f"] is new and new._original is stock and tagged(new, "demo")
+    assert new(1) == 20
+    assert install(table, "f", "demo", lambda orig: None) is None and table["f"] is new
+    # another patch stacks on top and keeps the first as its original
+    other = install(table, "f", "other", lambda orig: (lambda x: orig(x) + 5))
+    assert other._original is new and other(1) == 25
+    assert install(None, "f", "demo", lambda orig: orig) is None  # class absent
+    assert install({}, "f", "demo", lambda orig: orig) is None  # attribute absent

@@ -5,6 +5,7 @@ what trains, and the padded batch's layout. The step itself runs on the GPU
 import torch
 
 from claudemaxing_amd import qlora_step
+from claudemaxing_amd._patching import tagged
 from claudemaxing_amd.lora import LoRALinear
 from claudemaxing_amd.nf4_linear import NF4Linear
 
@@ -84,7 +85,7 @@ def test_unpatched_restores_and_reapplies():
     apply()
     patch_qwen2_grouped_sdpa()
     sdpa = AttentionInterface._global_mapping["sdpa"]
-    assert getattr(sdpa, "_grouped_sdpa", False)
+    assert tagged(sdpa, "packed_sdpa")
     patched = (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
                mq.apply_rotary_pos_emb, lora._branch_applies)
     with qlora_step.unpatched():
