@@ -305,3 +305,79 @@ def test_install_is_idempotent_and_records_the_original():
     assert other._original is new and other(1) == 25
     assert install(None, "f", "demo", lambda orig: orig) is None  # class absent
     assert install({}, "f", "demo", lambda orig: orig) is None  # attribute absent
+
+
+# -- Qwen2MLP ------------------------------------------------------------------------------------
+def _mlp(act="silu"):
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    torch.manual_seed(0)
+    return modeling.Qwen2MLP(modeling.Qwen2Config(hidden_size=32, intermediate_size=64,
+                                                  hidden_act=act))
+
+
+def test_mlp_patch_falls_back_for_host_tensors_and_other_activations(monkeypatch):
+    """The reference's test_patch_falls_back_for_cpu_and_other_activations: a host input, or an
+    activation other than silu on a GPU input, runs the original forward, unchanged."""
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    from claudemaxing_amd import swiglu_recompute as SR
+
+    saved = modeling.Qwen2MLP.forward
+    original = getattr(saved, "_original", saved)
+    monkeypatch.setattr(modeling.Qwen2MLP, "forward", saved)
+    SR.patch_qwen2_mlp_recompute()
+    assert tagged(modeling.Qwen2MLP.forward, "mlp_recompute")
+    launched = []
+    monkeypatch.setattr(SR, "_swiglu_fwd", lambda *a: launched.append(a))
+    monkeypatch.setattr(SR.MLPInputRecompute, "apply", lambda *a: launched.append(a))
+    mlp = _mlp()
+    x = torch.randn(2, 5, 32, requires_grad=True)
+    assert torch.equal(mlp(x), original(mlp, x))
+    gelu = _mlp("gelu")
+    xg = _cuda(torch.randn(2, 5, 32))  # looks like a GPU tensor to the guard
+    assert torch.equal(gelu(xg), original(gelu, xg))
+    assert not launched
+
+
+def test_mlp_patch_is_idempotent(monkeypatch):
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    from claudemaxing_amd import swiglu_recompute as SR
+
+    saved = modeling.Qwen2MLP.forward
+    monkeypatch.setattr(modeling.Qwen2MLP, "forward", saved)
+    SR.patch_qwen2_mlp_recompute()
+    first = modeling.Qwen2MLP.forward
+    SR.patch_qwen2_mlp_recompute()
+    assert modeling.Qwen2MLP.forward is first
+    assert tagged(first, "mlp_recompute")
+    assert getattr(first, "_original", None) in (saved, getattr(saved, "_original", None))
+
+
+def test_mlp_patch_routes_frozen_and_trainable_projections(monkeypatch):
+    """On a GPU input with silu: frozen gate/up projections under a gradient take
+    MLPInputRecompute (told the down projection's 4-bit compute dtype, None for a dense one);
+    trainable projections, or no gradient, take the recomputing activation between the layer's
+    own projections. The kernels are intercepted, so nothing launches."""
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    from claudemaxing_amd import swiglu_recompute as SR
+
+    monkeypatch.setattr(modeling.Qwen2MLP, "forward", modeling.Qwen2MLP.forward)
+    SR.patch_qwen2_mlp_recompute()
+    seen = []
+    monkeypatch.setattr(SR.MLPInputRecompute, "apply",
+                        lambda x, g, u, dc: (seen.append(("recompute", dc)),
+                                             torch.zeros(*x.shape[:-1], 64))[1])
+    monkeypatch.setattr(SR, "swiglu_recompute",
+                        lambda gate, up, inplace=False: (seen.append(("activation", inplace)),
+                                                         gate * 0)[1])
+    mlp = _mlp()
+    x = _cuda(torch.randn(2, 5, 32)).requires_grad_(True)
+    mlp(x)  # trainable projections
+    mlp.requires_grad_(False)
+    mlp(x)  # frozen: the input is all that is kept
+    with torch.no_grad():
+        mlp(x)  # no gradient
+    assert seen == [("activation", True), ("recompute", None), ("activation", True)]

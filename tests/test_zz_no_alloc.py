@@ -13,7 +13,14 @@ from claudemaxing_amd import _lib
 from claudemaxing_amd import lm_head_loss as LH
 from oracle import inputs, lm_head as O
 from tests.conftest import banner
-from tests.helpers import assert_close
+from tests.helpers import assert_close as _assert_close
+
+
+def assert_close(actual, expected, tol, what=""):
+    """The reference's LM-head tolerance (test_lm_head_loss.py:105-108): atol is tol times the
+    largest expected value itself, however small (the hidden gradient's is ~0.1)."""
+    _assert_close(actual, expected, tol, what, floor=1e-6)
+
 
 pytestmark = pytest.mark.gpu
 
