@@ -73,9 +73,9 @@ class Kernel:
     """A benchmarked entry point: `launches` are (closure, tensors it uses) pairs, one per input
     copy, used round-robin; `work` is the algorithmic bytes (hbm) or FLOPs (mfma) of one."""
 
-    def __init__(self, name, config, bound, work, launches, step=True):
+    def __init__(self, name, config, bound, work, launches, step=True, plan=None):
         self.name, self.config, self.bound, self.work = name, config, bound, work
-        self.launches, self.step = launches, step
+        self.launches, self.step, self.plan = launches, step, plan
 
 
 def bound(name, *args):
@@ -565,15 +565,29 @@ def k_nf4_linear(dev, names):
     return out
 
 
+def _chunk_plan(n, vocab, hidden, chunk, noalloc=False):
+    """The vocabulary chunks and gradient K-slices of one LM-head call, e.g. {"chunks":
+    "4x32768+20864", "k_slices": 4}."""
+    from claudemaxing_amd import lm_head_loss
+
+    c, split = lm_head_loss.fused_head_plan(n, vocab, hidden, chunk, noalloc=noalloc)
+    full, rest = divmod(vocab, c)
+    chunks = f"{full}x{c}" + (f"+{rest}" if rest else "")
+    return {"chunks": chunks, "k_slices": split}
+
+
 def k_lmhead(dev):
+    import ctypes
+
     import torch
 
-    from claudemaxing_amd import lm_head_loss
+    from claudemaxing_amd import _lib, lm_head_loss
     from oracle import inputs
 
     h, w, t = inputs.lm_head(0)
     hd, wd, td = h.to(dev), w.to(dev), t.to(dev)
-    flops = 4 * h.shape[0] * w.shape[0] * h.shape[1]
+    n, vocab, hidden = h.shape[0], w.shape[0], h.shape[1]
+    flops = 4 * n * vocab * hidden
     w16 = lm_head_loss.fp16_head_weight(wd)  # the host's cached fp16 weight, as in training
     keep = (hd, wd, td, w16)
 
@@ -583,13 +597,34 @@ def k_lmhead(dev):
     def launch_8192(hd=hd, w16=w16, td=td):
         return lm_head_loss._fused_rows(hd, w16, td, True, 8192)
 
+    # the entry point that allocates nothing, at its own chunk (its outputs preallocated once)
+    outs = [torch.empty(n, device=dev), torch.empty(n, device=dev),
+            torch.empty(n, dtype=torch.int32, device=dev), torch.empty(n, hidden, device=dev)]
+    lib = _lib.load()
+    noalloc_args = (hd.data_ptr(), hd.stride(0), w16.data_ptr(), w16.stride(0), td.data_ptr(), n,
+                    vocab, hidden, 0, outs[0].data_ptr(), outs[1].data_ptr(),
+                    outs[2].data_ptr(), outs[3].data_ptr(), ctypes.c_float(1.0),
+                    _lib.stream(dev))
+
+    def launch_noalloc():
+        rc = lib.cm_lmhead_ce_noalloc(*noalloc_args)
+        if rc:
+            raise RuntimeError(f"cm_lmhead_ce_noalloc: {lib.cm_error_string(rc).decode()}")
+
     launch()
     launch_8192()
+    launch_noalloc()
     torch.cuda.synchronize()
-    return [Kernel("lmhead_ce", "N=2048 V=151936 H=1536 fp16", "mfma", flops, [(launch, keep)]),
-            Kernel("lmhead_ce_chunk8192", "the same in 8192-column vocabulary chunks (config 4's "
+    shape = f"N={n} V={vocab} H={hidden} fp16"
+    return [Kernel("lmhead_ce", shape, "mfma", flops, [(launch, keep)],
+                   plan=_chunk_plan(n, vocab, hidden, None)),
+            Kernel("lmhead_ce_chunk8192", shape + " in 8192-column vocabulary chunks (config 4's "
                    "stated chunk: a 32 MiB E buffer)", "mfma", flops, [(launch_8192, keep)],
-                   step=False)]
+                   step=False, plan=_chunk_plan(n, vocab, hidden, 8192)),
+            Kernel("lmhead_ce_noalloc", shape + " through cm_lmhead_ce_noalloc (no workspace "
+                   "argument: its own 64 MiB scratch array, its own chunk)", "mfma", flops,
+                   [(launch_noalloc, keep + tuple(outs))], step=False,
+                   plan=_chunk_plan(n, vocab, hidden, 0, noalloc=True))]
 
 
 ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_fwd_w32", "rmsnorm_bwd_w32",
@@ -955,6 +990,8 @@ def main():
                                   achieved=round(achieved, 1), unit=unit, bound=kern.bound,
                                   frac=round(achieved / peak, 4), work=kern.work,
                                   in_step=kern.step)
+        if kern.plan is not None:
+            results[kern.name]["plan"] = kern.plan
         print(f"[bench] {kern.name}: {ms * 1e3:.2f} us, {achieved:.1f} {unit} "
               f"({100 * achieved / peak:.1f}% of peak)", file=sys.stderr, flush=True)
     if not results:
@@ -994,7 +1031,7 @@ def main():
         "dtype": "fp16" if headline == "lmhead_ce" else "u8->fp16",
         "data": "synthetic (seeded CPU draws of BASELINE.json configs, copied to HBM)",
         "config": {"workload": headline, "shape": hr["config"], "parallelism": "none (1 GPU)",
-                   "cold_cache": "input copies rotated beyond 512 MiB"},
+                   "cold_cache": "input copies rotated beyond 512 MiB", **hr.get("plan", {})},
         "roofline": {"bound": hr["bound"], "achieved": hr["achieved"],
                      "peak": HBM_PEAK_GBS if hr["bound"] == "hbm" else MFMA_FP16_PEAK_TFLOPS,
                      "unit": hr["unit"], "frac": hr["frac"],

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -72,10 +72,11 @@ SIGNATURES = {
     "cm_lora_pack": (_I, [_P, _I, _P, _P, _P, _L, _F, _P]),
     "cm_lora_unpack": (_I, [_P, _P, _P, _P, _P, _I, _L, _F, _P]),
     "cm_xent_rows": (_I, [_P, _I, _L, _P, _P, _P, _P, _L, _L, _I, _F, _P]),
-    "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L, _P]),
+    "cm_lmhead_ce": (_I, [_P, _L, _P, _L, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P, _L, _P]),
     "cm_lmhead_ce_workspace_bytes": (_L, [_L, _L, _I, _L]),
-    "cm_lmhead_ce_noalloc": (_I, [_P, _L, _P, _L, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F,
-                                  _P]),
+    "cm_lmhead_ce_plan": (_I, [_L, _L, _I, _L, _P, _P]),
+    "cm_lmhead_ce_noalloc_plan": (_I, [_L, _L, _I, _L, _I, _P, _P]),
+    "cm_lmhead_ce_noalloc": (_I, [_P, _L, _P, _L, _P, _L, _L, _I, _L, _P, _P, _P, _P, _F, _P]),
     "cm_attn_fwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _I, _I, _I, _F,
                          _P, _P, _P, _L, _P]),
     "cm_attn_bwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _P, _P, _I, _I,

@@ -60,16 +60,8 @@ constexpr int kRowsPerBlock = 4;  // K2: token rows (one wavefront each) per wor
 
 // Tile configurations: BM, BN, wavefront grid WM x WN, stage depth BK, LDS ring stages, and the
 // minimum wavefronts per SIMD for __launch_bounds__ (which caps the registers per wavefront:
-// 2 gives 256, 1 gives 512). K1's variant 0 is the default; variant 1 is the alternative
-// measured beside it (a deeper ring of 32-column stages).
-#ifndef CM_LMH_K1
-#define CM_LMH_K1 0
-#endif
-#if CM_LMH_K1 == 1
-constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 32, kST1 = 4, kOcc1 = 2;
-#else
+// 2 gives 256, 1 gives 512).
 constexpr int kBM1 = 256, kBN1 = 256, kWM1 = 2, kWN1 = 4, kBK1 = 64, kST1 = 2, kOcc1 = 2;
-#endif
 constexpr int kThreads1 = kWM1 * kWN1 * cm::kWave;
 // K3's tile configurations, one per kind of hidden size (the tile's columns): 256 tokens x 192
 // hidden units on 4 x 2 wavefronts of 64 x 96 where the hidden size is a multiple of 192
@@ -755,8 +747,18 @@ int64_t k3_tiles(int64_t n_rows, int hidden) {
 // CUs (one workgroup each), but every slice is one more fp32 accumulator to read and rewrite
 // per chunk. Take the fewest slices whose wave fill is within 7% of the best one up to
 // kMaxSplit (N = 2048: 64 tiles x 4 at hidden 1536, 112 x 2 at 3584, 160 x 3 at 5120; N = 256:
-// 8 x 30).
-int n_split_for(int64_t n_rows, int hidden) {
+// 8 x 30), among the counts that leave no slice of a full chunk empty (whole_slices: an empty
+// slice's accumulator would still be read, rescaled and written back on every chunk, and its
+// workgroups would only pad the wave count).
+// Slices that hold columns when `groups` statistics groups are split into `sp` slices of equal
+// whole-group width (the last one shorter): fewer than sp when the width rounds up.
+int64_t whole_slices(int64_t groups, int64_t sp) {
+  if (groups <= 0 || sp <= 1) return 1;
+  const int64_t width = (groups + sp - 1) / sp;
+  return (groups + width - 1) / width;
+}
+
+int n_split_for(int64_t n_rows, int hidden, int64_t groups) {
   const int64_t tiles = k3_tiles(n_rows, hidden);
   auto fill = [&](int64_t sp) {
     const int64_t wg = tiles * sp;
@@ -767,10 +769,12 @@ int n_split_for(int64_t n_rows, int hidden) {
   const int64_t slice_bytes = round_up(n_rows * hidden * 4, 256);
   int64_t cap = 1 + (int64_t{128} << 20) / (slice_bytes > 0 ? slice_bytes : 1);
   if (cap > kMaxSplit) cap = kMaxSplit;
+  auto usable = [&](int sp) { return whole_slices(groups, sp) == sp; };
   double best = 0.0;
-  for (int sp = 1; sp <= cap; ++sp) best = fill(sp) > best ? fill(sp) : best;
   for (int sp = 1; sp <= cap; ++sp)
-    if (fill(sp) >= best - 0.07) return sp;
+    if (usable(sp)) best = fill(sp) > best ? fill(sp) : best;
+  for (int sp = 1; sp <= cap; ++sp)
+    if (usable(sp) && fill(sp) >= best - 0.07) return sp;
   return 1;
 }
 
@@ -788,7 +792,10 @@ Layout layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk, bool wan
   if (L.chunk > kMaxChunk) L.chunk = kMaxChunk;
   L.n_groups = L.chunk / kGroup;
   L.n_chunks = (vocab + L.chunk - 1) / L.chunk;
-  L.n_split = want_grad ? std::min(n_split_for(n_rows, hidden), max_split) : 1;
+  L.n_split = want_grad ? static_cast<int>(whole_slices(
+                              L.n_groups, std::min(n_split_for(n_rows, hidden, L.n_groups),
+                                                   max_split)))
+                        : 1;
   int64_t off = 0;
   L.off_e16 = off;
   off += round_up(e_rows(n_rows) * L.chunk * 2, 256);
@@ -812,6 +819,16 @@ extern "C" int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, i
                                                 int64_t chunk_cols) {
   if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0) return 0;
   return layout(n_rows, vocab, hidden_size, chunk_cols, true).total;
+}
+
+extern "C" int cm_lmhead_ce_plan(int64_t n_rows, int64_t vocab, int hidden_size,
+                                 int64_t chunk_cols, int64_t* chunk, int* n_split) {
+  CM_CHECK_ARG(n_rows > 0 && vocab > 0 && hidden_size > 0 && chunk_cols >= 0);
+  CM_CHECK_ARG(chunk != nullptr && n_split != nullptr);
+  const Layout L = layout(n_rows, vocab, hidden_size, chunk_cols, true);
+  *chunk = L.chunk;
+  *n_split = L.n_split;
+  return 0;
 }
 
 namespace {
@@ -948,13 +965,12 @@ int run_lmhead(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_
 }  // namespace
 
 extern "C" int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-                            const void* weight_t, const int64_t* target, int64_t n_rows,
+                            const int64_t* target, int64_t n_rows,
                             int64_t vocab, int hidden_size, int64_t chunk_cols, float* loss,
                             float* entropy, int32_t* correct, float* grad, float grad_scale,
                             void* workspace, int64_t workspace_bytes, void* stream) {
   CM_CHECK_ARG(n_rows >= 0);
   if (n_rows == 0) return 0;
-  (void)weight_t;  // accepted for compatibility; the gradient GEMM reads the weight as stored
   CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                        chunk_cols, loss, entropy, correct));
   CM_CHECK_ARG(workspace != nullptr);
@@ -999,6 +1015,30 @@ int scratch_of_current_device(char** out) {
   return 0;
 }
 
+// Estimated time of one call with layout L, to rank the layouts that fit the scratch. Per
+// chunk: the logits GEMM's whole waves of 256 x 256 workgroups (one per CU, ~53 us per wave at
+// hidden 1536 on MI355X, epilogue included), the gradient GEMM's work spread over whole waves of
+// its tiles x slices (~0.95 PFLOP/s when the grid fills the chip), the read and rewrite of every
+// slice's accumulator (~9 TB/s) and ~2 us of launch ramps. At N = 2048 it gives 2090 us for the
+// default layout (4 x 32768 + 20864 columns, 4 slices; measured 2094-2124) and 2590 us for
+// 23 x 6400 + 4736 columns with 4 slices (measured 2591).
+double est_cost_us(int64_t n_rows, int64_t vocab, int hidden, const Layout& L) {
+  const int64_t token_tiles = (n_rows + kBN1 - 1) / kBN1;
+  const double wave1_us = 53.0 * hidden / 1536.0;
+  const int64_t wg3 = k3_tiles(n_rows, hidden) * L.n_split;
+  const double fill3 = static_cast<double>(wg3) / static_cast<double>((wg3 + kCUs - 1) / kCUs * kCUs);
+  const double rmw_us = 2.0 * L.n_split * static_cast<double>(n_rows) * hidden * 4 / 9.0e6;
+  double us = 0.0;
+  for (int64_t c = 0; c < L.n_chunks; ++c) {
+    const int64_t cols = std::min(L.chunk, vocab - c * L.chunk);
+    const int64_t wg1 = (cols + kBM1 - 1) / kBM1 * token_tiles;
+    us += static_cast<double>((wg1 + kCUs - 1) / kCUs) * wave1_us;
+    us += 2.0 * static_cast<double>(n_rows) * cols * hidden / 0.95e9 / fill3;
+    us += (c == 0 ? 0.5 : 1.0) * rmw_us + 2.0;
+  }
+  return us;
+}
+
 // The chunk the scratch can hold: chunk_cols itself when given (0 when it does not fit), else
 // the largest multiple of 256 columns (at most the whole vocabulary) whose layout fits.
 int64_t scratch_chunk(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_cols,
@@ -1015,31 +1055,68 @@ int64_t scratch_chunk(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_c
   return lo * kChunkAlign;
 }
 
+// The layout cm_lmhead_ce_noalloc runs in its scratch (false: none fits). K-slices (each an fp32
+// [n_rows, hidden] accumulator) and chunk: with chunk_cols given, the most slices up to the
+// workspace entry's that fit beside that chunk; else, of the pairs (slice count, a chunk from
+// the largest that fits beside that many slices down to half of it), the one estimated fastest.
+bool scratch_layout(int64_t n_rows, int64_t vocab, int hidden, int64_t chunk_cols,
+                    bool want_grad, Layout* out) {
+  int best_split = 0;
+  int64_t best_chunk = 0;
+  double best_cost = 0.0;
+  for (int sp = kMaxSplit; sp >= 1; --sp) {
+    const int64_t largest = scratch_chunk(n_rows, vocab, hidden, chunk_cols, want_grad, sp);
+    if (largest == 0) continue;
+    // with chunk_cols given, that chunk; else every multiple of 256 columns from the largest
+    // that fits down to half of it (a smaller chunk can fill the logits GEMM's waves better)
+    const int64_t smallest = chunk_cols > 0 ? largest : std::max<int64_t>(kChunkAlign, largest / 2);
+    bool any = false;
+    for (int64_t chunk = largest; chunk >= smallest; chunk -= kChunkAlign) {
+      const Layout T = layout(n_rows, vocab, hidden, chunk, want_grad, sp);
+      if (T.n_split < sp) continue;  // the same layout as a smaller count, visited later
+      any = true;
+      const double cost = est_cost_us(n_rows, vocab, hidden, T);
+      if (best_split == 0 || cost < best_cost) {
+        best_split = sp;
+        best_chunk = chunk;
+        best_cost = cost;
+      }
+    }
+    if (chunk_cols > 0 && any) break;
+  }
+  if (best_split == 0) return false;
+  *out = layout(n_rows, vocab, hidden, best_chunk, want_grad, best_split);
+  return out->total <= kScratchBytes;
+}
+
 }  // namespace
 
+extern "C" int cm_lmhead_ce_noalloc_plan(int64_t n_rows, int64_t vocab, int hidden_size,
+                                         int64_t chunk_cols, int want_grad, int64_t* chunk,
+                                         int* n_split) {
+  CM_CHECK_ARG(n_rows > 0 && vocab > 0 && hidden_size > 0 && chunk_cols >= 0);
+  CM_CHECK_ARG(chunk != nullptr && n_split != nullptr);
+  Layout L;
+  if (!scratch_layout(n_rows, vocab, hidden_size, chunk_cols, want_grad != 0, &L))
+    return CM_ERROR_SCRATCH_TOO_SMALL;
+  *chunk = L.chunk;
+  *n_split = L.n_split;
+  return 0;
+}
+
 extern "C" int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void* weight,
-                                    int64_t ld_w, const void* weight_t, const int64_t* target,
+                                    int64_t ld_w, const int64_t* target,
                                     int64_t n_rows, int64_t vocab, int hidden_size,
                                     int64_t chunk_cols, float* loss, float* entropy,
                                     int32_t* correct, float* grad, float grad_scale,
                                     void* stream) {
   CM_CHECK_ARG(n_rows >= 0);
   if (n_rows == 0) return 0;
-  (void)weight_t;  // accepted for compatibility; the gradient GEMM reads the weight as stored
   CM_CHECK_ARG(args_ok(hidden, ld_h, weight, ld_w, target, n_rows, vocab, hidden_size,
                        chunk_cols, loss, entropy, correct));
-  const bool want_grad = grad != nullptr;
-  // the workspace entry's K-slices where they fit the scratch, else fewer (each is an fp32
-  // [n_rows, hidden] accumulator)
-  int max_split = kMaxSplit;
-  int64_t chunk = 0;
-  for (; max_split >= 1; --max_split) {
-    chunk = scratch_chunk(n_rows, vocab, hidden_size, chunk_cols, want_grad, max_split);
-    if (chunk != 0) break;
-  }
-  if (chunk == 0) return CM_ERROR_SCRATCH_TOO_SMALL;
-  const Layout L = layout(n_rows, vocab, hidden_size, chunk, want_grad, max_split);
-  if (L.total > kScratchBytes) return CM_ERROR_SCRATCH_TOO_SMALL;
+  Layout L;
+  if (!scratch_layout(n_rows, vocab, hidden_size, chunk_cols, grad != nullptr, &L))
+    return CM_ERROR_SCRATCH_TOO_SMALL;
   char* ws = nullptr;
   const int st = scratch_of_current_device(&ws);
   if (st) return st;

@@ -379,24 +379,16 @@ int tiles_bound(int len) {
   return per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 12 ? 12 : 16;
 }
 
-#ifndef CM_LORA_QUAD_ROWS
-#define CM_LORA_QUAD_ROWS 0
-#endif
 // Token rows per workgroup of the column-quad kernels: the most (of 1, 2, 4, 8, 16) that still
 // gives the CUs a workgroup each.
 int quad_rows(int64_t T) {
-  if (CM_LORA_QUAD_ROWS > 0) return CM_LORA_QUAD_ROWS;
   int r = 16;
   while (r > 1 && (T + r - 1) / r < kCUs) r /= 2;
   return r;
 }
 
-#ifndef CM_LORA_TILE_ROWS
-#define CM_LORA_TILE_ROWS 0
-#endif
 // Token rows per tile: 16, or fewer when 16-row tiles would leave CUs idle.
 int tile_rows(int64_t T) {
-  if (CM_LORA_TILE_ROWS > 0) return CM_LORA_TILE_ROWS;
   const int64_t r = (T + kCUs - 1) / kCUs;
   return static_cast<int>(std::min<int64_t>(kTileRows, std::max<int64_t>(1, r)));
 }

@@ -22,13 +22,7 @@ namespace {
 #pragma clang fp contract(off)
 
 constexpr int kThreads = 256;
-#ifndef CM_NF4_UNITS
-#define CM_NF4_UNITS 4
-#endif
-#ifndef CM_NF4_NT_STORE
-#define CM_NF4_NT_STORE 1
-#endif
-constexpr int kUnits = CM_NF4_UNITS;  // 4-byte units per lane
+constexpr int kUnits = 4;  // 4-byte units per lane
 constexpr int64_t kResidentBlocks = 2048;  // 256-lane workgroups the chip holds at once
 
 template <bool NESTED>
@@ -55,11 +49,7 @@ struct Pack8<_Float16> {
     h8 h;
 #pragma unroll
     for (int i = 0; i < 8; ++i) h[i] = cm::from_f32<_Float16>(v[i]);
-#if CM_NF4_NT_STORE
     __builtin_nontemporal_store(h, reinterpret_cast<h8*>(out));
-#else
-    *reinterpret_cast<h8*>(out) = h;
-#endif
   }
 };
 

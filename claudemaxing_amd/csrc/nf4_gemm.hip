@@ -468,18 +468,11 @@ __global__ __launch_bounds__(kThreads, 2) void nf4_gemm_kernel(const Args args) 
 // The contraction may be split over gridDim: slice s of S covers stages [s n / S, (s + 1) n / S)
 // and writes fp32 partial sums; nf4_gemm_reduce adds the slices in order (deterministic), adds
 // the bias and rounds.
-#ifndef CM_NF4_CONSUMERS
-#define CM_NF4_CONSUMERS 8
-#endif
-constexpr int kConsumers = CM_NF4_CONSUMERS;  // MFMA wavefronts: 2 x 2 or 4 x 2
+constexpr int kConsumers = 8;  // MFMA wavefronts: 4 x 2 (256-row tiles) or 2 x 4 (128-row)
 constexpr int kProducers = 4;
 constexpr int kWsThreads = (kConsumers + kProducers) * 64;
 constexpr int kRing = 3;
 constexpr int kWsBN = 128;
-#ifndef CM_NF4_WIDE_TOKENS
-#define CM_NF4_WIDE_TOKENS 1
-#endif
-constexpr bool kWideTokens = CM_NF4_WIDE_TOKENS;
 
 // One global_load_lds_dword: lane l's 4 bytes from g land at lds_lane0 + 4 l (wave-uniform base in
 // M0); issued like gemm::dma16.
@@ -999,7 +992,7 @@ Plan plan_for(const Args& a, bool trans) {
       if (sp2 > n_stages_all / 8) sp2 = n_stages_all / 8;
       if (sp2 < 1) sp2 = 1;
     }
-    if (kWideTokens && a.m >= 384 && tiles2 * sp2 >= kCUs * 3 / 4) {
+    if (a.m >= 384 && tiles2 * sp2 >= kCUs * 3 / 4) {
       p.bm = 128;
       p.bn = 256;
       p.tiles = tiles2;

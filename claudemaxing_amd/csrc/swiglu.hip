@@ -12,18 +12,12 @@
 // contiguous 1 KiB span. 2^x is v_exp_f32 and 1/x is v_rcp_f32 (about 1 ulp each; the
 // reference's Triton exp2 and division are not correctly rounded either). Every input element
 // is read exactly once, so loads and stores are both nontemporal.
-#ifndef CM_VEC_NT_LOAD
-#define CM_VEC_NT_LOAD 1
-#endif
 #include "vec.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-#ifndef CM_SWIGLU_UNITS
-#define CM_SWIGLU_UNITS 1
-#endif
-constexpr int kUnits = CM_SWIGLU_UNITS;
+constexpr int kUnits = 1;  // 8-element vectors per lane
 constexpr float kNegLog2e = -1.4426950408889634f;
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -43,8 +37,8 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_kernel(const GT* __restri
     const int64_t e0 = vi * 8;
     const int cnt = n - e0 >= 8 ? 8 : static_cast<int>(n - e0);
     float g[8], u[8], o[8];
-    cm::Vec8<GT, ALIGNED>::load(gate + e0, g, cnt);
-    cm::Vec8<UT, ALIGNED>::load(up + e0, u, cnt);
+    cm::Vec8<GT, ALIGNED, true>::load(gate + e0, g, cnt);
+    cm::Vec8<UT, ALIGNED, true>::load(up + e0, u, cnt);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float s = g[i] * rcp_fast(1.0f + exp2_fast(g[i] * kNegLog2e));
@@ -71,9 +65,9 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const DT* __restri
     const int64_t e0 = vi * 8;
     const int cnt = n - e0 >= 8 ? 8 : static_cast<int>(n - e0);
     float d[8], g[8], u[8], dg[8], du[8];
-    cm::Vec8<DT, ALIGNED>::load(dy + e0, d, cnt);
-    cm::Vec8<GT, ALIGNED>::load(gate + e0, g, cnt);
-    if (want_dgate) cm::Vec8<UT, ALIGNED>::load(up + e0, u, cnt);
+    cm::Vec8<DT, ALIGNED, true>::load(dy + e0, d, cnt);
+    cm::Vec8<GT, ALIGNED, true>::load(gate + e0, g, cnt);
+    if (want_dgate) cm::Vec8<UT, ALIGNED, true>::load(up + e0, u, cnt);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float sig = rcp_fast(1.0f + exp2_fast(g[i] * kNegLog2e));

@@ -5,45 +5,36 @@
 
 #include "common.h"
 
-// Streaming hints for the aligned 16-byte accesses: with CM_VEC_NT_STORE / CM_VEC_NT_LOAD set,
-// they are issued as nontemporal (streaming) accesses. Measured on MI355X with cold caches,
-// nontemporal stores speed up every elementwise kernel here (SwiGLU forward 21.0 -> 18.6 us,
-// RMSNorm backward 8.0 -> 6.5 us, LoRA unpack 5.7 -> 4.9 us); nontemporal loads help only
-// kernels that read each input once (SwiGLU backward 35.8 -> 30.9 us) and slow RMSNorm, which
-// reads its rows twice, so a file opts into them by defining CM_VEC_NT_LOAD before this header.
-#ifndef CM_VEC_NT_STORE
-#define CM_VEC_NT_STORE 1
-#endif
-#ifndef CM_VEC_NT_LOAD
-#define CM_VEC_NT_LOAD 0
-#endif
-
+// Streaming hints for the aligned 16-byte accesses. Stores are nontemporal (streaming): measured
+// on MI355X with cold caches, they speed up every elementwise kernel here (SwiGLU forward
+// 21.0 -> 18.6 us, RMSNorm backward 8.0 -> 6.5 us, LoRA unpack 5.7 -> 4.9 us). Loads are
+// nontemporal only where a kernel asks (Vec8's STREAM): that helps kernels that read each input
+// once (SwiGLU backward 35.8 -> 30.9 us) and slows RMSNorm, which reads its rows twice.
 namespace cm {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 16 bytes at p (16-byte aligned), as any 16-byte type V.
-template <typename V>
+// 16 bytes at p (16-byte aligned), as any 16-byte type V; STREAM = a nontemporal load.
+template <typename V, bool STREAM = false>
 __device__ __forceinline__ V load16(const void* p) {
   static_assert(sizeof(V) == 16, "16-byte accesses only");
-#if CM_VEC_NT_LOAD
-  return __builtin_bit_cast(V, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
-#else
-  return __builtin_bit_cast(V, *static_cast<const u32x4*>(p));
-#endif
+  if constexpr (STREAM) {
+    return __builtin_bit_cast(V, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
+  } else {
+    return __builtin_bit_cast(V, *static_cast<const u32x4*>(p));
+  }
 }
 
+// 16 bytes to p (16-byte aligned), nontemporal.
 template <typename V>
 __device__ __forceinline__ void store16(void* p, V v) {
   static_assert(sizeof(V) == 16, "16-byte accesses only");
-#if CM_VEC_NT_STORE
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), static_cast<u32x4*>(p));
-#else
-  *static_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v);
-#endif
 }
 
-template <typename T, bool ALIGNED>
+// Eight elements of T at a time, converted to and from fp32. ALIGNED: every 8-element group is
+// 16-byte aligned (16-byte accesses); STREAM: its loads are nontemporal.
+template <typename T, bool ALIGNED, bool STREAM = false>
 struct Vec8 {
   // Load elements [0, cnt) of p (cnt <= 8); the rest are 0.
   static __device__ __forceinline__ void load(const T* p, float (&v)[8], int cnt = 8) {
@@ -57,12 +48,12 @@ struct Vec8 {
   }
 };
 
-template <>
-struct Vec8<_Float16, true> {
+template <bool STREAM>
+struct Vec8<_Float16, true, STREAM> {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   static __device__ __forceinline__ void load(const _Float16* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const h8 h = load16<h8>(p);
+      const h8 h = load16<h8, STREAM>(p);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(h[i]);
     } else {
@@ -81,11 +72,11 @@ struct Vec8<_Float16, true> {
   }
 };
 
-template <>
-struct Vec8<bf16_t, true> {
+template <bool STREAM>
+struct Vec8<bf16_t, true, STREAM> {
   static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const uint4 w = load16<uint4>(p);
+      const uint4 w = load16<uint4, STREAM>(p);
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -110,12 +101,12 @@ struct Vec8<bf16_t, true> {
   }
 };
 
-template <>
-struct Vec8<float, true> {
+template <bool STREAM>
+struct Vec8<float, true, STREAM> {
   static __device__ __forceinline__ void load(const float* p, float (&v)[8], int cnt = 8) {
     if (cnt == 8) {
-      const float4 a = load16<float4>(p);
-      const float4 b = load16<float4>(p + 4);
+      const float4 a = load16<float4, STREAM>(p);
+      const float4 b = load16<float4, STREAM>(p + 4);
       v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
       v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {

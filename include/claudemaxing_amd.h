@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 1
+#define CM_ABI_VERSION 2
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -208,9 +208,9 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
  *   grad (if not NULL) [n_rows, H] fp32 = grad_scale * sum_v (softmax_v - [v == t_r]) W[v,:]
  *     (zero rows for unlabelled targets)
  * hidden fp16 [n_rows, H] (row stride ld_h), W fp16 [V, H] (row stride ld_w), target int64.
- * weight_t is not read (any value, NULL included): the gradient pass reads W itself, through
- * transposing LDS reads, so no transposed copy of the weight exists. H, ld_h, ld_w must be
- * multiples of 8 and the bases 16-byte aligned.
+ * Both contractions read W as stored (the gradient pass through transposing LDS reads), so no
+ * transposed copy of the weight exists. H, ld_h, ld_w must be multiples of 8 and the bases
+ * 16-byte aligned.
  * The vocabulary is walked in chunks of chunk_cols columns (rounded up to a multiple of 256, at
  * most 262144; 0 = the library's default, which keeps the chunk buffer at 128 MiB or less); the
  * result does not depend on the chunk size beyond fp32 rounding.
@@ -218,13 +218,18 @@ int cm_xent_rows(void* logits, int logits_dtype, int64_t row_stride, const int64
  * 256-B aligned.
  */
 int cm_lmhead_ce(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-                 const void* weight_t, const int64_t* target, int64_t n_rows, int64_t vocab,
-                 int hidden_size,
+                 const int64_t* target, int64_t n_rows, int64_t vocab, int hidden_size,
                  int64_t chunk_cols, float* loss, float* entropy, int32_t* correct, float* grad,
                  float grad_scale, void* workspace, int64_t workspace_bytes, void* stream);
 /* Workspace bytes cm_lmhead_ce needs for these sizes (chunk_cols as passed to cm_lmhead_ce). */
 int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_size,
                                      int64_t chunk_cols);
+/* The plan cm_lmhead_ce runs with a gradient at these sizes: *chunk = the vocabulary chunk's
+ * columns (the last chunk takes the rest), *n_split = the gradient contraction's K-slices.
+ * A query only (no launch, no device access); no counterpart in the reference, whose chunk is
+ * its own rule (lm_head_loss.py:209-211). */
+int cm_lmhead_ce_plan(int64_t n_rows, int64_t vocab, int hidden_size, int64_t chunk_cols,
+                      int64_t* chunk, int* n_split);
 
 /* cm_lmhead_ce without a workspace argument: it allocates nothing (no hipMalloc / hipFree or
  * allocating library call, on any call). No counterpart in the reference: it is for callers
@@ -234,21 +239,30 @@ int64_t cm_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab, int hidden_s
  * Its scratch is a file-scope device array of CM_LMHEAD_NOALLOC_SCRATCH_BYTES, one per GPU,
  * held by that GPU until the process ends; its device address is looked up once per device on
  * the first call with that device current, so call it with the stream's device current. The
- * vocabulary chunk is chunk_cols when given, else the largest multiple of 256 columns whose
- * workspace (cm_lmhead_ce_workspace_bytes with that chunk; less without a gradient) fits the
- * scratch: with the same chunk the results are bit-identical to
- * cm_lmhead_ce's. Sizes whose smallest layout (or the given chunk's) does not fit return
- * CM_ERROR_SCRATCH_TOO_SMALL before anything is launched. Every call on one GPU uses that GPU's
+ * gradient pass splits its contraction into K-slices (one fp32 [n_rows, H] accumulator each);
+ * the scratch holds the vocabulary chunk's buffers and the slices' accumulators, and the entry
+ * point picks the (slices, chunk) pair it estimates fastest among those that fit: chunk_cols
+ * when given, with the most slices (up to cm_lmhead_ce's count) that fit beside it; else, over
+ * the slice counts, the chunks (multiples of 256 columns) from the largest that fits down to
+ * half of it. Where it runs cm_lmhead_ce's slice count and chunk, the results are bit-identical to
+ * cm_lmhead_ce's; with fewer slices only the fp32 summation order of the gradient differs
+ * (within the same tolerances). Sizes whose smallest layout (or the given chunk's) does not fit
+ * return CM_ERROR_SCRATCH_TOO_SMALL before anything is launched. Every call on one GPU uses that GPU's
  * one array: calls that overlap on one GPU (other streams, other threads) race; nothing in the
  * array needs to start at any value, so stream-ordered calls need nothing between them.
  */
 #define CM_LMHEAD_NOALLOC_SCRATCH_BYTES (64LL << 20)
 #define CM_ERROR_SCRATCH_TOO_SMALL 20001
 int cm_lmhead_ce_noalloc(const void* hidden, int64_t ld_h, const void* weight, int64_t ld_w,
-                         const void* weight_t, const int64_t* target, int64_t n_rows,
-                         int64_t vocab, int hidden_size, int64_t chunk_cols, float* loss,
+                         const int64_t* target, int64_t n_rows, int64_t vocab,
+                         int hidden_size, int64_t chunk_cols, float* loss,
                          float* entropy, int32_t* correct, float* grad, float grad_scale,
                          void* stream);
+/* The plan cm_lmhead_ce_noalloc runs at these sizes (want_grad: a gradient is asked for): the
+ * chunk's columns and the K-slices, as cm_lmhead_ce_plan; CM_ERROR_SCRATCH_TOO_SMALL when
+ * nothing fits. A query only. */
+int cm_lmhead_ce_noalloc_plan(int64_t n_rows, int64_t vocab, int hidden_size, int64_t chunk_cols,
+                              int want_grad, int64_t* chunk, int* n_split);
 
 /* ------------------------------------------------------------------------------------------ */
 /* Causal grouped-query attention over a packed batch of variable-length rows, forward. Replaces,

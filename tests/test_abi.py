@@ -239,3 +239,26 @@ def test_peak_probes_refuse_bad_arguments(lib):
     assert lib.cm_probe_hbm(1 << 40, None, 4100, 1, 1, 1 << 40, None) != 0  # not 16-byte words
     assert lib.cm_probe_mfma_f16(1 << 40, 10, 3, 1 << 40, None) != 0  # 3 accumulator chains
     assert lib.cm_probe_mfma_f16_flops(10, 3) == 0
+
+
+def test_lmhead_plans(lib):
+    """The chunk and gradient K-slices each LM-head entry point runs (queries, no GPU): at config
+    4 four slices fill the 256 CUs (64 output tiles x 4); at its stated 8192-column chunk the
+    no-allocation entry fits three slices beside the chunk's buffers in its 64 MiB scratch; no
+    plan leaves a slice of a full chunk without columns."""
+    from claudemaxing_amd import lm_head_loss as LH
+
+    V, H = 151936, 1536
+    assert LH.fused_head_plan(2048, V, H) == (32768, 4)
+    assert LH.fused_head_plan(2048, V, H, 8192) == (8192, 4)
+    assert LH.fused_head_plan(2048, V, H, 8192, noalloc=True) == (8192, 3)
+    chunk, split = LH.fused_head_plan(2048, V, H, noalloc=True)
+    assert 1 <= split <= 4 and chunk % 256 == 0 and chunk >= 2048
+    with pytest.raises(RuntimeError, match="scratch"):
+        LH.fused_head_plan(2048, V, H, V, noalloc=True)
+    for n, c in ((128, 4096), (256, 0), (300, 2048), (1100, 4096), (2048, 0), (5000, 0)):
+        for noalloc in (False, True):
+            chunk, split = LH.fused_head_plan(n, V, H, c, noalloc=noalloc)
+            groups = chunk // 128
+            width = -(-groups // split)
+            assert -(-groups // width) == split, (n, c, noalloc, chunk, split)

@@ -36,7 +36,7 @@ def _noalloc(h16, w16, tgt, chunk, want_grad=True):
     grad = torch.full((n, hidden), -7.0, device=dev) if want_grad else None
     before = torch.cuda.memory_allocated(dev)
     rc = _lib.load().cm_lmhead_ce_noalloc(
-        h16.data_ptr(), h16.stride(0), w16.data_ptr(), w16.stride(0), None,
+        h16.data_ptr(), h16.stride(0), w16.data_ptr(), w16.stride(0),
         tgt.data_ptr(), n, w16.shape[0], hidden, chunk, loss.data_ptr(), ent.data_ptr(),
         corr.data_ptr(), _lib.ptr(grad), 1.0, _lib.stream(dev))
     assert torch.cuda.memory_allocated(dev) == before  # no allocation through torch either
@@ -105,3 +105,28 @@ def test_noalloc_own_chunk_and_refusal(dev):
     assert b"scratch" in _lib.load().cm_error_string(rc)
     torch.cuda.synchronize()
     assert torch.all(out[0] == -7.0) and torch.all(out[3] == -7.0)
+
+
+def test_noalloc_fewer_slices_at_config4_chunk8192(dev):
+    """Config 4 at its stated 8192-column chunk: the chunk's buffers (35 MiB) and the workspace
+    entry's four gradient K-slices (three 12.6 MB accumulators beside the output) exceed the
+    64 MiB scratch, so the entry point runs three slices. The logits pass is the same (same
+    chunk), so loss, entropy and correct are the workspace entry's bits; the gradient sums its
+    slices in another fp32 order and agrees within tolerance, and a seeded 64-row subset
+    matches the oracle."""
+    banner("lmhead noalloc: config 4, chunk 8192, fewer slices")
+    assert LH.fused_head_plan(2048, 151936, 1536, 8192) == (8192, 4)
+    assert LH.fused_head_plan(2048, 151936, 1536, 8192, noalloc=True) == (8192, 3)
+    h, w, t = inputs.lm_head(0)
+    hd, wd, td = h.to(dev), w.to(dev), t.to(dev)
+    w16 = LH.fp16_head_weight(wd)
+    rc, got = _noalloc(hd, w16, td, 8192)
+    assert rc == 0, _lib.load().cm_error_string(rc)
+    ref = LH._fused_rows(hd, w16, td, True, 8192)
+    torch.cuda.synchronize()
+    _same_bits(got[:3], ref[:3], "forward terms")
+    assert_close(got[3], ref[3], 1e-3, "grad vs the workspace entry")
+    rows = torch.randperm(2048, generator=torch.Generator().manual_seed(2))[:64]
+    o = O.head(h[rows], w, t[rows])
+    assert_close(got[0][rows.to(dev)], o[0], 1e-4, "loss vs oracle")
+    assert_close(got[3][rows.to(dev)], o[3], 1e-2, "grad vs oracle")
