@@ -364,16 +364,24 @@ def k_copy_ref(dev):
 
 
 def k_floor(dev, names):
-    """What a launch costs on this box whatever it does, under the same cold-cache rotation:
-    a kernel that does no work (torch's spin kernel with a zero cycle count), a one-wavefront
-    kernel (a 64-element fill) and a 1 MiB device copy. These set the floor under the small
-    config-2 / config-5 launches."""
+    """What a launch costs on this box whatever it does: the library's empty kernel
+    (cm_probe_launch, through the same ctypes path as every kernel here) with one wavefront and
+    with the grid of the config-2 RoPE launch (1193 workgroups of 256 lanes), a one-wavefront
+    torch kernel (a 64-element fill) and a 1 MiB torch device copy. The HIP-event figures here
+    are the rate at which the host issues them back to back; the rocprofv3 kernel trace of the
+    same command gives the device time of each (the floor under the small config-2 / config-5
+    launches)."""
     import torch
 
     out = []
+    st = _stream(dev)
     if "floor_empty" in names:
-        out.append(Kernel("floor_empty", "torch.cuda._sleep(0): one empty workgroup", "hbm", 0,
-                          [((lambda: torch.cuda._sleep(0)), ())], step=False))
+        out.append(Kernel("floor_empty", "cm_probe_launch: one empty wavefront", "hbm", 0,
+                          [(bound("cm_probe_launch", 1, 64, st), ())], step=False))
+    if "floor_empty_grid" in names:
+        out.append(Kernel("floor_empty_grid", "cm_probe_launch: 1193 empty workgroups of 256 "
+                          "lanes (the config-2 RoPE grid)", "hbm", 0,
+                          [(bound("cm_probe_launch", 1193, 256, st), ())], step=False))
     if "floor_one_wave" in names:
         launches = []
         for _ in range(64):
@@ -629,13 +637,13 @@ def k_lmhead(dev):
 
 ALL = ["nf4_dequant", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_fwd_w32", "rmsnorm_bwd_w32",
        "rmsnorm_fwd_qlora", "rmsnorm_bwd_qlora", "rope_fwd", "rope_bwd", "swiglu_fwd",
-       "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "floor_empty", "floor_one_wave",
-       "floor_copy_1mib", "nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw",
+       "swiglu_bwd", "lora_pack", "lora_unpack", "hbm_copy_ref", "floor_empty", "floor_empty_grid",
+       "floor_one_wave", "floor_copy_1mib", "nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw",
        "rope_bwd_bw", "lora_pack_bw", "lora_unpack_bw", "nf4_linear_fwd", "nf4_linear_bwd",
        "lmhead_ce"]
 BW_ROWS = {"nf4_dequant_bw", "rmsnorm_fwd_bw", "rmsnorm_bwd_bw", "rope_fwd_bw", "rope_bwd_bw",
            "lora_pack_bw", "lora_unpack_bw"}
-FLOORS = {"floor_empty", "floor_one_wave", "floor_copy_1mib"}
+FLOORS = {"floor_empty", "floor_empty_grid", "floor_one_wave", "floor_copy_1mib"}
 
 
 def build_kernels(dev, only):

@@ -92,6 +92,7 @@ SIGNATURES = {
     "cm_probe_hbm": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "cm_probe_mfma_f16": (_I, [_P, _I, _I, _P, _P]),
     "cm_probe_mfma_f16_flops": (_L, [_I, _I]),
+    "cm_probe_launch": (_I, [_I, _I, _P]),
     "cm_nf4_scale_map": (_I, [_PW, _P, _P]),
 }
 

@@ -16,6 +16,10 @@
 // data (the matrix cores draw more power on changing, non-zero operands, which sets the clock);
 // the sums are written only if they hit a sentinel. Fewer chains leave more wavefronts per SIMD
 // (registers), more chains more independent MFMAs per wavefront; bench.py takes the best.
+//
+// Launch floor: a kernel whose workgroups do nothing, launched through the same C ABI as the
+// library's kernels, so that a kernel trace gives the device time any launch of that grid costs
+// on this board (the floor under the small row kernels of a training step).
 #include "common.h"
 
 namespace {
@@ -88,7 +92,16 @@ __global__ __launch_bounds__(kThreads) void mfma_rate(const half8* __restrict__ 
   if (s == 1234567.0f) sink[0] = s;
 }
 
+__global__ void empty_kernel() {}
+
 }  // namespace
+
+extern "C" int cm_probe_launch(int blocks, int threads, void* stream) {
+  CM_CHECK_ARG(blocks > 0 && threads > 0 && threads <= 1024 && threads % cm::kWave == 0);
+  hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream));
+  return cm::launch_status();
+}
 
 extern "C" int cm_probe_hbm(const void* src, void* dst, int64_t bytes, int per_lane,
                             int nt_loads, uint32_t* sink, void* stream) {

@@ -443,6 +443,10 @@ int cm_probe_mfma_f16(const void* operands, int iters, int chains, float* sink, 
 /* Matrix-core FLOPs of one cm_probe_mfma_f16 call (0 for invalid arguments). */
 int64_t cm_probe_mfma_f16_flops(int iters, int chains);
 
+/* Launch floor: `blocks` workgroups of `threads` (a multiple of 64, at most 1024) threads that
+ * do nothing; a kernel trace gives the device time a launch of that grid costs. */
+int cm_probe_launch(int blocks, int threads, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

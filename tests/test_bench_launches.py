@@ -131,7 +131,7 @@ def recorded(monkeypatch):
 
 def test_every_bench_launch_stays_inside_its_tensors(recorded):
     dev = torch.device("cpu")
-    # torch-only lines (the device copy, the launch floors) bind no C-ABI call
+    # the device copy and the launch floors pass no tensors to check
     names = set(bench.ALL) - {"lmhead_ce", "hbm_copy_ref"} - bench.FLOORS
     kernels = bench.build_kernels(dev, sorted(names))
     # "_unfused" and "_split" lines time torch-level comparison paths beside a C-ABI entry
