@@ -913,17 +913,20 @@ def qlora_step_bench(dev, steps, warmup=2):
     from claudemaxing_amd import qlora_step
 
     t0 = time.perf_counter()
+    whole = qlora_step.VramPoller(dev).__enter__()  # the build and every step below
     model = qlora_step.build_model(dev, seed=0)
     batch, lengths = qlora_step.make_batch(dev, seed=0)
     opt = qlora_step.make_optimizer(model)
     scaler = torch.amp.GradScaler("cuda")
     build_s = time.perf_counter() - t0
+    build_peak_allocated = torch.cuda.max_memory_allocated() / 2 ** 30
     # the headline step figure: a fresh batch (new lengths) every step, eager, TRL's metrics
     # computed every step; then one repeated batch eager; then the fresh batches with a new HIP
     # graph captured for every batch (capture inside the timed step), and the repeated batch
     # replayed from a graph. The eager runs come first: the capture stream keeps torch's BLAS
     # workspaces, which would otherwise count in the eager peaks.
-    rd = qlora_step.time_distinct_batches(model, opt, scaler, steps, warmup)
+    with qlora_step.VramPoller(dev) as vram:
+        rd = qlora_step.time_distinct_batches(model, opt, scaler, steps, warmup)
     r = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup)
     rdg = qlora_step.time_distinct_batches(model, opt, scaler, max(3, steps // 3), 1,
                                            graphed=True)
@@ -936,6 +939,17 @@ def qlora_step_bench(dev, steps, warmup=2):
                    tokens=rd["tokens"], tokens_per_s=round(rd["tokens_per_s"], 1),
                    peak_allocated_gb=round(rd["peak_allocated_gb"], 3),
                    peak_reserved_gb=round(rd["peak_reserved_gb"], 3),
+                   peak_allocated_mib=round(rd["peak_allocated_gb"] * 1024),
+                   peak_reserved_mib=round(rd["peak_reserved_gb"] * 1024),
+                   device_used_peak_mib=round(vram.peak),
+                   device_used_at_start_mib=round(whole.start),
+                   device_used_peak_over_start_mib=round(vram.peak - whole.start),
+                   memory_note="torch's peak allocated / reserved bytes over the timed steps, and "
+                               "device memory in use (total - free, every 100 ms, as the "
+                               "reference's harness polls nvidia-smi) at its peak over them and "
+                               "before this process allocated anything; the reference publishes "
+                               "2447 / 2696 MiB allocated / reserved and a 2839 MiB nvidia-smi "
+                               "peak (T4, EXPERIMENTS.md run 5)",
                    note="eager, a new batch every step (the headline step figure)",
                    graphed_with_capture=dict(
                        median_ms=round(rdg["median_ms"], 2),
@@ -960,6 +974,9 @@ def qlora_step_bench(dev, steps, warmup=2):
                                  "shape; packing and the GradScaler/AdamW step eager; "
                                  "peak_hbm_gb = the replay's peak allocated bytes + the "
                                  "graph's private pool (activations of the captured pass)"))
+    whole.__exit__(None, None, None)
+    out["build_peak_allocated_gb"] = round(build_peak_allocated, 3)
+    out["device_used_peak_whole_run_mib"] = round(whole.peak)
     del model, opt
     torch.cuda.empty_cache()
     return out

@@ -25,6 +25,7 @@ so the same model can be run through both (the parity test of the step).
 """
 
 import contextlib
+import threading
 import time
 
 import torch
@@ -60,37 +61,84 @@ def qwen2_config(**overrides):
 
 
 def build_model(device, seed=0, r=16, alpha=32, dropout=0.05, patch=True, **overrides):
-    """The QLoRA model: random-init Qwen2 weights (seeded), NF4 decoder linears, LoRA on q/v."""
+    """The QLoRA model: random-init Qwen2 weights (seeded), NF4 decoder linears, LoRA on q/v.
+
+    transformers' Qwen2ForCausalLM is built on the meta device and materialized part by part:
+    the embedding (tied to the head), the final norm and the rotary table, then one decoder layer
+    at a time, whose fp32 linears exist on `device` only until they are stored as NF4. The
+    device's peak during the build is then the embedding, one fp32 layer and the NF4 layers
+    so far (~1.8 GB at the 1.5B shape), where building the whole fp32 model first took 6.8 GB
+    and left its NF4 layers scattered over 2 GB of cached, unreleasable segments. Weights are
+    drawn as transformers' _init_weights draws them (linears and embedding N(0,
+    initializer_range), zero biases, unit norm weights) and rounded to fp16 values, as a
+    checkpoint loaded in fp16 and upcast for k-bit training."""
     from transformers import Qwen2ForCausalLM
+    from transformers.models.qwen2.modeling_qwen2 import (Qwen2DecoderLayer, Qwen2RMSNorm,
+                                                          Qwen2RotaryEmbedding)
 
     if patch:
         apply()
     cfg = qwen2_config(**overrides)
+    device = torch.device(device)
+    std = cfg.initializer_range
     torch.manual_seed(seed)
-    with torch.device(device):
+
+    def init_(module):
+        """transformers' initialization of one module's own parameters, rounded to fp16."""
+        with torch.no_grad():
+            if isinstance(module, (torch.nn.Linear, torch.nn.Embedding)):
+                module.weight.normal_(0.0, std)
+                if getattr(module, "bias", None) is not None:
+                    module.bias.zero_()
+            elif isinstance(module, Qwen2RMSNorm):
+                module.weight.fill_(1.0)
+            for p in module.parameters(recurse=False):
+                p.copy_(p.to(torch.float16))
+
+    with torch.device("meta"):
         model = Qwen2ForCausalLM(cfg)
-    model.requires_grad_(False)
-    # as a checkpoint loaded in fp16 and upcast for k-bit training: fp32 values that are fp16
-    # numbers (the tied embedding is then stored back in fp16 by the fused head, losslessly)
-    with torch.no_grad():
-        for p in model.parameters():
-            p.copy_(p.to(torch.float16))
-    for layer in model.model.layers:
-        for block_name, names in NF4_TARGETS:
-            block = getattr(layer, block_name)
-            for name in names:
-                lin = getattr(block, name)
-                out_dtype = torch.float32 if name in RESIDUAL_OUTPUTS else None
-                setattr(block, name, NF4Linear.from_weight(lin.weight, bias=lin.bias,
-                                                           out_dtype=out_dtype))
-                del lin
-        for name in LORA_TARGETS:
-            base = getattr(layer.self_attn, name)
-            with torch.device(device):
+    inner = model.model
+    with torch.device(device):
+        inner.embed_tokens = torch.nn.Embedding(cfg.vocab_size, cfg.hidden_size,
+                                                cfg.pad_token_id)
+        init_(inner.embed_tokens)
+        if cfg.pad_token_id is not None:
+            with torch.no_grad():
+                inner.embed_tokens.weight[cfg.pad_token_id].zero_()
+        inner.norm = Qwen2RMSNorm(cfg.hidden_size, eps=cfg.rms_norm_eps)
+        init_(inner.norm)
+        inner.rotary_emb = Qwen2RotaryEmbedding(config=cfg)
+        if cfg.tie_word_embeddings:
+            model.lm_head.weight = inner.embed_tokens.weight
+        else:
+            model.lm_head = torch.nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+            init_(model.lm_head)
+        for i in range(cfg.num_hidden_layers):
+            layer = Qwen2DecoderLayer(cfg, i)
+            for module in layer.modules():
+                init_(module)
+            layer.requires_grad_(False)
+            for block_name, names in NF4_TARGETS:
+                block = getattr(layer, block_name)
+                for name in names:
+                    lin = getattr(block, name)
+                    out_dtype = torch.float32 if name in RESIDUAL_OUTPUTS else None
+                    setattr(block, name, NF4Linear.from_weight(lin.weight, bias=lin.bias,
+                                                               out_dtype=out_dtype))
+                    del lin
+            for name in LORA_TARGETS:
+                base = getattr(layer.self_attn, name)
                 setattr(layer.self_attn, name, LoRALinear(base, r=r, alpha=alpha,
                                                           dropout=dropout))
+            inner.layers[i] = layer
+    left = [n for n, t in list(model.named_parameters()) + list(model.named_buffers())
+            if t.is_meta]
+    if left:
+        raise RuntimeError(f"build_model left tensors unmaterialized: {left[:4]}")
+    for n, p in model.named_parameters():
+        p.requires_grad_("lora_" in n)
     model.train()
-    if device != "cpu" and torch.device(device).type == "cuda":
+    if device.type == "cuda":
         torch.cuda.empty_cache()
     return model
 
@@ -300,6 +348,45 @@ def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, graphed
                 tokens_per_s=sum(tokens) / (sum(times) * 1e-3),
                 peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
                 peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30)
+
+
+class VramPoller:
+    """Device memory in use (MiB), sampled every `interval` s from a thread while the block runs,
+    as the reference's harness samples nvidia-smi's memory.used every 100 ms
+    (harness/common.py:48-85). The figure is device-level, total minus free
+    (torch.cuda.mem_get_info): every process on the device, the runtime's own allocations and
+    torch's cache, not only torch's allocated bytes (amd-smi on these boxes reports no per-device
+    use). `start` is the first sample, `peak` the largest."""
+
+    def __init__(self, device=None, interval=0.1):
+        self.device = torch.device("cuda", torch.cuda.current_device()) if device is None \
+            else torch.device(device)
+        self.interval, self.start, self.peak, self.samples = interval, None, 0.0, 0
+        self._stop = threading.Event()
+
+    def _used_mib(self):
+        free, total = torch.cuda.mem_get_info(self.device)
+        return (total - free) / 2 ** 20
+
+    def _run(self):
+        while not self._stop.is_set():
+            used = self._used_mib()
+            self.peak = max(self.peak, used)
+            self.samples += 1
+            self._stop.wait(self.interval)
+
+    def __enter__(self):
+        self.start = self._used_mib()
+        self.peak = self.start
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join(timeout=5)
+        self.peak = max(self.peak, self._used_mib())
+        return False
 
 
 @contextlib.contextmanager
