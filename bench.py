@@ -912,6 +912,7 @@ def qlora_step_bench(dev, steps, warmup=2):
 
     from claudemaxing_amd import qlora_step
 
+    torch.cuda.reset_peak_memory_stats()  # the kernel lines above are not the step's
     t0 = time.perf_counter()
     whole = qlora_step.VramPoller(dev).__enter__()  # the build and every step below
     model = qlora_step.build_model(dev, seed=0)
