@@ -22,6 +22,13 @@
 // feeds the next MFMA straight from registers, against a transposed operand tile read as one
 // 16-byte chunk per lane.
 //
+// The row bounds are a device-resident image (Rows, written by cm_attn_rows_image on the host and
+// copied to the device by the caller) and the grids are sized for a capacity of padded positions
+// given by the caller: blocks past the image's own padded count exit at once. One launch, or one
+// captured HIP graph, thus serves every packing whose padded count fits the capacity, the image
+// being rewritten before each replay. Every kernel checks the image against the capacity and the
+// token count it was launched for, and a workgroup whose row is inconsistent writes nothing.
+//
 // Forward, per (64-query block, head): S^T = K Q^T (lane = query, so the row statistics are
 // lane-local up to one shuffle between the two lane halves), online softmax in the log2 domain,
 // O^T += V^T P^T. The log2-domain log-sum-exp of every position is kept for the backward.
@@ -30,6 +37,8 @@
 // partials and summed over the heads of each key/value group by a last pass (no atomics: the
 // results are the same bits on every run); per (64-query block, head) S^T and dP^T again and
 // dQ^T += K^T dS^T.
+#include <cstring>
+
 #include "common.h"
 #include "gemm_lds.h"
 
@@ -55,6 +64,21 @@ __device__ __forceinline__ int row_of_block(const Rows& rows, int b) {
   int r = 0;
   while (r + 1 < rows.n && rows.pstart[r + 1] / kBlk <= b) ++r;
   return r;
+}
+
+// Whether padded block b of a launch for n_tokens tokens and n_pad padded positions has work:
+// the image is consistent with the launch (a row count the struct holds, n_tokens tokens, a
+// padded count within n_pad) and b lies inside its padded positions, in a row whose real tokens
+// fit its padded blocks. Uniform over the workgroup (scalar loads of the image).
+__device__ __forceinline__ bool block_live(const Rows& rows, int b, int n_tokens, int n_pad) {
+  const int n = rows.n;
+  if (n < 1 || n > kMaxRows || rows.start[n] != n_tokens || rows.pstart[n] > n_pad ||
+      b * kBlk >= rows.pstart[n])
+    return false;
+  const int r = row_of_block(rows, b);
+  const int len = rows.start[r + 1] - rows.start[r];
+  return len >= 0 && rows.start[r] >= 0 && len <= rows.pstart[r + 1] - rows.pstart[r] &&
+         rows.pstart[r] % kBlk == 0 && rows.start[r + 1] <= n_tokens;
 }
 
 // Stored slot of position p inside its 16-group (an involution: bits 2 and 3 swapped).
@@ -164,8 +188,11 @@ struct Jobs {
   int n;
 };
 
-__global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, Rows rows, int n_pad) {
+__global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Rows* rows_p,
+                                                            int n_tokens, int n_pad) {
   __shared__ _Float16 tile[kD * kBlk];  // transposed staging [d][slot]
+  const Rows& rows = *rows_p;
+  if (!block_live(rows, blockIdx.x, n_tokens, n_pad)) return;
   const int y = blockIdx.y;
   // the job of this blockIdx.y, selected with static indices only
   Job job = jobs.job[0];
@@ -236,12 +263,15 @@ constexpr int kVTile = kD * (kBlk / 8);   // V^T tile: 128 d x 8 chunks
 
 __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
     const void* __restrict__ q, int q_dtype, int64_t sq_h, int64_t sq_t,
-    const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16, Rows rows, int n_pad,
-    int hpg, int H, float c_log2, _Float16* __restrict__ out, float* __restrict__ lse2) {
+    const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
+    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, int H, float c_log2,
+    _Float16* __restrict__ out, float* __restrict__ lse2) {
   constexpr int kStage = kKTile + kVTile;
   __shared__ uint4 lds[2][2][kStage];  // [pair][stage]
+  const Rows& rows = *rows_p;
   const int h = blockIdx.y, g = h / hpg;
   const int b = blockIdx.x;
+  if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
   const int len = rows.start[r + 1] - rows.start[r];
@@ -387,14 +417,16 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
     const _Float16* __restrict__ q16, const _Float16* __restrict__ qt16,
     const _Float16* __restrict__ do16, const _Float16* __restrict__ dot16,
     const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
-    const float* __restrict__ lse2, const float* __restrict__ delta, Rows rows, int n_pad,
-    int hpg, float c_log2, float scale, float* __restrict__ dk_part,
-    float* __restrict__ dv_part) {
+    const float* __restrict__ lse2, const float* __restrict__ delta,
+    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, float c_log2, float scale,
+    float* __restrict__ dk_part, float* __restrict__ dv_part) {
   constexpr int kVec = 2 * kQTile + 2 * kQTTile;  // lse (8 chunks) and Delta (8) follow the tiles
   constexpr int kStage = kVec + 16;
   __shared__ uint4 lds[2][2][kStage];
+  const Rows& rows = *rows_p;
   const int h = blockIdx.y, g = h / hpg;
   const int b = blockIdx.x;
+  if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int kb = b - rows.pstart[r] / kBlk;
   const int len = rows.start[r + 1] - rows.start[r];
@@ -533,12 +565,14 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     const _Float16* __restrict__ q16, const _Float16* __restrict__ do16,
     const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
     const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
-    const float* __restrict__ delta, Rows rows, int n_pad, int hpg, float c_log2, float scale,
-    OT* __restrict__ dq, int tok_major) {
+    const float* __restrict__ delta, const Rows* __restrict__ rows_p, int n_tokens, int n_pad,
+    int hpg, float c_log2, float scale, OT* __restrict__ dq, int tok_major) {
   constexpr int kStage = 2 * kKVTile + kKTTile;
   __shared__ uint4 lds[2][2][kStage];
+  const Rows& rows = *rows_p;
   const int h = blockIdx.y, g = h / hpg;
   const int b = blockIdx.x;
+  if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
   const int len = rows.start[r + 1] - rows.start[r];
@@ -617,7 +651,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   // dq is [H][N][D], or [N][H][D] with tok_major
   const int64_t tok = rows.start[r] + ql;
   OT* row = dq + (tok_major ? tok * gridDim.y + h
-                            : static_cast<int64_t>(h) * rows.start[rows.n] + tok) * kD;
+                            : static_cast<int64_t>(h) * n_tokens + tok) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -631,12 +665,14 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
 // Thread (position, 4 values of d) of key/value head blockIdx.y.
 template <typename OT>
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
-    const float* __restrict__ dk_part, const float* __restrict__ dv_part, Rows rows, int n_pad,
-    int hpg, OT* __restrict__ dk, OT* __restrict__ dv, int tok_major) {
+    const float* __restrict__ dk_part, const float* __restrict__ dv_part,
+    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, OT* __restrict__ dk,
+    OT* __restrict__ dv, int tok_major) {
+  const Rows& rows = *rows_p;
   const int g = blockIdx.y;
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int pos = i / (kD / 4), d = (i % (kD / 4)) * 4;
-  if (pos >= n_pad) return;
+  if (pos >= n_pad || !block_live(rows, pos / kBlk, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, pos / kBlk);
   const int local = pos - rows.pstart[r];
   if (local >= rows.start[r + 1] - rows.start[r]) return;
@@ -651,7 +687,7 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
   // dK, dV are [G][N][D], or [N][G][D] with tok_major
   const int64_t tok = rows.start[r] + local;
   const int64_t o =
-      (tok_major ? tok * gridDim.y + g : static_cast<int64_t>(g) * rows.start[rows.n] + tok) * kD +
+      (tok_major ? tok * gridDim.y + g : static_cast<int64_t>(g) * n_tokens + tok) * kD +
       d;
   dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
   dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
@@ -715,24 +751,40 @@ extern "C" int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows) {
   return n_pad;
 }
 
+extern "C" int64_t cm_attn_rows_bytes(void) { return static_cast<int64_t>(sizeof(Rows)); }
+
+extern "C" int64_t cm_attn_rows_image(const int64_t* bounds, int n_rows, void* image) {
+  Rows rows;
+  int64_t n_pad;
+  if (!image || build_rows(bounds, n_rows, rows, n_pad)) return -1;
+  memcpy(image, &rows, sizeof(Rows));
+  return n_pad;
+}
+
 extern "C" int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim,
                                            int backward) {
   if (n_pad < 0 || H <= 0 || G <= 0 || head_dim != kD) return -1;
   return static_cast<int64_t>(backward ? bwd_ws_bytes(n_pad, H, G) : fwd_ws_bytes(n_pad, G));
 }
 
+// Launch arguments shared by both directions: the rows image (device memory, 16-byte aligned), the
+// token count and a padded capacity that is a positive multiple of the block.
+bool rows_args_ok(const void* rows, int64_t n_tokens, int64_t n_pad) {
+  return rows && (reinterpret_cast<uintptr_t>(rows) & 15) == 0 && n_tokens >= 0 &&
+         n_tokens <= 0x3fffffff && n_pad > 0 && n_pad % kBlk == 0 && n_pad <= 0x3fffffff &&
+         n_pad / kBlk <= 0x7fffffff;
+}
+
 extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
                            int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
-                           int64_t sv_h, int64_t sv_t, const int64_t* bounds, int n_rows, int H,
-                           int G, int head_dim, float scale, void* out, float* lse2,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
-  Rows rows;
-  int64_t n_pad;
-  CM_CHECK_ARG(build_rows(bounds, n_rows, rows, n_pad) == 0);
+                           int64_t sv_h, int64_t sv_t, const void* rows_image, int64_t n_tokens,
+                           int64_t n_pad, int H, int G, int head_dim, float scale, void* out,
+                           float* lse2, void* workspace, int64_t workspace_bytes, void* stream) {
   CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
   CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
                (v_dtype == CM_F32 || v_dtype == CM_F16));
-  if (rows.start[n_rows] == 0) return 0;
+  if (n_tokens == 0) return 0;
+  CM_CHECK_ARG(rows_args_ok(rows_image, n_tokens, n_pad));
   CM_CHECK_ARG(q && k && v && out && lse2 && workspace);
   CM_CHECK_ARG(aligned_operand(q, q_dtype, sq_h, sq_t) && aligned_operand(k, k_dtype, sk_h, sk_t) &&
                aligned_operand(v, v_dtype, sv_h, sv_t));
@@ -749,31 +801,32 @@ extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   jobs.first[1] = G;
   jobs.n = 2;
   const int n_blocks = static_cast<int>(n_pad / kBlk);
+  const Rows* rows = static_cast<const Rows*>(rows_image);
+  const int nt = static_cast<int>(n_tokens), np = static_cast<int>(n_pad);
   hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * G), dim3(256), 0, s, jobs, rows,
-                     static_cast<int>(n_pad));
+                     nt, np);
   if (int st = cm::launch_status()) return st;
   hipLaunchKernelGGL(attn_fwd_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q, q_dtype, sq_h,
-                     sq_t, k16, vt16, rows, static_cast<int>(n_pad), H / G, H,
-                     scale * 1.4426950408889634f, static_cast<_Float16*>(out), lse2);
+                     sq_t, k16, vt16, rows, nt, np, H / G, H, scale * 1.4426950408889634f,
+                     static_cast<_Float16*>(out), lse2);
   return cm::launch_status();
 }
 
 extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
                            int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
                            int64_t sv_h, int64_t sv_t, const void* out, const void* dout,
-                           const float* lse2, const int64_t* bounds, int n_rows, int H, int G,
-                           int head_dim, float scale, void* dq, int dq_dtype, void* dk,
-                           void* dv, int dkv_dtype, int grads_token_major, void* workspace,
-                           int64_t workspace_bytes, void* stream) {
-  Rows rows;
-  int64_t n_pad;
-  CM_CHECK_ARG(build_rows(bounds, n_rows, rows, n_pad) == 0);
+                           const float* lse2, const void* rows_image, int64_t n_tokens,
+                           int64_t n_pad, int H, int G, int head_dim, float scale, void* dq,
+                           int dq_dtype, void* dk, void* dv, int dkv_dtype,
+                           int grads_token_major, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
   CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
   CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
                (v_dtype == CM_F32 || v_dtype == CM_F16));
   CM_CHECK_ARG((dq_dtype == CM_F32 || dq_dtype == CM_F16) &&
                (dkv_dtype == CM_F32 || dkv_dtype == CM_F16));
-  if (rows.start[n_rows] == 0) return 0;
+  if (n_tokens == 0) return 0;
+  CM_CHECK_ARG(rows_args_ok(rows_image, n_tokens, n_pad));
   CM_CHECK_ARG(q && k && v && out && dout && lse2 && dq && dk && dv && workspace);
   CM_CHECK_ARG(aligned_operand(q, q_dtype, sq_h, sq_t) && aligned_operand(k, k_dtype, sk_h, sk_t) &&
                aligned_operand(v, v_dtype, sv_h, sv_t));
@@ -795,8 +848,9 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   float* delta = ws.take<float>(static_cast<size_t>(H) * n_pad);
   float* dk_part = ws.take<float>(nq);
   float* dv_part = ws.take<float>(nq);
-  const int np = static_cast<int>(n_pad);
+  const int np = static_cast<int>(n_pad), nt = static_cast<int>(n_tokens);
   const int n_blocks = np / kBlk;
+  const Rows* rows = static_cast<const Rows*>(rows_image);
   // dO and O: [N][H][D] contiguous (the forward's output layout)
   Jobs jobs{};
   jobs.job[0] = Job{q, sq_h, sq_t, q16, qt16, nullptr, nullptr, 0, q_dtype, H};
@@ -810,30 +864,30 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   jobs.first[3] = 2 * H + G;
   jobs.n = 4;
   hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * H + 2 * G), dim3(256), 0, s, jobs,
-                     rows, np);
+                     rows, nt, np);
   if (int st = cm::launch_status()) return st;
   const float c_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q16, qt16,
-                     do16, dot16, k16, v16, lse2, delta, rows, np, H / G, c_log2, scale, dk_part,
-                     dv_part);
+                     do16, dot16, k16, v16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
+                     dk_part, dv_part);
   if (int st = cm::launch_status()) return st;
   if (dq_dtype == CM_F32) {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(n_blocks, H), dim3(kThreads), 0, s, q16,
-                       do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
+                       do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                        static_cast<float*>(dq), grads_token_major ? 1 : 0);
   } else {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(n_blocks, H), dim3(kThreads), 0, s,
-                       q16, do16, k16, v16, kt16, lse2, delta, rows, np, H / G, c_log2, scale,
+                       q16, do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                        static_cast<_Float16*>(dq), grads_token_major ? 1 : 0);
   }
   if (int st = cm::launch_status()) return st;
   if (dkv_dtype == CM_F32) {
     hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(np / 8, G), dim3(256), 0, s,
-                       dk_part, dv_part, rows, np, H / G, static_cast<float*>(dk),
+                       dk_part, dv_part, rows, nt, np, H / G, static_cast<float*>(dk),
                        static_cast<float*>(dv), grads_token_major ? 1 : 0);
   } else {
     hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(np / 8, G), dim3(256), 0, s,
-                       dk_part, dv_part, rows, np, H / G, static_cast<_Float16*>(dk),
+                       dk_part, dv_part, rows, nt, np, H / G, static_cast<_Float16*>(dk),
                        static_cast<_Float16*>(dv), grads_token_major ? 1 : 0);
   }
   return cm::launch_status();

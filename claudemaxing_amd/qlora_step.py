@@ -260,7 +260,7 @@ class GraphedStep:
                       use_cache=False)
         packed = _pack_batch(self.model, kwargs, batch["labels"])
         if (packed is None or packed.ids.shape != self.packed.ids.shape
-                or packed_rows(packed.mask) != packed_rows(self.packed.mask)):
+                or packed_rows(packed.mask).bounds != packed_rows(self.packed.mask).bounds):
             # the row structure matters to the opt-in packed-row attention, baked into a capture
             raise ValueError("the batch packs to another shape: capture a new GraphedStep")
         for name in ("ids", "pos", "mask", "target", "index"):

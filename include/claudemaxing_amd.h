@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 2
+#define CM_ABI_VERSION 3
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -276,19 +276,25 @@ int cm_lmhead_ce_noalloc_plan(int64_t n_rows, int64_t vocab, int hidden_size, in
  * are rounded to fp16 (as fp16 autocast rounds them); fp16 MFMA products, fp32 accumulation and
  * softmax. out fp16 [N][H][D] contiguous. lse2 f32 [H][n_pad] receives the log2-domain
  * log-sum-exp of scale * q.k of every padded position (the backward's input).
- * bounds: HOST array of n_rows + 1 row boundaries (0 = bounds[0] <= ... <= bounds[n_rows] = N),
- * n_rows <= 128. n_pad = cm_attn_padded_tokens(bounds, n_rows) (rows padded to multiples of 64).
+ * rows_image: DEVICE memory (16-byte aligned) holding cm_attn_rows_bytes() bytes that
+ * cm_attn_rows_image wrote for the batch's row bounds (its token count must be n_tokens = N),
+ * copied there by the caller. n_pad: the padded positions the launch is sized for, a multiple of
+ * 64 at least the image's padded count (cm_attn_padded_tokens of its bounds): blocks past the
+ * image's own count do nothing, so one launch (or one captured graph) sized for a capacity serves
+ * every row structure of N tokens that fits it, the image being rewritten in between. Kernels
+ * check the image against n_tokens and n_pad, and write nothing for rows inconsistent with them.
  * head_dim must be 128, H a multiple of G. Bases 16-byte aligned (out 8), strides multiples of 8
  * (f16) or 4 (f32) elements, workspace 256-byte aligned, cm_attn_workspace_bytes(n_pad, H, G,
  * head_dim, 0) bytes.
  */
 int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
                 int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
-                int64_t sv_h, int64_t sv_t, const int64_t* bounds, int n_rows, int H, int G,
-                int head_dim, float scale, void* out, float* lse2, void* workspace,
-                int64_t workspace_bytes, void* stream);
+                int64_t sv_h, int64_t sv_t, const void* rows_image, int64_t n_tokens,
+                int64_t n_pad, int H, int G, int head_dim, float scale, void* out, float* lse2,
+                void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Backward of cm_attn_fwd (the same q, k, v, bounds and scale; out and lse2 as it wrote them;
+/* Backward of cm_attn_fwd (the same q, k, v, rows image, n_tokens, n_pad and scale; out and lse2
+ * as it wrote them;
  * dout fp16 [N][H][D] contiguous). Writes dq [H][N][D] (dq_dtype), dk and dv [G][N][D]
  * (dkv_dtype), contiguous; f32 or f16; with grads_token_major != 0 they are [N][H][D] and
  * [N][G][D] instead (the layout of the projections the gradients flow back into). dk and dv
@@ -299,13 +305,22 @@ int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const vo
 int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
                 int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
                 int64_t sv_h, int64_t sv_t, const void* out, const void* dout, const float* lse2,
-                const int64_t* bounds, int n_rows, int H, int G, int head_dim, float scale,
-                void* dq, int dq_dtype, void* dk, void* dv, int dkv_dtype,
-                int grads_token_major, void* workspace, int64_t workspace_bytes, void* stream);
+                const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G,
+                int head_dim, float scale, void* dq, int dq_dtype, void* dk, void* dv,
+                int dkv_dtype, int grads_token_major, void* workspace, int64_t workspace_bytes,
+                void* stream);
 
 /* Padded token count of a packed batch: sum over rows of round_up(length, 64); -1 for invalid
  * bounds (not monotone, bounds[0] != 0, n_rows outside 1..128). */
 int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows);
+
+/* The row bounds as the attention kernels read them: bounds (HOST array of n_rows + 1 row ends,
+ * 0 = bounds[0] <= ... <= bounds[n_rows] = N, n_rows <= 128) written as an image of
+ * cm_attn_rows_bytes() bytes to the HOST buffer `image`, for the caller to copy to device memory.
+ * Returns the padded token count (cm_attn_padded_tokens), or -1 for invalid bounds. No counterpart
+ * in the reference, whose mask carries the rows (lm_head_loss.py:332-336). */
+int64_t cm_attn_rows_bytes(void);
+int64_t cm_attn_rows_image(const int64_t* bounds, int n_rows, void* image);
 
 /* Workspace bytes of cm_attn_fwd (backward = 0) or cm_attn_bwd (backward = 1); -1 if the sizes
  * are unsupported. */

@@ -38,12 +38,12 @@ def _bounds(lengths):
 
 
 def _packed_mask(lengths, dev):
-    from claudemaxing_amd.attention import ROWS_ATTR
+    from claudemaxing_amd.attention import ROWS_ATTR, PackedRows
 
     row = torch.cat([torch.full((n,), i) for i, n in enumerate(lengths)]).to(dev)
     col = torch.cat([torch.arange(n) for n in lengths]).to(dev)
     mask = ((row[:, None] == row[None, :]) & (col[None, :] <= col[:, None]))[None, None]
-    setattr(mask, ROWS_ATTR, _bounds(lengths))
+    setattr(mask, ROWS_ATTR, PackedRows(_bounds(lengths)))
     return mask
 
 
@@ -282,7 +282,7 @@ def test_pack_batch_records_rows(dev):
     lm = SimpleNamespace(lm_head=head, config=SimpleNamespace(_attn_implementation="sdpa"))
     packed = _pack_batch(lm, dict(input_ids=batch["input_ids"],
                                   attention_mask=batch["attention_mask"]), batch["labels"])
-    bounds = packed_rows(packed.mask)
+    bounds = packed_rows(packed.mask).bounds
     assert bounds == tuple([0] + torch.cumsum(lengths, 0).tolist())
     # the recorded rows are exactly the blocks of the mask
     m = packed.mask[0, 0].cpu()
