@@ -930,8 +930,14 @@ def qlora_step_bench(dev, steps, warmup=2):
         rd = qlora_step.time_distinct_batches(model, opt, scaler, steps, warmup)
     r = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup)
     rdg = qlora_step.time_distinct_batches(model, opt, scaler, max(3, steps // 3), 1,
-                                           graphed=True)
+                                           mode="capture_each")
     rg = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup, graphed=True)
+    # the SFT figure: fresh batches every step, each replayed from its 256-token bucket's graph
+    # (the first batch of a bucket captures it inside its timed step), TRL's metrics every step
+    torch.cuda.empty_cache()
+    with qlora_step.VramPoller(dev) as vram_b:
+        rb = qlora_step.time_distinct_batches(model, opt, scaler, 3 * steps, 2, seed0=5000,
+                                              mode="bucketed", bucket=256)
     tokens = int(lengths.sum())
     out = dict(config="Qwen2.5-1.5B shape, 28 layers, NF4 + LoRA r16 q/v, batch 4 of U[64,512] "
                       "tokens packed out, fp16 autocast, AdamW + GradScaler",
@@ -951,7 +957,24 @@ def qlora_step_bench(dev, steps, warmup=2):
                                "before this process allocated anything; the reference publishes "
                                "2447 / 2696 MiB allocated / reserved and a 2839 MiB nvidia-smi "
                                "peak (T4, EXPERIMENTS.md run 5)",
-                   note="eager, a new batch every step (the headline step figure)",
+                   note="eager, a new batch every step",
+                   bucketed_graphs=dict(
+                       median_ms=round(rb["median_ms"], 2), mean_ms=round(rb["mean_ms"], 2),
+                       step_ms=[round(x, 2) for x in rb["step_ms"]], tokens=rb["tokens"],
+                       tokens_per_s=round(rb["tokens_per_s"], 1),
+                       captures_timed=rb["captures_timed"],
+                       capture_ms=[round(x, 1) for x in rb["capture_ms"]],
+                       buckets=rb["buckets"], graph_pool_gb=round(rb["graph_pool_gb"], 3),
+                       peak_allocated_gb=round(rb["peak_allocated_gb"], 3),
+                       peak_reserved_gb=round(rb["peak_reserved_gb"], 3),
+                       device_used_peak_mib=round(vram_b.peak),
+                       device_used_peak_over_start_mib=round(vram_b.peak - whole.start),
+                       note="the step an SFT run sees: a new batch every step, packed to the "
+                            "next multiple of 256 tokens (a filler row with ignored labels) and "
+                            "replayed from that bucket's HIP graph; a bucket's first batch "
+                            "captures its graph inside the timed step (captures_timed of them, "
+                            "capture_ms each); graphs share one memory pool; TRL's three "
+                            "metrics every step"),
                    graphed_with_capture=dict(
                        median_ms=round(rdg["median_ms"], 2),
                        step_ms=[round(x, 2) for x in rdg["step_ms"]],

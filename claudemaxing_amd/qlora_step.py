@@ -33,7 +33,7 @@ import torch
 from . import apply
 from .attention import packed_rows
 from .embedding import shrink_tied_embedding
-from .lm_head_loss import (_REQUEST_ATTR, _STEP_ATTR, _pack_batch, _packed_forward,
+from .lm_head_loss import (_REQUEST_ATTR, _STEP_ATTR, HeadTerms, _pack_batch, _packed_forward,
                            head_metrics_from_logits, trl_metrics)
 from .lora import LoRALinear
 from .nf4_linear import NF4Linear
@@ -215,24 +215,27 @@ class GraphedStep:
 
     What stays outside the graph, because it synchronises with the host: packing the batch
     (`_pack_batch` reads the number of real tokens), and the GradScaler step (its inf check) with
-    AdamW. The graph is captured for one packed batch; `load` copies another batch of the same
-    packed shape into its inputs. The gradients live in the graph's buffers: they are
-    overwritten by each replay and must not be set to None. Nothing in the captured region
+    AdamW. The graph is captured for one packed shape; `load` copies another batch of that
+    packed shape into its inputs: with `bucket`, every batch whose real tokens round up to the
+    same multiple of the bucket (the packed batch's filler row makes up the rest, and the
+    attention reads its rows from the device image `load` rewrites), else the same row lengths.
+    The gradients live in the graph's buffers: they are overwritten by each replay, and `step`
+    points the LoRA parameters at them before the optimizer step. Nothing in the captured region
     allocates outside torch's graph pool or synchronises (the kernel library never does; the
     RMSNorm tiny-column map is computed in the warm-up), and LoRA dropout draws from torch's
-    graph-safe generator, so every replay has fresh masks."""
+    graph-safe generator, so every replay has fresh masks. Graphs given one `pool` share its
+    memory for their activations (replayed one at a time, never concurrently)."""
 
-    def __init__(self, model, opt, scaler, batch, warmup=3):
+    def __init__(self, model, opt, scaler, batch, warmup=3, bucket=None, pool=None):
         self.model, self.opt, self.scaler = model, opt, scaler
         self.params = lora_parameters(model)
+        self.bucket = bucket
         with torch.autocast("cuda", dtype=torch.float16):
             shrink_tied_embedding(model)  # as the fused head's forward does
-        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
-                      use_cache=False)
-        self.packed = _pack_batch(model, kwargs, batch["labels"])
-        if self.packed is None:
-            raise ValueError("GraphedStep needs a padded batch with pads to pack out")
-        side = _capture_stream(next(model.parameters()).device)
+        self.packed = self._pack(batch)
+        device = next(model.parameters()).device
+        self.packed.rows.image_on(device)  # the rows' device image, made before the capture
+        side = _capture_stream(device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(warmup):
@@ -241,8 +244,18 @@ class GraphedStep:
         torch.cuda.current_stream().wait_stream(side)
         self._zero()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
+        with torch.cuda.graph(self.graph, pool=pool, stream=side):
             self.loss = self._forward_backward()
+        self.terms = model.__dict__.pop(_STEP_ATTR, None)  # packed per-token terms, [1, N]
+        self.grads = [p.grad for p in self.params]
+
+    def _pack(self, batch):
+        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                      use_cache=False)
+        packed = _pack_batch(self.model, kwargs, batch["labels"], bucket=self.bucket)
+        if packed is None:
+            raise ValueError("GraphedStep needs a padded batch with pads to pack out")
+        return packed
 
     def _zero(self):
         for p in self.params:
@@ -250,21 +263,22 @@ class GraphedStep:
 
     def _forward_backward(self):
         with torch.autocast("cuda", dtype=torch.float16):
-            out = _packed_forward(self.model, dict(use_cache=False), self.packed)
+            out = _packed_forward(self.model, dict(use_cache=False), self.packed, unpack=False)
         self.scaler.scale(out.loss).backward()
         return out.loss.detach()
 
-    def load(self, batch):
-        """Copy a batch with the same packed shape into the graph's inputs."""
-        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
-                      use_cache=False)
-        packed = _pack_batch(self.model, kwargs, batch["labels"])
-        if (packed is None or packed.ids.shape != self.packed.ids.shape
-                or packed_rows(packed.mask).bounds != packed_rows(self.packed.mask).bounds):
-            # the row structure matters to the opt-in packed-row attention, baked into a capture
+    def load(self, batch, packed=None):
+        """Copy a batch with this graph's packed shape into the graph's inputs (`packed`: the
+        batch already packed for this graph's bucket)."""
+        packed = packed if packed is not None else self._pack(batch)
+        if packed.ids.shape != self.packed.ids.shape or (
+                self.bucket is None and packed.rows.bounds != self.packed.rows.bounds):
+            # without a bucket, the rows' capacity is their own padded count: same rows only
             raise ValueError("the batch packs to another shape: capture a new GraphedStep")
-        for name in ("ids", "pos", "mask", "target", "index"):
+        self.packed.rows.load(packed.rows.bounds)
+        for name in ("ids", "pos", "mask", "target"):
             getattr(self.packed, name).copy_(getattr(packed, name))
+        self.packed.B, self.packed.T, self.packed.index = packed.B, packed.T, packed.index
 
     def pool_bytes(self):
         """Bytes of the segments of the graph's private memory pool: the activations and
@@ -274,12 +288,65 @@ class GraphedStep:
         return sum(seg["total_size"] for seg in torch.cuda.memory_snapshot()
                    if tuple(seg.get("segment_pool_id", ())) == pool)
 
-    def step(self):
-        """Replay forward + backward, then the GradScaler step with AdamW; the loss tensor."""
+    def step(self, metrics=None, inputs=None):
+        """Replay forward + backward, then the GradScaler step with AdamW; the loss tensor. With
+        a `metrics` dict (and the batch as `inputs`), TRL's three metrics of the loaded batch
+        are filled in from the replay's per-token terms."""
         self.graph.replay()
+        if metrics is not None:
+            p = self.packed
+            terms = HeadTerms(p.unpack(self.terms.token_loss), p.unpack(self.terms.token_entropy),
+                              self.terms.correct, self.terms.labelled)
+            metrics.update(trl_metrics(terms, inputs))
+        for p, g in zip(self.params, self.grads):
+            p.grad = g
         self.scaler.step(self.opt)
         self.scaler.update()
         return self.loss.clone()
+
+
+class BucketedGraphSteps:
+    """Training steps over batches of any packed length, each replayed from a captured HIP
+    graph: a batch's real tokens are packed to the next multiple of `bucket` (a filler row with
+    ignored labels), and the first batch of each bucket captures that bucket's GraphedStep
+    (then ~70-150 ms); later batches of the bucket only load their tokens and rows into it. The
+    graphs share one memory pool, so the activations take the largest bucket's, not the sum.
+    Only the first capture runs eager warm-up passes (the lazy state they set up: BLAS handles
+    and workspaces, the RMSNorm tiny-column maps, the NF4 descriptors, is shared by every
+    bucket), so later captures add no eager activations beside the pool."""
+
+    def __init__(self, model, opt, scaler, bucket=256, warmup=1):
+        self.model, self.opt, self.scaler = model, opt, scaler
+        self.bucket, self.warmup = bucket, warmup
+        self.graphs = {}
+        self.pool = torch.cuda.graph_pool_handle()
+        self.capture_ms = []
+
+    def step(self, batch, metrics=None):
+        kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                      use_cache=False)
+        packed = _pack_batch(self.model, kwargs, batch["labels"], bucket=self.bucket)
+        if packed is None:
+            raise ValueError("BucketedGraphSteps needs padded batches with pads to pack out")
+        total = packed.ids.shape[1]
+        g = self.graphs.get(total)
+        if g is None:
+            t0 = time.perf_counter()
+            g = self.graphs[total] = GraphedStep(
+                self.model, self.opt, self.scaler, batch,
+                warmup=0 if self.capture_ms else self.warmup, bucket=self.bucket,
+                pool=self.pool)
+            torch.cuda.empty_cache()  # the warm-up's eager blocks outside the graph pool
+            self.capture_ms.append((time.perf_counter() - t0) * 1e3)
+        else:
+            g.load(batch, packed)
+        return g.step(metrics, batch)
+
+    def pool_bytes(self):
+        """Bytes of the shared graph pool's segments."""
+        if not self.graphs:
+            return 0
+        return next(iter(self.graphs.values())).pool_bytes()
 
 
 def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
@@ -315,25 +382,36 @@ def time_steps(model, opt, scaler, batch, steps, warmup, graphed=False):
     return out
 
 
-def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, graphed=False):
+def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, mode="eager",
+                          bucket=256):
     """Per-step wall times (ms) over a fresh batch every step (new U[64, 512] lengths, so the
     packed shape changes every step, as in SFT), each step between two device syncs, with TRL's
-    three metrics computed every step as its compute_loss does. With graphed, every step
-    captures a new GraphedStep for its batch and replays it once: the capture (and its warm-up
-    passes) is inside the timed step. Returns the median, the times, the real tokens per step
-    and the peak HBM."""
+    three metrics computed every step as its compute_loss does. mode: "eager"; "capture_each"
+    (every step captures a new GraphedStep for its batch and replays it once); "bucketed"
+    (BucketedGraphSteps: a step replays its bucket's graph, and the first batch of a bucket
+    captures it, inside the timed step). Returns the median, the times, the real tokens per
+    step, the peak HBM, and for "bucketed" the captures made while timing and the graph pool's
+    size."""
     def batch_of(i):
         return make_batch(next(model.parameters()).device, seed=seed0 + i)
 
+    runner = BucketedGraphSteps(model, opt, scaler, bucket) if mode == "bucketed" else None
+
     def run(batch):
-        if graphed:
-            return GraphedStep(model, opt, scaler, batch, warmup=1).step()
+        if mode == "capture_each":
+            return GraphedStep(model, opt, scaler, batch, warmup=1).step(metrics={},
+                                                                         inputs=batch)
+        if mode == "bucketed":
+            return runner.step(batch, metrics={})
+        if mode != "eager":
+            raise ValueError(f"unknown mode {mode!r}")
         return train_step(model, opt, scaler, batch, metrics={})
 
     for i in range(warmup):
         run(batch_of(i)[0])
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
+    captured_before = len(runner.capture_ms) if runner else 0
     times, tokens = [], []
     for i in range(steps):
         batch, lengths = batch_of(warmup + i)
@@ -344,10 +422,15 @@ def time_distinct_batches(model, opt, scaler, steps, warmup, seed0=1000, graphed
         times.append((time.perf_counter() - t0) * 1e3)
         tokens.append(int(lengths.sum()))
     ordered = sorted(times)
-    return dict(median_ms=ordered[len(ordered) // 2], step_ms=times, tokens=tokens,
-                tokens_per_s=sum(tokens) / (sum(times) * 1e-3),
-                peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
-                peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30)
+    out = dict(median_ms=ordered[len(ordered) // 2], mean_ms=sum(times) / len(times),
+               step_ms=times, tokens=tokens, tokens_per_s=sum(tokens) / (sum(times) * 1e-3),
+               peak_allocated_gb=torch.cuda.max_memory_allocated() / 2 ** 30,
+               peak_reserved_gb=torch.cuda.max_memory_reserved() / 2 ** 30)
+    if runner is not None:
+        out.update(captures_timed=len(runner.capture_ms) - captured_before,
+                   capture_ms=runner.capture_ms[captured_before:],
+                   buckets=sorted(runner.graphs), graph_pool_gb=runner.pool_bytes() / 2 ** 30)
+    return out
 
 
 class VramPoller:

@@ -300,3 +300,103 @@ def test_training_curve_matches_stock(dev):
     assert first <= 0.01
     assert all(v <= 0.03 for v in gaps.values()), gaps
     assert 0.2 < stock_c[0]["mean_token_accuracy"] < 0.95  # the labels are learnable, not noise
+
+
+def _eager_metrics(model, batch):
+    """TRL's three metrics of the eager fused forward on `batch` (packed without a bucket)."""
+    from claudemaxing_amd.lm_head_loss import _STEP_ATTR, trl_metrics
+
+    model.__dict__[qlora_step._REQUEST_ATTR] = True
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        model(**batch, use_cache=False)
+    model.__dict__.pop(qlora_step._REQUEST_ATTR, None)
+    return trl_metrics(model.__dict__.pop(_STEP_ATTR), batch)
+
+
+def _eager_scaled(model, batch, bucket, scale):
+    """Loss and LoRA gradients of the eager fused step on `batch` (packed to `bucket`, or without
+    filler when None), backpropagated at the loss scale `scale` as the GradScaler does and then
+    unscaled (a power of two: exact): small fp16 gradients keep their precision, as in
+    training."""
+    from claudemaxing_amd.lm_head_loss import _pack_batch, _packed_forward
+
+    model.zero_grad(set_to_none=True)
+    kwargs = dict(input_ids=batch["input_ids"], attention_mask=batch["attention_mask"],
+                  use_cache=False)
+    packed = _pack_batch(model, kwargs, batch["labels"], bucket=bucket)
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = _packed_forward(model, dict(use_cache=False), packed)
+    (out.loss * scale).backward()
+    return float(out.loss.detach()), [p.grad.detach().float() / scale
+                                      for p in qlora_step.lora_parameters(model)]
+
+
+@pytest.mark.gpu
+def test_bucketed_graph_matches_eager_unpadded(dev):
+    """One graph captured for a 256-token bucket replays five distinct batches of that bucket
+    (each packed with a filler row of ignored labels up to the bucket, its rows loaded into the
+    attention's device image), dropout off:
+      * each replay gives the bits of the eager step on the same bucketed packing (loss and
+        every LoRA gradient): loading a batch into the graph is exact;
+      * against the eager step on the batch packed without filler, the loss agrees to 1e-4
+        relative and the gradients to 2e-2 of their largest entry (the filler changes the token
+        count, so GEMM routes, tilings and split-K slicing, and with them fp32 summation orders
+        and fp16 rounding points, as between the fused and the stock step), and TRL's metrics
+        agree, num_tokens exactly (the batch's own token count).
+    Then batches of two other buckets run through BucketedGraphSteps (one shared pool, one
+    capture per bucket)."""
+    banner("qlora step: bucketed graph vs eager, 2 layers, 5 batches")
+    model = qlora_step.build_model(dev, seed=0, dropout=0.0, **TWO_LAYERS)
+    params = qlora_step.lora_parameters(model)
+    names = [n for n, p in model.named_parameters() if p.requires_grad]
+    opt = torch.optim.SGD(params, lr=0.0)  # the weights stay put between comparisons
+    scaler = torch.amp.GradScaler("cuda")
+    bucket, batches, total0 = 256, [], None
+    for seed in range(100, 600):
+        b, lengths = qlora_step.make_batch(dev, seed=seed)
+        total = -(-int(lengths.sum()) // bucket) * bucket
+        total0 = total0 or total
+        if total == total0:
+            batches.append((b, int(lengths.sum())))
+        if len(batches) == 5:
+            break
+    assert len(batches) == 5
+    gstep = qlora_step.GraphedStep(model, opt, scaler, batches[0][0], warmup=2, bucket=bucket)
+    assert gstep.packed.ids.shape[1] == total0
+    for i, (b, n_real) in enumerate(batches):
+        if i:
+            gstep.load(b)
+        m = {}
+        g_loss = float(gstep.step(m, b))
+        torch.cuda.synchronize()
+        g_grads = [p.grad.detach().float().clone() for p in params]  # unscaled by the step
+        scale = float(scaler.get_scale())
+        k_loss, k_grads = _eager_scaled(model, b, bucket, scale)
+        assert g_loss == k_loss, (i, g_loss, k_loss)
+        for name, gg, kg in zip(names, g_grads, k_grads):
+            assert torch.equal(gg, kg), (i, name)
+        e_loss, e_grads = _eager_scaled(model, b, None, scale)
+        e_m = _eager_metrics(model, b)
+        assert abs(g_loss - e_loss) <= 1e-4 * abs(e_loss), (i, g_loss, e_loss)
+        for name, gg, eg in zip(names, g_grads, e_grads):
+            err = float((gg - eg).abs().max())
+            assert err <= 2e-2 * float(eg.abs().max()), (i, name, err)
+        assert m["num_tokens"] == e_m["num_tokens"] == n_real
+        assert abs(m["entropy"] - e_m["entropy"]) <= 1e-4 * abs(e_m["entropy"]), (m, e_m)
+        labelled = int((b["labels"][:, 1:] != -100).sum())
+        assert abs(m["mean_token_accuracy"] - e_m["mean_token_accuracy"]) <= 1.0 / labelled
+    runner = qlora_step.BucketedGraphSteps(model, opt, scaler, bucket=bucket)
+    seen = set()
+    for seed in range(600, 900):
+        b, lengths = qlora_step.make_batch(dev, seed=seed)
+        total = -(-int(lengths.sum()) // bucket) * bucket
+        if total == total0 or (len(seen) == 2 and total not in seen):
+            continue
+        seen.add(total)
+        loss = float(runner.step(b, metrics={}))
+        torch.cuda.synchronize()
+        assert torch.isfinite(torch.tensor(loss))
+        if len(seen) == 2 and seed >= 640:
+            break
+    assert len(seen) == 2
+    assert sorted(runner.graphs) == sorted(seen) and len(runner.capture_ms) == 2
