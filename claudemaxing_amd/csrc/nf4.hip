@@ -12,8 +12,8 @@
 // 1 KiB slices of the packed weight, so every load and store instruction of a wavefront covers
 // one contiguous span (256 B in, 1 KiB out for fp16). The fp16 outputs go out as nontemporal
 // stores (measured on MI355X: 8.7 -> 7.5 us on the [8960,1536] weight, cold
-// caches). The 16-entry code table sits in LDS: the 16 entries fall in 16 distinct banks, so the
-// per-lane lookups never conflict.
+// caches). The code table sits in LDS as 256 pairs (code[b >> 4], code[b & 15]), one per packed
+// byte value b, so a byte's two code values are one 8-byte lookup indexed by the byte itself.
 #include "common.h"
 
 namespace {
@@ -81,9 +81,13 @@ struct Pack8<float> {
 // Vector path: packed 4-byte aligned, out 16-byte aligned. Units [0, n_units) of 4 bytes. A
 // workgroup's 1024 units span at most 256 absmax blocks (blocksize >= 32 elements = 4 units), and
 // lane t stages block blk0 + t in LDS: its absmax byte and absmax2 entry (or its fp32 absmax),
-// with one entry of the 256-entry code2 table per lane and the 16-entry code table. Those loads
-// are issued first, then the lane's packed words; one barrier, after which a unit's scale is
-// code2[q8] * absmax2 + offset from LDS. A lane thus issues its 4 word loads and at most 3
+// with one entry of the 256-entry code2 table and one of the 256 code pairs per lane. Those
+// loads are issued first, then the lane's packed words; one barrier, after which a unit's scale
+// is code2[q8] * absmax2 + offset from LDS and each of its bytes one pair lookup (a lookup per
+// nibble and the nibble arithmetic took 201 VALU instructions and 40 LDS reads per lane, the
+// pairs 158 and 24: 6.8-7.0 -> 6.6 us at [8960,1536], same process, bit-identical). Workgroups
+// whose units all lie inside the weight (all but the last) skip the per-unit bounds tests
+// (-0.1 us). A lane thus issues its 4 word loads and at most 3
 // coalesced others (loading the absmax byte and absmax2 entry per unit took 12, and the kernel
 // 7.2 us at [8960,1536] against 6.0 us for the same loads and stores without the decode; now
 // 6.7 us). SCALES_FIRST issues the block loads before the packed words: faster when every
@@ -98,7 +102,8 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
     OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
   static_assert(kThreads >= 256, "one code2 entry per lane");
   static_assert(kThreads * kUnits / 4 <= kThreads, "one absmax block of the range per lane");
-  __shared__ float s_code[16];
+  static_assert(kThreads == 256, "one code pair per lane");
+  __shared__ float2 s_pair[256];  // packed byte b -> (code[b >> 4], code[b & 15])
   __shared__ float s_code2[NESTED ? 256 : 1];
   __shared__ uint2 s_blk[kThreads];  // block blk0 + t: {absmax byte, absmax2 bits} or {-, absmax}
   const int t = threadIdx.x;
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
                      ? (kThreads * kUnits) >> unit_shift
                      : 1;
   uint32_t q8 = 0;
-  float a2 = 0.0f, c = 0.0f, c2 = 0.0f;
+  float a2 = 0.0f, c2 = 0.0f;
   uint32_t word[kUnits];
   auto load_words = [&] {
 #pragma unroll
@@ -130,18 +135,16 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
       }
     }
   }
-  if (t < 16) c = code[t];
+  const float2 pair = make_float2(code[t >> 4], code[t & 15]);
   if constexpr (NESTED) c2 = code2[t];
   if constexpr (SCALES_FIRST) load_words();
   if (t < nb) s_blk[t] = uint2{q8, __builtin_bit_cast(uint32_t, a2)};
-  if (t < 16) s_code[t] = c;
+  s_pair[t] = pair;
   if constexpr (NESTED) s_code2[t] = c2;
   const float offset = NESTED ? *offset_ptr : 0.0f;
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kUnits; ++j) {
+  auto unit = [&](int j) {
     const int64_t u = u0 + t + j * kThreads;
-    if (u >= n_units) break;
     const uint2 e = s_blk[static_cast<uint32_t>(u >> unit_shift) - blk0];
     float s;
     if constexpr (NESTED) {
@@ -153,11 +156,19 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
     float v[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t byte = (word[j] >> (8 * k)) & 0xffu;
-      v[2 * k] = s_code[byte >> 4] * s;
-      v[2 * k + 1] = s_code[byte & 0xfu] * s;
+      const float2 cp = s_pair[(word[j] >> (8 * k)) & 0xffu];  // high nibble first
+      v[2 * k] = cp.x * s;
+      v[2 * k + 1] = cp.y * s;
     }
     Pack8<OutT>::store(out + 8 * u, v);
+  };
+  if (u0 + kThreads * kUnits <= n_units) {  // every workgroup but the last: no bounds tests
+#pragma unroll
+    for (int j = 0; j < kUnits; ++j) unit(j);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kUnits; ++j)
+      if (u0 + t + j * kThreads < n_units) unit(j);
   }
 }
 
