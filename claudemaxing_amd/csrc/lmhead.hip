@@ -153,19 +153,40 @@ struct EpiProbs {
 #define Z(e) acc[(e) / 16][nt][(e) % 16]
       // A plain conversion (an accumulator, not a product, so there is no multiply for the
       // compiler to fuse it with): it can be computed for every element and selected, where
-      // cm::from_f32's register pin made the compiler branch around each conversion.
+      // cm::from_f32's register pin made the compiler branch around each conversion. Groups
+      // wholly inside the chunk (all but the chunk's last tile; wave-uniform) need no select.
+      if (mb + kGroup <= n_voc) {
 #pragma unroll
-      for (int e = 0; e < TM * 16; ++e)
-        Z(e) = mb + vrow(e) < n_voc ? static_cast<float>(static_cast<_Float16>(Z(e))) : kNoLogit;
-      // group max and first argmax over both halves of the wavefront (branch-free)
-      float m = kNoLogit;
-      int best = -1;
+        for (int e = 0; e < TM * 16; ++e) Z(e) = static_cast<float>(static_cast<_Float16>(Z(e)));
+      } else {
 #pragma unroll
-      for (int e = 0; e < TM * 16; ++e) {
-        const bool take = Z(e) > m;
-        m = take ? Z(e) : m;
-        best = take ? mb + vrow(e) : best;
+        for (int e = 0; e < TM * 16; ++e)
+          Z(e) = mb + vrow(e) < n_voc ? static_cast<float>(static_cast<_Float16>(Z(e))) : kNoLogit;
       }
+      // group max and first argmax over both halves of the wavefront (branch-free). In a lane,
+      // ascending e is ascending vocabulary row (vrow), so the lane's first argmax is the least e
+      // holding the lane's maximum: the maximum as four independent running maxima (no compare-
+      // select chain through all 64 values), then the least e equal to it, also four chains.
+      // Maxima that are not above kNoLogit (no usable logit) leave best = -1.
+      constexpr int kQ = TM * 4;  // values per chain
+      float mq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        mq[q] = Z(q * kQ);
+#pragma unroll
+        for (int e = q * kQ + 1; e < (q + 1) * kQ; ++e) mq[q] = fmaxf(mq[q], Z(e));
+      }
+      float m = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
+      int fq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        fq[q] = -1;
+#pragma unroll
+        for (int e = (q + 1) * kQ - 1; e >= q * kQ; --e) fq[q] = Z(e) == m ? e : fq[q];
+      }
+      const int first = fq[0] >= 0 ? fq[0] : fq[1] >= 0 ? fq[1] : fq[2] >= 0 ? fq[2] : fq[3];
+      int best = m > kNoLogit && first >= 0 ? mb + vrow(first) : -1;
+      if (best < 0) m = kNoLogit;
       const float m_o = __shfl_xor(m, 32, cm::kWave);
       const int best_o = __shfl_xor(best, 32, cm::kWave);
       const bool other = m_o > m || (m_o == m && best_o >= 0 && (best < 0 || best_o < best));
