@@ -1017,6 +1017,25 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     only = [x for x in args.only.split(",") if x]
+    # the training step first, while nothing else holds device memory: its device-level memory
+    # figures (polled total - free) then start from what the process holds after HIP's start
+    step = None
+    if not args.no_step and (not only or "qlora_step" in only):
+        print("[bench] qlora_step ...", file=sys.stderr, flush=True)
+        step = qlora_step_bench(dev, args.step_steps)
+        b = step["distinct_batches"]["bucketed_graphs"]
+        print(f"[bench] qlora_step: {step['distinct_batches']['median_ms']} ms per step eager over "
+              f"distinct batches, {b['median_ms']} ms median ({b['mean_ms']} mean, "
+              f"{b['captures_timed']} captures) replayed from bucketed graphs "
+              f"({step['distinct_batches']['graphed_with_capture']['median_ms']} ms capturing a "
+              f"graph per batch); fixed batch {step['median_ms']} ms eager, "
+              f"{step['graphed']['median_ms']} ms graphed; eager peak allocated / reserved "
+              f"{step['distinct_batches']['peak_allocated_mib']} / "
+              f"{step['distinct_batches']['peak_reserved_mib']} MiB, device in use "
+              f"{step['distinct_batches']['device_used_peak_over_start_mib']} MiB over the "
+              f"process start", file=sys.stderr, flush=True)
+        gc.collect()
+        torch.cuda.empty_cache()
     kernels = build_kernels(dev, only)
     torch.cuda.synchronize()
     results = {}
@@ -1093,17 +1112,8 @@ def main():
         "in_step_kernel_sum_ms": round(sum(r["us"] for r in results.values()
                                            if r["in_step"]) / 1e3, 4),
     }
-    if not args.no_step and (not only or "qlora_step" in only):
-        print("[bench] qlora_step ...", file=sys.stderr, flush=True)
-        line["qlora_step"] = qlora_step_bench(dev, args.step_steps)
-        q = line["qlora_step"]
-        print(f"[bench] qlora_step: {q['distinct_batches']['median_ms']} ms per step eager over "
-              f"distinct batches ({q['distinct_batches']['graphed_with_capture']['median_ms']} ms "
-              f"capturing a graph per batch); fixed batch {q['median_ms']} ms eager, "
-              f"{q['graphed']['median_ms']} ms graphed; peak allocated "
-              f"{q['distinct_batches']['peak_allocated_gb']} GB eager over distinct batches, "
-              f"{q['peak_allocated_gb']} GB eager fixed, {q['graphed']['peak_hbm_gb']} GB graphed "
-              f"(graph pool included)", file=sys.stderr, flush=True)
+    if step is not None:
+        line["qlora_step"] = step
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(headline)
     print(json.dumps(line), flush=True)
