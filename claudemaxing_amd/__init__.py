@@ -7,6 +7,7 @@ through ctypes.
 """
 
 from .attention import patch_qwen2_grouped_sdpa
+from .decoder import patch_qwen2_decoder_residual
 from .lm_head_loss import patch_fused_head_loss
 from .lora import patch_peft_lora_4bit
 from .nf4 import patch_bnb_nf4_dequant
@@ -17,7 +18,9 @@ from .swiglu_recompute import patch_qwen2_mlp_recompute
 
 
 def apply():
-    """Apply the patches in the reference's order (solution/__init__.py:25-34). The last one,
+    """Apply the patches in the reference's order (solution/__init__.py:25-34), with two of this
+    package's own before the last (q/k/v as one fused NF4 GEMM, and the decoder layer's residual
+    adds inside its norms: the same arithmetic in fewer launches). The last one,
     the attention patch (attention.py, `patch_qwen2_grouped_sdpa`), routes the packed batch of
     the fused training forward to the native packed causal attention kernels. Other boolean
     masks keep transformers' own path: the reference's per-kv-head grouped SDPA is slower than
@@ -30,4 +33,5 @@ def apply():
     patch_bnb_nf4_dequant()  # NF4 dequantization (when bitsandbytes is installed)
     patch_peft_lora_4bit()  # LoRA branch with a packed dropout mask (when peft is installed)
     patch_qwen2_fused_qkv()  # q/k/v of NF4 + LoRA blocks as one fused NF4 GEMM each way
+    patch_qwen2_decoder_residual()  # the decoder layer's residual adds inside its norms
     patch_qwen2_grouped_sdpa()  # causal attention of the packed batch

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -65,6 +65,10 @@ SIGNATURES = {
     "cm_rmsnorm_fwd": (_I, [_P, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P, _I, _L, _I, _F, _P]),
     "cm_rmsnorm_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _L, _I, _P]),
     "cm_rmsnorm_bwd_partials": (_L, [_L]),
+    "cm_rmsnorm_add_fwd": (_I, [_P, _P, _I, _L, _P, _I, _P, _P, _P, _P, _P, _P, _I, _L, _I, _F,
+                                _P]),
+    "cm_rmsnorm_bwd_res": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _L,
+                                _I, _P]),
     "cm_rope": (_I, [_P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _I, _P, _I, _P, _P, _I,
                      _L, _L, _I, _I, _I, _I, _P]),
     "cm_swiglu_fwd": (_I, [_P, _I, _P, _I, _P, _I, _L, _I, _P]),

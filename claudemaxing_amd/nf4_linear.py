@@ -18,7 +18,7 @@ import torch
 from . import _lib
 from .gemm import gemm_f32, gemm_f32_supported, split_k_pays
 from .nf4 import _BLOCKSIZES, QuantState, _nf4_code, _offset_tensor, dequantize_nf4, quantize_nf4
-from .rmsnorm import fp16_copy_of
+from .rmsnorm import fp16_copy_of, fp16_grad_copy_of
 
 # ---------------------------------------------------------------------------------------------
 # The fused path: NF4 weights expanded inside the GEMM (csrc/nf4_gemm.hip), fp16 compute.
@@ -256,7 +256,8 @@ class MatMulNF4(torch.autograd.Function):
     def backward(ctx, grad):
         if not ctx.needs_input_grad[0]:
             return None, None, None, None, None, None
-        grad = grad.to(ctx.compute)
+        low = fp16_grad_copy_of(grad) if ctx.compute == torch.float16 else None
+        grad = low if low is not None else grad.to(ctx.compute)
         if ctx.fused and ctx.x_dtype in (torch.float16, torch.float32):
             dx = nf4_linear_bwd([grad], [(ctx.packed, ctx.state)], ctx.x_dtype)
             return dx, None, None, None, None, None

@@ -474,8 +474,8 @@ class VramPoller:
 
 @contextlib.contextmanager
 def unpatched():
-    """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, attention block, causal-LM
-    forward, sdpa attention) and the plain LoRA computation (nn.Dropout + two linears) for the duration of the block; the kernel
+    """The stock transformers Qwen2 code paths (RMSNorm, RoPE, MLP, attention block, decoder
+    layer, causal-LM forward, sdpa attention) and the plain LoRA computation (nn.Dropout + two linears) for the duration of the block; the kernel
     set's paths are put back afterwards. NF4Linear keeps its dequant kernel (bit-exact to the
     NF4 oracle, so the weights are the same either way)."""
     from transformers.models.qwen2 import modeling_qwen2 as mq
@@ -492,7 +492,7 @@ def unpatched():
         AttentionInterface._global_mapping["sdpa"] = sdpa._original
     for owner, attr in ((mq.Qwen2RMSNorm, "forward"), (mq.Qwen2MLP, "forward"),
                         (mq.Qwen2ForCausalLM, "forward"), (mq.Qwen2Attention, "forward"),
-                        (mq, "apply_rotary_pos_emb")):
+                        (mq.Qwen2DecoderLayer, "forward"), (mq, "apply_rotary_pos_emb")):
         current = getattr(owner, attr)
         original = getattr(current, "_original", None)
         if original is not None:

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 3
+#define CM_ABI_VERSION 4
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -124,6 +124,30 @@ int cm_rmsnorm_bwd(const void* dy, int dy_dtype, const void* xs, int xs_dtype, c
                    int64_t n_rows, int n_cols, void* stream);
 /* Number of partial dw rows cm_rmsnorm_bwd writes for n_rows rows. */
 int64_t cm_rmsnorm_bwd_partials(int64_t n_rows);
+
+/* The residual add before a norm, fused into it. No counterpart in the reference: transformers'
+ * Qwen2DecoderLayer.forward (modeling_qwen2.py) adds the residual in torch (`residual +
+ * hidden_states`) and then calls the norm, which solution/rmsnorm.py:147-192 replaces.
+ *   h = residual + x   (fp32, one rounding; residual contiguous fp32 [n_rows, n_cols]; x of any
+ *                       float dtype with row stride x_row_stride), written to h
+ *   then cm_rmsnorm_fwd of h (an fp32 input): out (fp32), rstd, and low16 / small16 as there.
+ */
+int cm_rmsnorm_add_fwd(const float* residual, const void* x, int x_dtype, int64_t x_row_stride,
+                       const void* w, int w_dtype, float* h, float* out, float* rstd, void* low16,
+                       const int32_t* slot, void* small16, int n_small, int64_t n_rows,
+                       int n_cols, float eps, void* stream);
+
+/* cm_rmsnorm_bwd for an fp32 x with the residual's gradient added and an fp16 copy written. No
+ * counterpart in the reference: autograd adds the two gradients of the decoder layer's h (the
+ * residual's and the norm's) in torch, and the projection before h casts that sum to fp16.
+ *   dx = dres + (cm_rmsnorm_bwd's dx)   (fp32, one rounding; dres NULL: the norm's dx alone)
+ *   dx16 = fp16(dx) when dx16 != NULL
+ * dres, dx and dx16 are contiguous [n_rows, n_cols]; the other arguments as cm_rmsnorm_bwd's.
+ */
+int cm_rmsnorm_bwd_res(const void* dy, int dy_dtype, const void* xs, int xs_dtype, const void* w,
+                       int w_dtype, const float* rstd, const float* dres, float* dx, void* dx16,
+                       float* dw_partial, const int32_t* slot, const void* small16, int n_small,
+                       int saved_output, int64_t n_rows, int n_cols, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
 /* Rotary position embedding, forward or backward (transposed rotation), on up to two tensors

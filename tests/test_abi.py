@@ -71,6 +71,11 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_rmsnorm_fwd(None, 1, 4, None, 0, None, 1, None, None, None, None, 1, 2, 8,
                               1e-6, None) == INVALID  # row stride < n_cols
     assert lib.cm_xent_rows(None, 1, 4, None, None, None, None, 1, 8, 0, 1.0, None) == INVALID
+    # residual norm: the residual and h are required; the residual gradient needs an fp32 x
+    assert lib.cm_rmsnorm_add_fwd(None, 0x1000, 0, 8, 0x2000, 0, None, 0x3000, 0x4000, None,
+                                  None, None, 1, 2, 8, 1e-6, None) == INVALID
+    assert lib.cm_rmsnorm_bwd_res(0x1000, 1, 0x2000, 1, 0x3000, 1, 0x4000, 0x5000, 0x6000, None,
+                                  None, None, None, 1, 0, 2, 8, None) == INVALID
     # fused LoRA adapter: rank must be 16, K and N multiples of 8 and <= 2048
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 4, 1536, 1536,
                                  8, 1.05, 2.0, None) == INVALID
@@ -93,6 +98,10 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.cm_lora_pack(None, 0, None, None, None, 0, 1.0, None) == 0
     assert lib.cm_swiglu_fwd(None, 1, None, 1, None, 1, 0, 1, None) == 0
     assert lib.cm_rmsnorm_bwd_partials(0) == 0
+    assert lib.cm_rmsnorm_add_fwd(None, None, 0, 8, None, 0, None, None, None, None, None, None,
+                                  1, 0, 8, 1e-6, None) == 0
+    assert lib.cm_rmsnorm_bwd_res(None, 0, None, 0, None, 0, None, None, None, None, None, None,
+                                  None, 1, 0, 0, 8, None) == 0
     assert lib.cm_rmsnorm_bwd_partials(10) == 12
     assert lib.cm_lora_fused_fwd(None, None, None, None, None, None, None, None, 0, 1536, 256,
                                  16, 1.05, 2.0, None) == 0

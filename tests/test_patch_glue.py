@@ -381,3 +381,90 @@ def test_mlp_patch_routes_frozen_and_trainable_projections(monkeypatch):
     with torch.no_grad():
         mlp(x)  # no gradient
     assert seen == [("activation", True), ("recompute", None), ("activation", True)]
+
+
+# -- Qwen2DecoderLayer ---------------------------------------------------------------------------
+def _layer():
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    torch.manual_seed(0)
+    cfg = modeling.Qwen2Config(hidden_size=32, intermediate_size=64, num_attention_heads=2,
+                               num_key_value_heads=1)
+    cfg._attn_implementation = "eager"
+    return modeling.Qwen2DecoderLayer(cfg, 0), cfg
+
+
+def test_decoder_patch_is_idempotent_and_runs_the_original_on_the_host(monkeypatch):
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    from claudemaxing_amd import decoder as D
+
+    saved = modeling.Qwen2DecoderLayer.forward
+    original = getattr(saved, "_original", saved)
+    monkeypatch.setattr(modeling.Qwen2DecoderLayer, "forward", saved)
+    D.patch_qwen2_decoder_residual()
+    first = modeling.Qwen2DecoderLayer.forward
+    D.patch_qwen2_decoder_residual()
+    assert modeling.Qwen2DecoderLayer.forward is first and tagged(first, "decoder_residual")
+    layer, cfg = _layer()
+    x = torch.randn(1, 5, 32)
+    pos = torch.arange(5).unsqueeze(0)
+    pe = modeling.Qwen2RotaryEmbedding(cfg)(x, pos)
+    got = layer(x, position_ids=pos, position_embeddings=pe)
+    want = original(layer, x, position_ids=pos, position_embeddings=pe)
+    assert torch.equal(got, want)
+
+
+def test_decoder_patch_routes_only_fusable_layers(monkeypatch):
+    """A GPU-looking fp32 stream through the package's norms takes norm_pass, the attention,
+    add_norm and the MLP with the last add in torch; an fp16 stream, a hooked norm, or the stock
+    norm forward takes the original layer. The kernels are intercepted, so nothing launches."""
+    from transformers.models.qwen2 import modeling_qwen2 as modeling
+
+    from claudemaxing_amd import decoder as D
+    from claudemaxing_amd import rmsnorm as RN
+
+    monkeypatch.setattr(modeling.Qwen2DecoderLayer, "forward",
+                        modeling.Qwen2DecoderLayer.forward)
+    monkeypatch.setattr(modeling.Qwen2RMSNorm, "forward", modeling.Qwen2RMSNorm.forward)
+    D.patch_qwen2_decoder_residual()
+    seen = []
+    monkeypatch.setattr(D, "norm_pass", lambda x, w, eps: (seen.append("norm_pass"), (x, x))[1])
+    monkeypatch.setattr(D, "add_norm",
+                        lambda r, x, w, eps: (seen.append("add_norm"), (x, r + x))[1])
+
+    class Attn(torch.nn.Module):
+        def forward(self, hidden_states, **kwargs):
+            seen.append("attn")
+            return hidden_states * 2, None
+
+    class Mlp(torch.nn.Module):
+        def forward(self, x):
+            seen.append("mlp")
+            return x * 3
+
+    layer, _ = _layer()
+    layer.self_attn, layer.mlp = Attn(), Mlp()
+    x = _cuda(torch.ones(1, 4, 32))
+    stock_norm = modeling.Qwen2RMSNorm.forward
+    if not tagged(stock_norm, "rmsnorm"):
+        RN.patch_qwen2_rmsnorm()
+    # fused: h = x + 2x, out = h + 3 * (2x)
+    out = layer(x)
+    assert seen == ["norm_pass", "attn", "add_norm", "mlp"]
+    assert torch.equal(out.as_subclass(torch.Tensor), torch.full((1, 4, 32), 9.0))
+    seen.clear()
+    for case in ("fp16", "hook", "stock norm"):
+        xs = x
+        handle = None
+        if case == "fp16":
+            xs = _cuda(torch.ones(1, 4, 32, dtype=torch.float16))
+        elif case == "hook":
+            handle = layer.input_layernorm.register_forward_hook(lambda *a: None)
+        else:
+            monkeypatch.setattr(modeling.Qwen2RMSNorm, "forward",
+                                modeling.Qwen2RMSNorm.forward._original)
+        assert not D._norms_fusable(layer, xs), case
+        if handle is not None:
+            handle.remove()
+    assert not seen

@@ -87,16 +87,17 @@ def test_unpatched_restores_and_reapplies():
     sdpa = AttentionInterface._global_mapping["sdpa"]
     assert tagged(sdpa, "packed_sdpa")
     patched = (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
-               mq.apply_rotary_pos_emb, lora._branch_applies)
+               mq.apply_rotary_pos_emb, mq.Qwen2DecoderLayer.forward, lora._branch_applies)
     with qlora_step.unpatched():
         assert AttentionInterface._global_mapping["sdpa"] is sdpa._original
         assert mq.Qwen2RMSNorm.forward is patched[0]._original
         assert mq.Qwen2MLP.forward is patched[1]._original
         assert mq.Qwen2ForCausalLM.forward is patched[2]._original
         assert mq.apply_rotary_pos_emb is patched[3]._original
+        assert mq.Qwen2DecoderLayer.forward is patched[4]._original
         assert lora._branch_applies(None, 0.5, None, None, True) is False
     assert (mq.Qwen2RMSNorm.forward, mq.Qwen2MLP.forward, mq.Qwen2ForCausalLM.forward,
-            mq.apply_rotary_pos_emb, lora._branch_applies) == patched
+            mq.apply_rotary_pos_emb, mq.Qwen2DecoderLayer.forward, lora._branch_applies) == patched
     assert AttentionInterface._global_mapping["sdpa"] is sdpa
 
 
