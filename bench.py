@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--only", default="")
     p.add_argument("--step-steps", type=int, default=10, help="timed QLoRA steps (config 5)")
     p.add_argument("--no-step", action="store_true", help="skip the QLoRA step (config 5)")
+    p.add_argument("--step-graphed-only", action="store_true",
+                   help="time only the repeated batch replayed from its graph (for a kernel "
+                        "trace of that step alone)")
     p.add_argument("--no-peaks", action="store_true",
                    help="skip the on-box HBM and matrix-core peak probes")
     p.add_argument("--no-power", action="store_true",
@@ -901,6 +904,26 @@ def cpu_baseline(headline):
                        f"median of 3 ({dt * 1e3:.0f} ms)")
 
 
+def qlora_step_graphed_bench(dev, steps, warmup=2):
+    """Config 5's repeated batch replayed from its HIP graph, nothing else (one eager step before
+    the capture warms up the model), for a kernel trace of that step alone."""
+    import torch
+
+    from claudemaxing_amd import qlora_step
+
+    model = qlora_step.build_model(dev, seed=0)
+    batch, lengths = qlora_step.make_batch(dev, seed=0)
+    opt = qlora_step.make_optimizer(model)
+    scaler = torch.amp.GradScaler("cuda")
+    qlora_step.train_step(model, opt, scaler, batch)
+    rg = qlora_step.time_steps(model, opt, scaler, batch, steps, warmup, graphed=True)
+    tokens = int(lengths.sum())
+    return dict(fixed_batch=f"{tokens} real tokens (lengths {lengths.tolist()}), repeated",
+                graphed=dict(median_ms=round(rg["median_ms"], 2),
+                             step_ms=[round(x, 2) for x in rg["step_ms"]],
+                             tokens_per_s=round(tokens / (rg["median_ms"] * 1e-3), 1)))
+
+
 def qlora_step_bench(dev, steps, warmup=2):
     """Config 5: one QLoRA training step of the 28-layer Qwen2.5-1.5B-shaped model (random
     init, NF4 base weights, LoRA r16/a32/p0.05 on q/v, fp16 autocast, AdamW + GradScaler, batch
@@ -1022,7 +1045,13 @@ def main():
     step = None
     if not args.no_step and (not only or "qlora_step" in only):
         print("[bench] qlora_step ...", file=sys.stderr, flush=True)
-        step = qlora_step_bench(dev, args.step_steps)
+        if args.step_graphed_only:
+            step = qlora_step_graphed_bench(dev, args.step_steps)
+            print(f"[bench] qlora_step: {step['graphed']['median_ms']} ms graphed", file=sys.stderr,
+                  flush=True)
+        else:
+            step = qlora_step_bench(dev, args.step_steps)
+    if step is not None and not args.step_graphed_only:
         b = step["distinct_batches"]["bucketed_graphs"]
         print(f"[bench] qlora_step: {step['distinct_batches']['median_ms']} ms per step eager over "
               f"distinct batches, {b['median_ms']} ms median ({b['mean_ms']} mean, "
@@ -1034,6 +1063,7 @@ def main():
               f"{step['distinct_batches']['peak_reserved_mib']} MiB, device in use "
               f"{step['distinct_batches']['device_used_peak_over_start_mib']} MiB over the "
               f"process start", file=sys.stderr, flush=True)
+    if step is not None:
         gc.collect()
         torch.cuda.empty_cache()
     kernels = build_kernels(dev, only)

@@ -159,7 +159,9 @@ int cm_rmsnorm_bwd_res(const void* dy, int dy_dtype, const void* xs, int xs_dtyp
  * h = D/2 and bit 0 of flags selecting the backward rotation:
  *   forward:  o[:h] = x1*c1 - x2*s1;  o[h:] = x2*c2 + x1*s2
  *   backward: o[:h] = x1*c1 + x2*s2;  o[h:] = x2*c2 - x1*s1         (fp32 arithmetic)
- * Pass x1 = NULL (H1 = 0) to rotate one tensor. D must be even and <= 512.
+ * Pass x1 = NULL (H1 = 0) to rotate one tensor. D must be even and <= 512. Each tensor has its
+ * own input and output dtype; the two share one launch when the dtypes agree, and for fp32
+ * cos/sin with fp32 x0/out0 and (x1, out1) = (fp16, fp32) or (fp32, fp16).
  */
 int cm_rope(const void* x0, int x0_dtype, int64_t sb0, int64_t sh0, int64_t st0, int H0,
             void* out0, int out0_dtype, const void* x1, int x1_dtype, int64_t sb1, int64_t sh1,

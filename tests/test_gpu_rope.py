@@ -75,3 +75,34 @@ def test_non_contiguous_gradient(dev):
     (rq.transpose(1, 2).sum() + rk.mean()).backward()
     assert_close(qd.grad, q1.grad, 1e-5, "dq")
     assert_close(kd.grad, k1.grad, 1e-5, "dk")
+
+
+def test_mixed_dtypes_one_launch_equals_separate(dev):
+    """The training step's pair -- fp32 q, fp16 k, fp32 cos/sin -- rotated in one launch each way
+    (fp32 outputs forward; fp32 dq and fp16 dk backward): the bits of rotating each tensor alone,
+    the fp16 dk being the fp32 gradient's cast, and within the fp32 tolerance of the oracle."""
+    banner("rope mixed q fp32 / k fp16, one launch")
+    from claudemaxing_amd.rope import _rotate_pair
+
+    q, k, cos, sin = make(1, 1193, 12, 2, 128, F32, seed=4)
+    k = k.to(F16)
+    g = torch.Generator().manual_seed(5)
+    gq = torch.randn(q.shape, generator=g)
+    gk = torch.randn(k.shape, generator=g)
+    qd, kd = q.to(dev).requires_grad_(), k.to(dev).requires_grad_()
+    cd, sd = cos.to(dev), sin.to(dev)
+    oq, ok = rope(qd, kd, cd, sd)
+    torch.autograd.backward((oq, ok), (gq.to(dev), gk.to(dev)))
+    assert (oq.dtype, ok.dtype, qd.grad.dtype, kd.grad.dtype) == (F32, F32, F32, F16)
+    aq, _ = _rotate_pair(q.to(dev), None, cd, sd, F32, None, backward=False)
+    _, ak = _rotate_pair(None, k.to(dev), cd, sd, None, F32, backward=False)
+    bq, _ = _rotate_pair(gq.to(dev), None, cd, sd, F32, None, backward=True)
+    _, bk = _rotate_pair(None, gk.to(dev), cd, sd, None, F32, backward=True)
+    torch.cuda.synchronize()
+    assert torch.equal(oq, aq) and torch.equal(ok, ak)
+    assert torch.equal(qd.grad, bq) and torch.equal(kd.grad, bk.to(F16))
+    rq, rk, rdq, rdk = O.forward_backward(q, k.float(), cos, sin, gq, gk)
+    assert_close(oq, rq, 1e-5, "q")
+    assert_close(ok, rk, 1e-5, "k")
+    assert_close(qd.grad, rdq, 1e-5, "dq")
+    assert_close(kd.grad.float(), rdk, 2e-3, "dk (fp16)")
