@@ -114,7 +114,10 @@ def test_conversion_never_holds_both_copies(dev):
     block = 8192 * 256  # elements of one verified row block
     # never the fp32 weight plus the whole fp16 one: at most one block's temporaries on top
     assert torch.cuda.max_memory_allocated() - base <= 7 * block + 2 ** 20
-    assert base - torch.cuda.memory_allocated() >= 2 * n - 2 ** 16  # half the bytes remain
+    # half the bytes remain; the caching allocator may hand the fp16 copy a cached block up to
+    # 1 MiB larger than asked (it splits a large block only when more than 1 MiB would remain),
+    # and counts the whole block as allocated
+    assert base - torch.cuda.memory_allocated() >= 2 * n - 2 ** 20
 
 
 def test_fused_head_reads_the_fp16_weight(dev):
