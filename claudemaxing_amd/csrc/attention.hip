@@ -81,6 +81,17 @@ __device__ __forceinline__ bool block_live(const Rows& rows, int b, int n_tokens
          rows.pstart[r] % kBlk == 0 && rows.start[r + 1] <= n_tokens;
 }
 
+// Grids of the forward and backward kernels: (heads, padded blocks), heads the fast dimension,
+// so that the blocks of one position are dispatched together. A query block's work grows with
+// its index in its row (it sees every key block before it), so the query kernels take the
+// padded blocks in reverse: the last (heaviest) blocks of the rows go out first and the ones
+// that wait for a free CU when the blocks outnumber the CUs (264 at the training step's 1276
+// tokens) are rows' first, lightest blocks. The key-block kernel's work shrinks along a row, so
+// it keeps the natural order.
+__device__ __forceinline__ int heavy_first_query_block() {
+  return static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);
+}
+
 // Stored slot of position p inside its 16-group (an involution: bits 2 and 3 swapped).
 __device__ __forceinline__ int perm16(int p) {
   return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);
@@ -269,8 +280,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   constexpr int kStage = kKTile + kVTile;
   __shared__ uint4 lds[2][2][kStage];  // [pair][stage]
   const Rows& rows = *rows_p;
-  const int h = blockIdx.y, g = h / hpg;
-  const int b = blockIdx.x;
+  const int h = blockIdx.x, g = h / hpg;
+  const int b = heavy_first_query_block();
   if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
@@ -424,8 +435,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
   constexpr int kStage = kVec + 16;
   __shared__ uint4 lds[2][2][kStage];
   const Rows& rows = *rows_p;
-  const int h = blockIdx.y, g = h / hpg;
-  const int b = blockIdx.x;
+  const int h = blockIdx.x, g = h / hpg;
+  const int b = blockIdx.y;  // a row's first key blocks (the most queries) dispatched first
   if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int kb = b - rows.pstart[r] / kBlk;
@@ -570,8 +581,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   constexpr int kStage = 2 * kKVTile + kKTTile;
   __shared__ uint4 lds[2][2][kStage];
   const Rows& rows = *rows_p;
-  const int h = blockIdx.y, g = h / hpg;
-  const int b = blockIdx.x;
+  const int h = blockIdx.x, g = h / hpg;
+  const int b = heavy_first_query_block();
   if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
@@ -650,7 +661,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   if (pair == 1 || ql >= len) return;
   // dq is [H][N][D], or [N][H][D] with tok_major
   const int64_t tok = rows.start[r] + ql;
-  OT* row = dq + (tok_major ? tok * gridDim.y + h
+  OT* row = dq + (tok_major ? tok * gridDim.x + h  // gridDim.x = H
                             : static_cast<int64_t>(h) * n_tokens + tok) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
@@ -770,9 +781,9 @@ extern "C" int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head
 // Launch arguments shared by both directions: the rows image (device memory, 16-byte aligned), the
 // token count and a padded capacity that is a positive multiple of the block.
 bool rows_args_ok(const void* rows, int64_t n_tokens, int64_t n_pad) {
+  // the padded blocks are the grids' second dimension (at most 65535)
   return rows && (reinterpret_cast<uintptr_t>(rows) & 15) == 0 && n_tokens >= 0 &&
-         n_tokens <= 0x3fffffff && n_pad > 0 && n_pad % kBlk == 0 && n_pad <= 0x3fffffff &&
-         n_pad / kBlk <= 0x7fffffff;
+         n_tokens <= 0x3fffffff && n_pad > 0 && n_pad % kBlk == 0 && n_pad / kBlk <= 65535;
 }
 
 extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
@@ -806,7 +817,7 @@ extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * G), dim3(256), 0, s, jobs, rows,
                      nt, np);
   if (int st = cm::launch_status()) return st;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q, q_dtype, sq_h,
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(H, n_blocks), dim3(kThreads), 0, s, q, q_dtype, sq_h,
                      sq_t, k16, vt16, rows, nt, np, H / G, H, scale * 1.4426950408889634f,
                      static_cast<_Float16*>(out), lse2);
   return cm::launch_status();
@@ -867,16 +878,16 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
                      rows, nt, np);
   if (int st = cm::launch_status()) return st;
   const float c_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(n_blocks, H), dim3(kThreads), 0, s, q16, qt16,
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(H, n_blocks), dim3(kThreads), 0, s, q16, qt16,
                      do16, dot16, k16, v16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                      dk_part, dv_part);
   if (int st = cm::launch_status()) return st;
   if (dq_dtype == CM_F32) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(n_blocks, H), dim3(kThreads), 0, s, q16,
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(H, n_blocks), dim3(kThreads), 0, s, q16,
                        do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                        static_cast<float*>(dq), grads_token_major ? 1 : 0);
   } else {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(n_blocks, H), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(H, n_blocks), dim3(kThreads), 0, s,
                        q16, do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                        static_cast<_Float16*>(dq), grads_token_major ? 1 : 0);
   }

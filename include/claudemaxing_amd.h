@@ -305,9 +305,10 @@ int cm_lmhead_ce_noalloc_plan(int64_t n_rows, int64_t vocab, int hidden_size, in
  * rows_image: DEVICE memory (16-byte aligned) holding cm_attn_rows_bytes() bytes that
  * cm_attn_rows_image wrote for the batch's row bounds (its token count must be n_tokens = N),
  * copied there by the caller. n_pad: the padded positions the launch is sized for, a multiple of
- * 64 at least the image's padded count (cm_attn_padded_tokens of its bounds): blocks past the
- * image's own count do nothing, so one launch (or one captured graph) sized for a capacity serves
- * every row structure of N tokens that fits it, the image being rewritten in between. Kernels
+ * 64 (at most 64 x 65535) at least the image's padded count (cm_attn_padded_tokens of its bounds):
+ * blocks past the image's own count do nothing, so one launch (or one captured graph) sized for a
+ * capacity serves every row structure of N tokens that fits it, the image being rewritten in
+ * between. Kernels
  * check the image against n_tokens and n_pad, and write nothing for rows inconsistent with them.
  * head_dim must be 128, H a multiple of G. Bases 16-byte aligned (out 8), strides multiples of 8
  * (f16) or 4 (f32) elements, workspace 256-byte aligned, cm_attn_workspace_bytes(n_pad, H, G,

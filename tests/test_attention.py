@@ -68,6 +68,7 @@ def test_argument_checks(lib):
     assert _fwd(lib, ws_bytes=1024) == INVALID         # workspace too small
     assert _fwd(lib, n_pad=400) == INVALID             # capacity not whole 64-position blocks
     assert _fwd(lib, n_pad=0) == INVALID
+    assert _fwd(lib, n_pad=64 * 65536) == INVALID      # more padded blocks than a grid dimension
     assert _fwd(lib, rows=0) == INVALID                # no rows image
     assert _fwd(lib, rows=(1 << 20) + 8) == INVALID    # image not 16-byte aligned
     assert _fwd(lib, n_tokens=0) == 0                  # no tokens: nothing to do
