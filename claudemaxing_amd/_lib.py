@@ -62,6 +62,8 @@ SIGNATURES = {
     "cm_lora_weight_grads_workspace_bytes": (_L, [_L, _I, _I]),
     "cm_lora_weight_grads": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _P, _L, _P]),
     "cm_gemm_f32": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _L, _P]),
+    "cm_gemm_f32_add": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _P, _L,
+                             _P]),
     "cm_rmsnorm_fwd": (_I, [_P, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P, _I, _L, _I, _F, _P]),
     "cm_rmsnorm_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _L, _I, _P]),
     "cm_rmsnorm_bwd_partials": (_L, [_L]),

@@ -77,9 +77,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(Pairs p, int rema
   }
 }
 
-// out = sum over the S slices in slice order, 4 values per lane.
+// out = sum over the S slices in slice order, 4 values per lane; with `residual`, out = residual
+// + that sum (the residual add of the layer the product ends, one more fp32 rounding).
 __global__ __launch_bounds__(256) void gemm_f32_sum(const float4* __restrict__ ws, int S,
-                                                    int64_t n4, float4* __restrict__ out) {
+                                                    int64_t n4, float4* __restrict__ out,
+                                                    const float4* __restrict__ residual) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n4) return;
   // the slices are loaded 8 at a time before they are added in slice order (a runtime-length
@@ -95,6 +97,10 @@ __global__ __launch_bounds__(256) void gemm_f32_sum(const float4* __restrict__ w
       if (s0 + k < S) {
         a.x += b[k].x; a.y += b[k].y; a.z += b[k].z; a.w += b[k].w;
       }
+  }
+  if (residual != nullptr) {
+    const float4 r = residual[i];
+    a.x = r.x + a.x; a.y = r.y + a.y; a.z = r.z + a.z; a.w = r.w + a.w;
   }
   out[i] = a;
 }
@@ -141,10 +147,12 @@ extern "C" int64_t cm_gemm_f32_workspace_bytes(int M, int N, int K0, int K1) {
   return static_cast<int64_t>(plan_for(M, N, K0, K1).total()) * M * N * 4;
 }
 
-extern "C" int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
-                           const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1,
-                           int M, int N, float* out, void* workspace, int64_t ws_bytes,
-                           void* stream) {
+namespace {
+
+int gemm_f32_impl(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                  const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M,
+                  int N, const float* residual, float* out, void* workspace, int64_t ws_bytes,
+                  void* stream) {
   CM_CHECK_ARG(shape_ok(M, N, K0, K1));
   if (M == 0 || N == 0) return 0;
   CM_CHECK_ARG(a0 && b0 && out && workspace && (K1 == 0 || (a1 && b1)));
@@ -152,7 +160,7 @@ extern "C" int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t
   CM_CHECK_ARG(K1 == 0 || (lda1 >= K1 && ldb1 >= K1 && lda1 % 8 == 0 && ldb1 % 8 == 0));
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   CM_CHECK_ARG(al16(a0) && al16(b0) && al16(out) && al16(workspace) &&
-               (K1 == 0 || (al16(a1) && al16(b1))));
+               (K1 == 0 || (al16(a1) && al16(b1))) && (!residual || al16(residual)));
   CM_CHECK_ARG(static_cast<int64_t>(M) * N % 4 == 0);
   const Plan pl = plan_for(M, N, K0, K1);
   CM_CHECK_ARG(ws_bytes >= static_cast<int64_t>(pl.total()) * M * N * 4);
@@ -173,6 +181,25 @@ extern "C" int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t
   const int64_t n4 = static_cast<int64_t>(M) * N / 4;
   hipLaunchKernelGGL(gemm_f32_sum, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, s,
                      reinterpret_cast<const float4*>(ws), pl.total(), n4,
-                     reinterpret_cast<float4*>(out));
+                     reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(residual));
   return cm::launch_status();
+}
+
+}  // namespace
+
+extern "C" int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                           const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1,
+                           int M, int N, float* out, void* workspace, int64_t ws_bytes,
+                           void* stream) {
+  return gemm_f32_impl(a0, lda0, b0, ldb0, K0, a1, lda1, b1, ldb1, K1, M, N, nullptr, out,
+                       workspace, ws_bytes, stream);
+}
+
+extern "C" int cm_gemm_f32_add(const void* a0, int64_t lda0, const void* b0, int64_t ldb0,
+                               int K0, const void* a1, int64_t lda1, const void* b1,
+                               int64_t ldb1, int K1, int M, int N, const float* residual,
+                               float* out, void* workspace, int64_t ws_bytes, void* stream) {
+  CM_CHECK_ARG(M == 0 || N == 0 || residual != nullptr);
+  return gemm_f32_impl(a0, lda0, b0, ldb0, K0, a1, lda1, b1, ldb1, K1, M, N, residual, out,
+                       workspace, ws_bytes, stream);
 }

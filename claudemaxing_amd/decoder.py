@@ -15,11 +15,12 @@ batch. `patch_qwen2_decoder_residual` runs the same arithmetic as
                                                 plus the bypass's, and its fp16 copy, one launch
     h = self_attn(y)
     y, h = add_norm(residual, h)                residual + h and its norm, one launch each way
-    h = h + mlp(y)
+    h = mlp(y, residual=h)                      the package's MLP adds h in its down projection's
+                                                last launch (the split-K GEMM's slice sum)
 
 with every add the same fp32 add (so the layer's outputs and gradients are the bits of the unfused
-layer with the same norm kernels), the last add left to torch (its backward costs no launch).
-The projections take the fp16 copies through rmsnorm.fp16_grad_copy_of.
+layer with the same kernels). The projections take the fp16 copies through
+rmsnorm.fp16_grad_copy_of.
 
 It applies where the norms are the package's (patch_qwen2_rmsnorm installed, no hooks on the norm
 modules) and take the kernels, on an fp32 residual stream; any other call runs the original.
@@ -29,6 +30,13 @@ import torch
 
 from ._patching import install, tagged
 from .rmsnorm import _kernel_covers, add_norm, norm_pass
+
+
+def _mlp_takes_residual(mlp):
+    """The MLP's forward is the package's (which takes `residual`) and no hook would see the
+    extra argument."""
+    return (tagged(type(mlp).forward, "mlp_recompute")
+            and not (mlp._forward_hooks or mlp._forward_pre_hooks))
 
 
 def _norms_fusable(layer, hidden):
@@ -74,6 +82,8 @@ def patch_qwen2_decoder_residual():
             else:
                 h = residual + attn
                 y = n2(h)
+            if _mlp_takes_residual(self.mlp):
+                return self.mlp(y, residual=h)
             return h + self.mlp(y)
 
         return forward

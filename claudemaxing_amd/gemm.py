@@ -39,8 +39,9 @@ def gemm_f32_supported(m, n, *pairs):
     return True
 
 
-def gemm_f32(*pairs, out=None):
-    """sum over the (A [M, K], B [N, K]) pairs of A @ B^T, fp32 [M, N]."""
+def gemm_f32(*pairs, out=None, residual=None):
+    """sum over the (A [M, K], B [N, K]) pairs of A @ B^T, fp32 [M, N]; with `residual` (fp32 [M, N]
+    contiguous) residual + that sum, added in the same launch (cm_gemm_f32_add)."""
     (a0, b0), rest = pairs[0], pairs[1:]
     m, n = a0.shape[0], b0.shape[0]
     if out is None:
@@ -54,8 +55,15 @@ def gemm_f32(*pairs, out=None):
     if ws_bytes < 0:
         raise RuntimeError("cm_gemm_f32_workspace_bytes: invalid shape")
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=a0.device)
-    _lib.call("cm_gemm_f32", a0.data_ptr(), a0.stride(0), b0.data_ptr(), b0.stride(0), k0,
-              _lib.ptr(a1), a1.stride(0) if rest else 0, _lib.ptr(b1),
-              b1.stride(0) if rest else 0, k1, m, n, out.data_ptr(), ws.data_ptr(), ws_bytes,
-              _lib.stream(a0.device))
+    common = (a0.data_ptr(), a0.stride(0), b0.data_ptr(), b0.stride(0), k0, _lib.ptr(a1),
+              a1.stride(0) if rest else 0, _lib.ptr(b1), b1.stride(0) if rest else 0, k1, m, n)
+    if residual is None:
+        _lib.call("cm_gemm_f32", *common, out.data_ptr(), ws.data_ptr(), ws_bytes,
+                  _lib.stream(a0.device))
+    else:
+        if (residual.dtype != torch.float32 or residual.shape != (m, n)
+                or not residual.is_contiguous()):
+            raise ValueError("gemm_f32: the residual must be a contiguous fp32 [M, N] tensor")
+        _lib.call("cm_gemm_f32_add", *common, residual.data_ptr(), out.data_ptr(),
+                  ws.data_ptr(), ws_bytes, _lib.stream(a0.device))
     return out

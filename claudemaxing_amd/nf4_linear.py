@@ -220,13 +220,21 @@ class MatMulNF4(torch.autograd.Function):
     copy the preceding norm wrote of it when there is one (rmsnorm.fp16_copy_of: the same values
     as x.to(fp16)), else cast. The output is the compute-dtype result, widened to `out_dtype`
     when that is given (an fp32 output of an fp16 product is written in fp32 by the GEMM, without
-    the fp16 rounding); the input gradient is returned in x's dtype.
+    the fp16 rounding); the input gradient is returned in x's dtype. With `residual` the result
+    is residual + that output (a decoder layer's last add), added by the split-K GEMM's sum launch
+    where the product takes it, by torch otherwise; the residual's gradient is the output's.
 
     In fp16 the weight is expanded inside the GEMM each way (cm_nf4_linear_fwd/bwd); otherwise
     it is expanded by the dequant kernel and multiplied by torch."""
 
     @staticmethod
-    def forward(ctx, x, packed, state, bias=None, compute=None, out_dtype=None):
+    def forward(ctx, x, packed, state, bias=None, compute=None, out_dtype=None, residual=None):
+        y = MatMulNF4._product(ctx, x, packed, state, bias, compute, out_dtype, residual)
+        return y if residual is None or ctx.residual_added else residual + y
+
+    @staticmethod
+    def _product(ctx, x, packed, state, bias, compute, out_dtype, residual):
+        ctx.residual_added = False
         compute = compute or x.dtype
         out_dtype = out_dtype or compute
         xc = x
@@ -245,7 +253,15 @@ class MatMulNF4(torch.autograd.Function):
             x2 = xc.reshape(-1, xc.shape[-1])
             if bias is None and split_k_pays(x2.shape[0], w.shape[0], x2.shape[1]) and \
                     gemm_f32_supported(x2.shape[0], w.shape[0], (x2, w)):
-                y = gemm_f32((x2, w))  # narrow output, long contraction: split along k
+                # narrow output, long contraction: split along k; a residual of the output's
+                # shape is added by the sum launch
+                r2 = None
+                if (residual is not None and residual.dtype == torch.float32
+                        and residual.is_contiguous()
+                        and residual.shape == (*xc.shape[:-1], w.shape[0])):
+                    r2 = residual.view(x2.shape[0], w.shape[0])
+                y = gemm_f32((x2, w), residual=r2)
+                ctx.residual_added = r2 is not None
             else:
                 y = (torch.mm(x2, w.t(), out_dtype=torch.float32) if bias is None else
                      torch.addmm(bias.float(), x2, w.t(), out_dtype=torch.float32))
@@ -254,19 +270,20 @@ class MatMulNF4(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
+        d_res = grad if ctx.needs_input_grad[6] else None
         if not ctx.needs_input_grad[0]:
-            return None, None, None, None, None, None
+            return None, None, None, None, None, None, d_res
         low = fp16_grad_copy_of(grad) if ctx.compute == torch.float16 else None
-        grad = low if low is not None else grad.to(ctx.compute)
+        g = low if low is not None else grad.to(ctx.compute)
         if ctx.fused and ctx.x_dtype in (torch.float16, torch.float32):
-            dx = nf4_linear_bwd([grad], [(ctx.packed, ctx.state)], ctx.x_dtype)
-            return dx, None, None, None, None, None
-        w = dequantize_nf4(ctx.packed, ctx.state, grad.dtype)
-        return torch.matmul(grad, w).to(ctx.x_dtype), None, None, None, None, None
+            dx = nf4_linear_bwd([g], [(ctx.packed, ctx.state)], ctx.x_dtype)
+            return dx, None, None, None, None, None, d_res
+        w = dequantize_nf4(ctx.packed, ctx.state, g.dtype)
+        return torch.matmul(g, w).to(ctx.x_dtype), None, None, None, None, None, d_res
 
 
-def matmul_nf4(x, packed, state, bias=None, compute=None, out_dtype=None):
-    return MatMulNF4.apply(x, packed, state, bias, compute, out_dtype)
+def matmul_nf4(x, packed, state, bias=None, compute=None, out_dtype=None, residual=None):
+    return MatMulNF4.apply(x, packed, state, bias, compute, out_dtype, residual)
 
 
 class NF4Linear(torch.nn.Module):
@@ -363,9 +380,11 @@ class NF4Linear(torch.nn.Module):
             self._bias_c = cached
         return cached[1]
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """x W^T (+ bias); with `residual`, residual + that (the add folded into the product's
+        last launch where it can be)."""
         return matmul_nf4(x, self.packed, self.quant_state, self._bias_in(self.compute_dtype),
-                          self.compute_dtype, self.out_dtype or x.dtype)
+                          self.compute_dtype, self.out_dtype or x.dtype, residual)
 
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -84,6 +84,14 @@ int64_t cm_gemm_f32_workspace_bytes(int M, int N, int K0, int K1);
 int cm_gemm_f32(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
                 const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M, int N,
                 float* out, void* workspace, int64_t ws_bytes, void* stream);
+/* cm_gemm_f32 with a residual: out = residual + (the same sum), one more fp32 rounding, in the
+ * slice-sum launch (residual [M, N] fp32 contiguous, 16-byte aligned, not overlapping out). No
+ * counterpart in the reference: the end of transformers' Qwen2DecoderLayer.forward adds the
+ * residual to the MLP's output in torch (`residual + hidden_states`). */
+int cm_gemm_f32_add(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                    const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M,
+                    int N, const float* residual, float* out, void* workspace, int64_t ws_bytes,
+                    void* stream);
 
 /* The same expansion written transposed, fp16 only: out[c][r] = W[r][c] for the weight W
  * [rows, cols] (rows a multiple of 64, cols of 128; packed 4-byte, out 16-byte aligned), the values

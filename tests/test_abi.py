@@ -193,6 +193,9 @@ def test_nf4_linear_argument_checks(lib):
     assert gf(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, o, w, big - 4, None) == INVALID
     assert gf(a, 64, b, 64, 64, None, 0, None, 0, 8, 64, 64, o, w, big, None) == INVALID
     assert gf(a, 64, b, 64, 64, None, 0, None, 0, 0, 0, 64, o, w, 0, None) == 0
+    ga = lib.cm_gemm_f32_add  # the residual is required and 16-byte aligned
+    assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, None, o, w, big, None) == INVALID
+    assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, w + 8, o, w, big, None) == INVALID
     # batched adapter weight gradients: 1..4 jobs, rank 16, widths multiples of 8, even strides,
     # a large enough workspace
     P, L, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int

@@ -136,8 +136,21 @@ def test_patched_layer_equals_unfused_step(dev, monkeypatch):
     batch, _ = qlora_step.make_batch(dev, seed=3)
     patched = mq.Qwen2DecoderLayer.forward
     assert getattr(patched, "_cm_patch", None) == "decoder_residual"
+    from claudemaxing_amd import gemm
+
+    adds = []
+    real = gemm.gemm_f32
+
+    def counting(*pairs, out=None, residual=None):
+        adds.append(residual is not None)
+        return real(*pairs, out=out, residual=residual)
+
+    monkeypatch.setattr(gemm, "gemm_f32", counting)
+    from claudemaxing_amd import nf4_linear
+    monkeypatch.setattr(nf4_linear, "gemm_f32", counting)
     loss1, grads1 = _loss_and_grads(model, batch)
     assert calls == ["norm_pass", "add_norm"] * 2
+    assert adds.count(True) == 2  # each layer's last residual added by its down projection
     mq.Qwen2DecoderLayer.forward = patched._original
     try:
         loss2, grads2 = _loss_and_grads(model, batch)

@@ -70,3 +70,18 @@ def test_unsupported_operands_are_refused(dev):
     assert not gemm_f32_supported(15, 16, (a, b))  # A's rows are not the output's M
     a3, b3 = _pair(3, 3, 64, dev, 6)
     assert not gemm_f32_supported(3, 3, (a3, b3))  # M * N not a multiple of 4
+
+
+@pytest.mark.parametrize("m,k0,k1", [(1276, 8960, 0), (300, 1032, 264)])
+def test_residual_added_in_the_sum_launch(m, k0, k1, dev):
+    """cm_gemm_f32_add: residual + the product, the bits of torch's fp32 add of the two."""
+    banner(f"gemm_f32 + residual m={m} k0={k0} k1={k1}")
+    n = 1536
+    pairs = [_pair(m, n, k0, dev, 5)] + ([_pair(m, n, k1, dev, 6)] if k1 else [])
+    res = torch.randn(m, n, device=dev, generator=torch.Generator(device=dev).manual_seed(7))
+    got = gemm_f32(*pairs, residual=res)
+    want = res + gemm_f32(*pairs)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError):
+        gemm_f32(*pairs, residual=res.t().contiguous().t())  # not contiguous

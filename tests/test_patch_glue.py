@@ -334,6 +334,8 @@ def test_mlp_patch_falls_back_for_host_tensors_and_other_activations(monkeypatch
     mlp = _mlp()
     x = torch.randn(2, 5, 32, requires_grad=True)
     assert torch.equal(mlp(x), original(mlp, x))
+    r = torch.randn(2, 5, 32)  # the decoder layer's residual, added to the original's output
+    assert torch.equal(mlp(x, residual=r), r + original(mlp, x))
     gelu = _mlp("gelu")
     xg = _cuda(torch.randn(2, 5, 32))  # looks like a GPU tensor to the guard
     assert torch.equal(gelu(xg), original(gelu, xg))
@@ -375,6 +377,12 @@ def test_mlp_patch_routes_frozen_and_trainable_projections(monkeypatch):
                                                          gate * 0)[1])
     mlp = _mlp()
     x = _cuda(torch.randn(2, 5, 32)).requires_grad_(True)
+    # a dense down projection: the residual is added after it
+    r = torch.ones(2, 5, 32)
+    got = mlp(x, residual=r)
+    assert torch.equal(got.as_subclass(torch.Tensor),
+                       r + mlp.down_proj(torch.zeros(2, 5, 64)).as_subclass(torch.Tensor))
+    seen.clear()
     mlp(x)  # trainable projections
     mlp.requires_grad_(False)
     mlp(x)  # frozen: the input is all that is kept
