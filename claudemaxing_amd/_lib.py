@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -87,6 +87,11 @@ SIGNATURES = {
                          _F, _P, _P, _P, _L, _P]),
     "cm_attn_bwd": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _P, _P, _L, _L,
                          _I, _I, _I, _F, _P, _I, _P, _P, _I, _I, _P, _L, _P]),
+    "cm_attn_fwd_rope": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _L, _P, _L,
+                              _L, _I, _I, _I, _F, _P, _P, _P, _L, _P]),
+    "cm_attn_bwd_rope": (_I, [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _L, _L, _P, _P, _L, _P, _P,
+                              _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _P, _I, _P, _I, _I, _P, _L,
+                              _P]),
     "cm_attn_padded_tokens": (_L, [_P, _I]),
     "cm_attn_rows_bytes": (_L, []),
     "cm_attn_rows_image": (_L, [_P, _I, _P]),

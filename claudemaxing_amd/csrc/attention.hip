@@ -139,6 +139,44 @@ __device__ __forceinline__ half8 zero8() {
   return f;
 }
 
+// Eight consecutive elements of a (fp32 or fp16) tensor as fp32.
+__device__ __forceinline__ void load8f(const void* base, int dtype, int64_t off, float (&f)[8]) {
+  if (dtype == CM_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+    const float4 a = p[0], b = p[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const half8 h = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(h[i]);
+  }
+}
+
+// Qwen2's rotary embedding fused into the attention: the rotation of the forward's q and k and
+// of the backward's q and k, and the transposed rotation of the gradients dq and dk. cos / sin
+// are fp32 rows [N][D] of the packed tokens with row stride cs_t; cos == nullptr: no rotation.
+struct Rope {
+  const float* cos;
+  const float* sin;
+  int64_t cs_t;
+};
+
+// One element of the rotation, with h = D / 2: the forward writes o[d] = x[d] c[d] - x[d+h] s[d]
+// and o[d+h] = x[d+h] c[d+h] + x[d] s[d+h]; the gradient's transposed rotation writes
+// o[d] = g[d] c[d] + g[d+h] s[d+h] and o[d+h] = g[d+h] c[d+h] - g[d] s[d]. x is the element, p
+// its partner (d +- h), cs the element's cos and sn the sin the formula takes (the element's
+// forward, the partner's backward). Each product is rounded before the sum, as the separate RoPE
+// kernel (no contraction) rounds them: the fused rotation gives its bits.
+__device__ __forceinline__ float rot_minus(float x, float p, float cs, float sn) {
+#pragma clang fp contract(off)
+  return x * cs - p * sn;
+}
+__device__ __forceinline__ float rot_plus(float x, float p, float cs, float sn) {
+#pragma clang fp contract(off)
+  return x * cs + p * sn;
+}
+
 // LDS tiles filled by global_load_lds_dwordx4 (64 lanes x 16 bytes into 64 consecutive slots).
 // A tile has ROWS rows of CH 16-byte chunks; the chunk of (row, logical c) is stored at
 // physical chunk c ^ swz(row), chosen so that a fragment read (16 consecutive rows at one
@@ -191,6 +229,7 @@ struct Job {
   int64_t so_t;
   int dtype;
   int heads;
+  Rope rope;            // rotate the rows on the way (q and k of a fused RoPE), or cos == nullptr
 };
 
 struct Jobs {
@@ -226,7 +265,29 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
     const int local = local0 + t;
     const bool ok = local < len;
     const int64_t tok = rows.start[r] + local;
-    const half8 x = ok ? load8(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8) : zero8();
+    half8 x;
+    if (job.rope.cos == nullptr) {
+      x = ok ? load8(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8) : zero8();
+    } else {
+      // the partner of chunk ch (d +- 64) is chunk ch ^ 8, held by the lane 8 away (a token's
+      // 16 chunks are 16 consecutive lanes, every lane of the loop active)
+      float xv[8], pv[8];
+      if (ok) {
+        load8f(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8, xv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[i] = __shfl_xor(xv[i], 8, cm::kWave);
+      const int64_t ct = ok ? tok : rows.start[r];  // pads: any row of the batch's tables
+      const float* cr = job.rope.cos + ct * job.rope.cs_t + ch * 8;
+      const float* sr = job.rope.sin + ct * job.rope.cs_t + ch * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        x[i] = static_cast<_Float16>(ch < 8 ? rot_minus(xv[i], pv[i], cr[i], sr[i])
+                                            : rot_plus(xv[i], pv[i], cr[i], sr[i]));
+    }
     if (job.nat)
       *reinterpret_cast<half8*>(job.nat + (static_cast<int64_t>(h) * n_pad + pos0 + t) * kD +
                                 ch * 8) = x;
@@ -276,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
     const void* __restrict__ q, int q_dtype, int64_t sq_h, int64_t sq_t,
     const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, int H, float c_log2,
-    _Float16* __restrict__ out, float* __restrict__ lse2) {
+    _Float16* __restrict__ out, float* __restrict__ lse2, int q_padded) {
   constexpr int kStage = kKTile + kVTile;
   __shared__ uint4 lds[2][2][kStage];  // [pair][stage]
   const Rows& rows = *rows_p;
@@ -305,7 +366,9 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
 
   half8 qf[kD / 16];
   {
-    const int64_t off = h * sq_h + static_cast<int64_t>(rows.start[r] + (q_ok ? ql : 0)) * sq_t;
+    // q as given (token rows), or its rotated fp16 copy in the padded positions (fused RoPE)
+    const int64_t at = q_padded ? p0 + (q_ok ? ql : 0) : rows.start[r] + (q_ok ? ql : 0);
+    const int64_t off = h * sq_h + at * sq_t;
 #pragma unroll
     for (int ds = 0; ds < kD / 16; ++ds)
       qf[ds] = q_ok ? load8(q, q_dtype, off + ds * 16 + hh * 8) : zero8();
@@ -577,7 +640,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
     const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
     const float* __restrict__ delta, const Rows* __restrict__ rows_p, int n_tokens, int n_pad,
-    int hpg, float c_log2, float scale, OT* __restrict__ dq, int tok_major) {
+    int hpg, float c_log2, float scale, OT* __restrict__ dq, int tok_major,
+    float* __restrict__ dq_rot) {
   constexpr int kStage = 2 * kKVTile + kKTTile;
   __shared__ uint4 lds[2][2][kStage];
   const Rows& rows = *rows_p;
@@ -661,6 +725,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   if (pair == 1 || ql >= len) return;
   // dq is [H][N][D], or [N][H][D] with tok_major
   const int64_t tok = rows.start[r] + ql;
+  if (dq_rot != nullptr) {
+    // fused RoPE: the gradient of the rotated q, [H][n_pad][D] fp32, which the reduce launch
+    // takes back through the transposed rotation (reading the cos / sin rows coalesced there)
+    float* rrow = dq_rot + (static_cast<int64_t>(h) * n_pad + p0 + ql) * kD;
+#pragma unroll
+    for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        rrow[dt * 32 + (e / 4) * 8 + hh * 4 + e % 4] =
+            (acc[dt][e] + xf[(dt * 16 + e) * cm::kWave]) * scale;
+    return;
+  }
   OT* row = dq + (tok_major ? tok * gridDim.x + h  // gridDim.x = H
                             : static_cast<int64_t>(h) * n_tokens + tok) * kD;
 #pragma unroll
@@ -673,20 +749,63 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
 
 // dK, dV = sum of the partials of the query heads of each group, [G][N][D] (or [N][G][D]) in the
 // output dtype.
-// Thread (position, 4 values of d) of key/value head blockIdx.y.
-template <typename OT>
+// Thread (position, 4 values of d) of key/value head blockIdx.y. With a fused RoPE, dK is the
+// gradient of the rotated k taken back through the transposed rotation (the partner values,
+// d +- 64, are 16 lanes away: a position's 32 threads are consecutive lanes and return together),
+// and blockIdx.y = G + h takes query head h's gradient (dq_rot, written by the dQ kernel) back
+// the same way into dq.
+struct DqRope {
+  const float* rot;  // [H][n_pad][D]
+  void* dq;          // [N][H][D] (token-major) or [H][N][D]
+  int f32;           // dq's dtype: fp32, else fp16
+  int H;
+};
+
+__device__ __forceinline__ float4 rotate_back(float4 v, int d, const Rope& rope, int64_t tok) {
+  const float4 p = make_float4(__shfl_xor(v.x, 16, cm::kWave), __shfl_xor(v.y, 16, cm::kWave),
+                               __shfl_xor(v.z, 16, cm::kWave), __shfl_xor(v.w, 16, cm::kWave));
+  const float* cr = rope.cos + tok * rope.cs_t + d;
+  const float* sp = rope.sin + tok * rope.cs_t + (d < 64 ? d + 64 : d - 64);  // the partner's
+  if (d < 64)
+    return make_float4(rot_plus(v.x, p.x, cr[0], sp[0]), rot_plus(v.y, p.y, cr[1], sp[1]),
+                       rot_plus(v.z, p.z, cr[2], sp[2]), rot_plus(v.w, p.w, cr[3], sp[3]));
+  return make_float4(rot_minus(v.x, p.x, cr[0], sp[0]), rot_minus(v.y, p.y, cr[1], sp[1]),
+                     rot_minus(v.z, p.z, cr[2], sp[2]), rot_minus(v.w, p.w, cr[3], sp[3]));
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float4 v) {
+  p[0] = cm::from_f32<T>(v.x); p[1] = cm::from_f32<T>(v.y);
+  p[2] = cm::from_f32<T>(v.z); p[3] = cm::from_f32<T>(v.w);
+}
+
+template <typename KT, typename VT>
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
     const float* __restrict__ dk_part, const float* __restrict__ dv_part,
-    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, OT* __restrict__ dk,
-    OT* __restrict__ dv, int tok_major) {
+    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, KT* __restrict__ dk,
+    VT* __restrict__ dv, int tok_major, Rope rope, DqRope dqr) {
   const Rows& rows = *rows_p;
-  const int g = blockIdx.y;
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int pos = i / (kD / 4), d = (i % (kD / 4)) * 4;
   if (pos >= n_pad || !block_live(rows, pos / kBlk, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, pos / kBlk);
   const int local = pos - rows.pstart[r];
   if (local >= rows.start[r + 1] - rows.start[r]) return;
+  const int64_t tok = rows.start[r] + local;
+  const int G = static_cast<int>(gridDim.y) - (dqr.rot != nullptr ? dqr.H : 0);
+  if (static_cast<int>(blockIdx.y) >= G) {  // query head blockIdx.y - G of a fused RoPE
+    const int h = blockIdx.y - G;
+    const float4 gq = *reinterpret_cast<const float4*>(
+        dqr.rot + (static_cast<int64_t>(h) * n_pad + pos) * kD + d);
+    const float4 o = rotate_back(gq, d, rope, tok);
+    const int64_t at = (tok_major ? tok * dqr.H + h : static_cast<int64_t>(h) * n_tokens + tok) * kD + d;
+    if (dqr.f32)
+      store4(static_cast<float*>(dqr.dq) + at, o);
+    else
+      store4(static_cast<_Float16*>(dqr.dq) + at, o);
+    return;
+  }
+  const int g = blockIdx.y;
   float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
   for (int j = 0; j < hpg; ++j) {
     const int64_t at = ((static_cast<int64_t>(g) * hpg + j) * n_pad + pos) * kD + d;
@@ -696,14 +815,10 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
     sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
   }
   // dK, dV are [G][N][D], or [N][G][D] with tok_major
-  const int64_t tok = rows.start[r] + local;
-  const int64_t o =
-      (tok_major ? tok * gridDim.y + g : static_cast<int64_t>(g) * n_tokens + tok) * kD +
-      d;
-  dk[o] = cm::from_f32<OT>(sk.x); dk[o + 1] = cm::from_f32<OT>(sk.y);
-  dk[o + 2] = cm::from_f32<OT>(sk.z); dk[o + 3] = cm::from_f32<OT>(sk.w);
-  dv[o] = cm::from_f32<OT>(sv.x); dv[o + 1] = cm::from_f32<OT>(sv.y);
-  dv[o + 2] = cm::from_f32<OT>(sv.z); dv[o + 3] = cm::from_f32<OT>(sv.w);
+  const int64_t o = (tok_major ? tok * G + g : static_cast<int64_t>(g) * n_tokens + tok) * kD + d;
+  if (rope.cos != nullptr) sk = rotate_back(sk, d, rope, tok);
+  store4(dk + o, sk);
+  store4(dv + o, sv);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -742,8 +857,10 @@ struct Workspace {
   }
 };
 
-size_t fwd_ws_bytes(int64_t n_pad, int G) {
-  return 2 * align256(static_cast<size_t>(G) * n_pad * kD * 2);
+// k16 and vt16, and q16 (the rotated q of a fused RoPE)
+size_t fwd_ws_bytes(int64_t n_pad, int H, int G) {
+  return 2 * align256(static_cast<size_t>(G) * n_pad * kD * 2) +
+         align256(static_cast<size_t>(H) * n_pad * kD * 2);
 }
 
 size_t bwd_ws_bytes(int64_t n_pad, int H, int G) {
@@ -775,7 +892,7 @@ extern "C" int64_t cm_attn_rows_image(const int64_t* bounds, int n_rows, void* i
 extern "C" int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim,
                                            int backward) {
   if (n_pad < 0 || H <= 0 || G <= 0 || head_dim != kD) return -1;
-  return static_cast<int64_t>(backward ? bwd_ws_bytes(n_pad, H, G) : fwd_ws_bytes(n_pad, G));
+  return static_cast<int64_t>(backward ? bwd_ws_bytes(n_pad, H, G) : fwd_ws_bytes(n_pad, H, G));
 }
 
 // Launch arguments shared by both directions: the rows image (device memory, 16-byte aligned), the
@@ -786,14 +903,25 @@ bool rows_args_ok(const void* rows, int64_t n_tokens, int64_t n_pad) {
          n_tokens <= 0x3fffffff && n_pad > 0 && n_pad % kBlk == 0 && n_pad / kBlk <= 65535;
 }
 
-extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
-                           int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
-                           int64_t sv_h, int64_t sv_t, const void* rows_image, int64_t n_tokens,
-                           int64_t n_pad, int H, int G, int head_dim, float scale, void* out,
-                           float* lse2, void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+// A fused RoPE's tables: none (cos == nullptr), or fp32 rows of 16-byte aligned cos / sin with a
+// row stride that keeps them aligned.
+bool rope_ok(const Rope& r) {
+  if (r.cos == nullptr) return r.sin == nullptr;
+  return r.sin != nullptr && (reinterpret_cast<uintptr_t>(r.cos) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(r.sin) & 15) == 0 && r.cs_t >= kD && r.cs_t % 4 == 0;
+}
+
+int fwd_impl(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k, int k_dtype,
+             int64_t sk_h, int64_t sk_t, const void* v, int v_dtype, int64_t sv_h, int64_t sv_t,
+             Rope rope, const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G,
+             int head_dim, float scale, void* out, float* lse2, void* workspace,
+             int64_t workspace_bytes, void* stream) {
   CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
   CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
                (v_dtype == CM_F32 || v_dtype == CM_F16));
+  CM_CHECK_ARG(rope_ok(rope));
   if (n_tokens == 0) return 0;
   CM_CHECK_ARG(rows_args_ok(rows_image, n_tokens, n_pad));
   CM_CHECK_ARG(q && k && v && out && lse2 && workspace);
@@ -801,41 +929,78 @@ extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
                aligned_operand(v, v_dtype, sv_h, sv_t));
   CM_CHECK_ARG((reinterpret_cast<uintptr_t>(out) & 7) == 0 &&
                (reinterpret_cast<uintptr_t>(workspace) & 255) == 0);
-  CM_CHECK_ARG(workspace_bytes >= static_cast<int64_t>(fwd_ws_bytes(n_pad, G)));
+  CM_CHECK_ARG(workspace_bytes >= static_cast<int64_t>(fwd_ws_bytes(n_pad, H, G)));
   hipStream_t s = static_cast<hipStream_t>(stream);
   Workspace ws{static_cast<char*>(workspace), 0, static_cast<size_t>(workspace_bytes)};
   _Float16* k16 = ws.take<_Float16>(static_cast<size_t>(G) * n_pad * kD);
   _Float16* vt16 = ws.take<_Float16>(static_cast<size_t>(G) * n_pad * kD);
+  _Float16* q16 = ws.take<_Float16>(static_cast<size_t>(H) * n_pad * kD);
+  const Rope none{nullptr, nullptr, 0};
+  const bool fused = rope.cos != nullptr;
+  // with a fused RoPE, q and k are rotated on their way into the fp16 copies, and the query
+  // kernel reads q's copy (in the padded positions) in place of q
   Jobs jobs{};
-  jobs.job[0] = Job{k, sk_h, sk_t, k16, nullptr, nullptr, nullptr, 0, k_dtype, G};
-  jobs.job[1] = Job{v, sv_h, sv_t, nullptr, vt16, nullptr, nullptr, 0, v_dtype, G};
+  jobs.job[0] = Job{k, sk_h, sk_t, k16, nullptr, nullptr, nullptr, 0, k_dtype, G, rope};
+  jobs.job[1] = Job{v, sv_h, sv_t, nullptr, vt16, nullptr, nullptr, 0, v_dtype, G, none};
+  jobs.job[2] = Job{q, sq_h, sq_t, q16, nullptr, nullptr, nullptr, 0, q_dtype, H, rope};
   jobs.first[1] = G;
-  jobs.n = 2;
+  jobs.first[2] = 2 * G;
+  jobs.n = fused ? 3 : 2;
   const int n_blocks = static_cast<int>(n_pad / kBlk);
   const Rows* rows = static_cast<const Rows*>(rows_image);
   const int nt = static_cast<int>(n_tokens), np = static_cast<int>(n_pad);
-  hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * G), dim3(256), 0, s, jobs, rows,
-                     nt, np);
+  hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * G + (fused ? H : 0)), dim3(256), 0,
+                     s, jobs, rows, nt, np);
   if (int st = cm::launch_status()) return st;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(H, n_blocks), dim3(kThreads), 0, s, q, q_dtype, sq_h,
-                     sq_t, k16, vt16, rows, nt, np, H / G, H, scale * 1.4426950408889634f,
-                     static_cast<_Float16*>(out), lse2);
+  const void* qa = fused ? static_cast<const void*>(q16) : q;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(H, n_blocks), dim3(kThreads), 0, s, qa,
+                     fused ? CM_F16 : q_dtype, fused ? static_cast<int64_t>(n_pad) * kD : sq_h,
+                     fused ? static_cast<int64_t>(kD) : sq_t, k16, vt16, rows, nt, np, H / G, H,
+                     scale * 1.4426950408889634f, static_cast<_Float16*>(out), lse2,
+                     fused ? 1 : 0);
   return cm::launch_status();
 }
 
-extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+}  // namespace
+
+extern "C" int cm_attn_fwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
                            int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
-                           int64_t sv_h, int64_t sv_t, const void* out, const void* dout,
-                           const float* lse2, const void* rows_image, int64_t n_tokens,
-                           int64_t n_pad, int H, int G, int head_dim, float scale, void* dq,
-                           int dq_dtype, void* dk, void* dv, int dkv_dtype,
-                           int grads_token_major, void* workspace, int64_t workspace_bytes,
-                           void* stream) {
+                           int64_t sv_h, int64_t sv_t, const void* rows_image, int64_t n_tokens,
+                           int64_t n_pad, int H, int G, int head_dim, float scale, void* out,
+                           float* lse2, void* workspace, int64_t workspace_bytes, void* stream) {
+  return fwd_impl(q, q_dtype, sq_h, sq_t, k, k_dtype, sk_h, sk_t, v, v_dtype, sv_h, sv_t,
+                  Rope{nullptr, nullptr, 0}, rows_image, n_tokens, n_pad, H, G, head_dim, scale,
+                  out, lse2, workspace, workspace_bytes, stream);
+}
+
+extern "C" int cm_attn_fwd_rope(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t,
+                                const void* k, int k_dtype, int64_t sk_h, int64_t sk_t,
+                                const void* v, int v_dtype, int64_t sv_h, int64_t sv_t,
+                                const float* cos, const float* sin, int64_t cs_t,
+                                const void* rows_image, int64_t n_tokens, int64_t n_pad, int H,
+                                int G, int head_dim, float scale, void* out, float* lse2,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  CM_CHECK_ARG(cos != nullptr);
+  return fwd_impl(q, q_dtype, sq_h, sq_t, k, k_dtype, sk_h, sk_t, v, v_dtype, sv_h, sv_t,
+                  Rope{cos, sin, cs_t}, rows_image, n_tokens, n_pad, H, G, head_dim, scale, out,
+                  lse2, workspace, workspace_bytes, stream);
+}
+
+namespace {
+
+int bwd_impl(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k, int k_dtype,
+             int64_t sk_h, int64_t sk_t, const void* v, int v_dtype, int64_t sv_h, int64_t sv_t,
+             Rope rope, const void* out, const void* dout, const float* lse2,
+             const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G, int head_dim,
+             float scale, void* dq, int dq_dtype, void* dk, int dk_dtype, void* dv, int dv_dtype,
+             int grads_token_major, void* workspace, int64_t workspace_bytes, void* stream) {
   CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
   CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
                (v_dtype == CM_F32 || v_dtype == CM_F16));
   CM_CHECK_ARG((dq_dtype == CM_F32 || dq_dtype == CM_F16) &&
-               (dkv_dtype == CM_F32 || dkv_dtype == CM_F16));
+               (dk_dtype == CM_F32 || dk_dtype == CM_F16) &&
+               (dv_dtype == CM_F32 || dv_dtype == CM_F16));
+  CM_CHECK_ARG(rope_ok(rope));
   if (n_tokens == 0) return 0;
   CM_CHECK_ARG(rows_args_ok(rows_image, n_tokens, n_pad));
   CM_CHECK_ARG(q && k && v && out && dout && lse2 && dq && dk && dv && workspace);
@@ -850,9 +1015,12 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   Workspace ws{static_cast<char*>(workspace), 0, static_cast<size_t>(workspace_bytes)};
   const size_t nq = static_cast<size_t>(H) * n_pad * kD, nk = static_cast<size_t>(G) * n_pad * kD;
   _Float16* q16 = ws.take<_Float16>(nq);
-  _Float16* qt16 = ws.take<_Float16>(nq);
   _Float16* do16 = ws.take<_Float16>(nq);
+  // qt16 and dot16 are read by the dK/dV kernel only; with a fused RoPE the dQ kernel, which runs
+  // after it, writes its fp32 [H][n_pad][D] dq_rot over the two (adjacent: nq fp32 values)
+  _Float16* qt16 = ws.take<_Float16>(nq);
   _Float16* dot16 = ws.take<_Float16>(nq);
+  float* dq_rot = rope.cos != nullptr ? reinterpret_cast<float*>(qt16) : nullptr;
   _Float16* k16 = ws.take<_Float16>(nk);
   _Float16* v16 = ws.take<_Float16>(nk);
   _Float16* kt16 = ws.take<_Float16>(nk);
@@ -862,14 +1030,16 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
   const int np = static_cast<int>(n_pad), nt = static_cast<int>(n_tokens);
   const int n_blocks = np / kBlk;
   const Rows* rows = static_cast<const Rows*>(rows_image);
-  // dO and O: [N][H][D] contiguous (the forward's output layout)
+  const Rope none{nullptr, nullptr, 0};
+  // dO and O: [N][H][D] contiguous (the forward's output layout); q and k rotated again on the
+  // way when the RoPE is fused
   Jobs jobs{};
-  jobs.job[0] = Job{q, sq_h, sq_t, q16, qt16, nullptr, nullptr, 0, q_dtype, H};
+  jobs.job[0] = Job{q, sq_h, sq_t, q16, qt16, nullptr, nullptr, 0, q_dtype, H, rope};
   jobs.job[1] = Job{dout, kD, static_cast<int64_t>(H) * kD, do16, dot16,
                     static_cast<const _Float16*>(out), delta, static_cast<int64_t>(H) * kD,
-                    CM_F16, H};
-  jobs.job[2] = Job{k, sk_h, sk_t, k16, kt16, nullptr, nullptr, 0, k_dtype, G};
-  jobs.job[3] = Job{v, sv_h, sv_t, v16, nullptr, nullptr, nullptr, 0, v_dtype, G};
+                    CM_F16, H, none};
+  jobs.job[2] = Job{k, sk_h, sk_t, k16, kt16, nullptr, nullptr, 0, k_dtype, G, rope};
+  jobs.job[3] = Job{v, sv_h, sv_t, v16, nullptr, nullptr, nullptr, 0, v_dtype, G, none};
   jobs.first[1] = H;
   jobs.first[2] = 2 * H;
   jobs.first[3] = 2 * H + G;
@@ -882,24 +1052,65 @@ extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_
                      do16, dot16, k16, v16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
                      dk_part, dv_part);
   if (int st = cm::launch_status()) return st;
+  const int tm = grads_token_major ? 1 : 0;
   if (dq_dtype == CM_F32) {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(H, n_blocks), dim3(kThreads), 0, s, q16,
                        do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
-                       static_cast<float*>(dq), grads_token_major ? 1 : 0);
+                       static_cast<float*>(dq), tm, dq_rot);
   } else {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(H, n_blocks), dim3(kThreads), 0, s,
                        q16, do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
-                       static_cast<_Float16*>(dq), grads_token_major ? 1 : 0);
+                       static_cast<_Float16*>(dq), tm, dq_rot);
   }
   if (int st = cm::launch_status()) return st;
-  if (dkv_dtype == CM_F32) {
-    hipLaunchKernelGGL(attn_bwd_reduce_kernel<float>, dim3(np / 8, G), dim3(256), 0, s,
-                       dk_part, dv_part, rows, nt, np, H / G, static_cast<float*>(dk),
-                       static_cast<float*>(dv), grads_token_major ? 1 : 0);
+  const DqRope dqr{dq_rot, dq, dq_dtype == CM_F32 ? 1 : 0, H};
+  const int reduce_y = G + (dq_rot != nullptr ? H : 0);
+#define CM_ATTN_REDUCE(KT, VT)                                                                   \
+  hipLaunchKernelGGL((attn_bwd_reduce_kernel<KT, VT>), dim3(np / 8, reduce_y), dim3(256), 0, s,  \
+                     dk_part, dv_part, rows, nt, np, H / G, static_cast<KT*>(dk),               \
+                     static_cast<VT*>(dv), tm, rope, dqr)
+  if (dk_dtype == CM_F32 && dv_dtype == CM_F32) {
+    CM_ATTN_REDUCE(float, float);
+  } else if (dk_dtype == CM_F16 && dv_dtype == CM_F16) {
+    CM_ATTN_REDUCE(_Float16, _Float16);
+  } else if (dk_dtype == CM_F16) {
+    CM_ATTN_REDUCE(_Float16, float);
   } else {
-    hipLaunchKernelGGL(attn_bwd_reduce_kernel<_Float16>, dim3(np / 8, G), dim3(256), 0, s,
-                       dk_part, dv_part, rows, nt, np, H / G, static_cast<_Float16*>(dk),
-                       static_cast<_Float16*>(dv), grads_token_major ? 1 : 0);
+    CM_ATTN_REDUCE(float, _Float16);
   }
+#undef CM_ATTN_REDUCE
   return cm::launch_status();
+}
+
+}  // namespace
+
+extern "C" int cm_attn_bwd(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                           int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                           int64_t sv_h, int64_t sv_t, const void* out, const void* dout,
+                           const float* lse2, const void* rows_image, int64_t n_tokens,
+                           int64_t n_pad, int H, int G, int head_dim, float scale, void* dq,
+                           int dq_dtype, void* dk, void* dv, int dkv_dtype,
+                           int grads_token_major, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  return bwd_impl(q, q_dtype, sq_h, sq_t, k, k_dtype, sk_h, sk_t, v, v_dtype, sv_h, sv_t,
+                  Rope{nullptr, nullptr, 0}, out, dout, lse2, rows_image, n_tokens, n_pad, H, G,
+                  head_dim, scale, dq, dq_dtype, dk, dkv_dtype, dv, dkv_dtype, grads_token_major,
+                  workspace, workspace_bytes, stream);
+}
+
+extern "C" int cm_attn_bwd_rope(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t,
+                                const void* k, int k_dtype, int64_t sk_h, int64_t sk_t,
+                                const void* v, int v_dtype, int64_t sv_h, int64_t sv_t,
+                                const float* cos, const float* sin, int64_t cs_t,
+                                const void* out, const void* dout, const float* lse2,
+                                const void* rows_image, int64_t n_tokens, int64_t n_pad, int H,
+                                int G, int head_dim, float scale, void* dq, int dq_dtype,
+                                void* dk, int dk_dtype, void* dv, int dv_dtype,
+                                int grads_token_major, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  CM_CHECK_ARG(cos != nullptr);
+  return bwd_impl(q, q_dtype, sq_h, sq_t, k, k_dtype, sk_h, sk_t, v, v_dtype, sv_h, sv_t,
+                  Rope{cos, sin, cs_t}, out, dout, lse2, rows_image, n_tokens, n_pad, H, G,
+                  head_dim, scale, dq, dq_dtype, dk, dk_dtype, dv, dv_dtype, grads_token_major,
+                  workspace, workspace_bytes, stream);
 }

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 4
+#define CM_ABI_VERSION 5
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -357,9 +357,36 @@ int64_t cm_attn_padded_tokens(const int64_t* bounds, int n_rows);
 int64_t cm_attn_rows_bytes(void);
 int64_t cm_attn_rows_image(const int64_t* bounds, int n_rows, void* image);
 
-/* Workspace bytes of cm_attn_fwd (backward = 0) or cm_attn_bwd (backward = 1); -1 if the sizes
- * are unsupported. */
+/* Workspace bytes of cm_attn_fwd / cm_attn_fwd_rope (backward = 0) or cm_attn_bwd /
+ * cm_attn_bwd_rope (backward = 1); -1 if the sizes are unsupported. */
 int64_t cm_attn_workspace_bytes(int64_t n_pad, int H, int G, int head_dim, int backward);
+
+/* cm_attn_fwd / cm_attn_bwd with the rotary embedding fused in: q and k are the projections
+ * before the rotation (transformers' apply_rotary_pos_emb, which solution/rope.py:60-82 replaces,
+ * is then not called), rotated on their way into the kernels' fp16 copies of q and k, and the
+ * backward returns the gradients of the unrotated q and k (the transposed rotation applied to the
+ * gradients of the rotated ones in the launch that sums dK and dV). With h = D / 2 and c, s the
+ * token's cos / sin rows:
+ *   rotate:     o[d] = x[d] c[d] - x[d+h] s[d],   o[d+h] = x[d+h] c[d+h] + x[d] s[d+h]
+ *   transposed: o[d] = g[d] c[d] + g[d+h] s[d+h], o[d+h] = g[d+h] c[d+h] - g[d] s[d]
+ * in fp32 with each product rounded before the sum (the bits of cm_rope followed by the unfused
+ * entry). cos, sin: fp32 [N][head_dim] of the packed tokens, row stride cs_t (a multiple of 4,
+ * at least head_dim), 16-byte aligned. The backward writes dK and dV in their own dtypes
+ * (dk_dtype, dv_dtype). No counterpart in the reference, which launches its RoPE kernel apart. */
+int cm_attn_fwd_rope(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                     int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                     int64_t sv_h, int64_t sv_t, const float* cos, const float* sin, int64_t cs_t,
+                     const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G,
+                     int head_dim, float scale, void* out, float* lse2, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+int cm_attn_bwd_rope(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void* k,
+                     int k_dtype, int64_t sk_h, int64_t sk_t, const void* v, int v_dtype,
+                     int64_t sv_h, int64_t sv_t, const float* cos, const float* sin, int64_t cs_t,
+                     const void* out, const void* dout, const float* lse2,
+                     const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G,
+                     int head_dim, float scale, void* dq, int dq_dtype, void* dk, int dk_dtype,
+                     void* dv, int dv_dtype, int grads_token_major, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
 /* A rank-16 LoRA adapter on a frozen base projection, fused per token row: forward. Replaces,

@@ -289,3 +289,57 @@ def test_pack_batch_records_rows(dev):
     for s, e in zip(bounds[:-1], bounds[1:]):
         assert torch.equal(m[s:e, s:e], torch.ones(e - s, e - s, dtype=torch.bool).tril())
         assert not m[s:e, :s].any() and not m[s:e, e:].any()
+
+
+def _rope_tables(lengths, dev, dim=128, theta=1e6):
+    """cos / sin [1, N, D] fp32 of packed rows whose positions restart at 0 (Qwen2's rotary
+    embedding over packed position ids)."""
+    pos = torch.cat([torch.arange(n, dtype=torch.float32) for n in lengths])
+    inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    emb = torch.cat((pos[:, None] * inv, pos[:, None] * inv), -1)
+    return emb.cos()[None].to(dev), emb.sin()[None].to(dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lengths", [[154, 284, 482, 356], [1, 63, 64, 65, 128, 129], [700]],
+                         ids=["config5", "edges", "one_row"])
+@pytest.mark.parametrize("layout", ["step", "fp16"])
+def test_fused_rope_equals_rope_then_attention(dev, lengths, layout):
+    """cm_attn_fwd_rope / cm_attn_bwd_rope on q, k before the rotation against RoPE's kernel
+    followed by the attention on the rotated q, k: output and every gradient the same bits. The
+    step's layout: q fp32 and v fp32 views of the projection outputs [N, H * D], k fp16 (the
+    fused q/k/v block's outputs) under fp16 autocast; and all fp16."""
+    banner(f"fused rope attention {layout} {lengths}")
+    from claudemaxing_amd.attention import packed_causal_attention
+    from claudemaxing_amd.rope import rope
+
+    n = sum(lengths)
+    g = torch.Generator(device=dev).manual_seed(11)
+    dtq, dtk = (torch.float32, torch.float16) if layout == "step" else (torch.float16,) * 2
+    base_q = torch.randn(1, n, 12 * 128, generator=g, device=dev).to(dtq)
+    base_k = torch.randn(1, n, 2 * 128, generator=g, device=dev).to(dtk)
+    base_v = torch.randn(1, n, 2 * 128, generator=g, device=dev).to(dtq)
+    do = torch.randn(1, n, 12, 128, generator=g, device=dev).half()
+    cos, sin = _rope_tables(lengths, dev)
+    bounds = _bounds(lengths)
+
+    def leaves():
+        q = base_q.clone().requires_grad_()
+        k = base_k.clone().requires_grad_()
+        v = base_v.clone().requires_grad_()
+        view = lambda t, h: t.view(1, n, h, 128).transpose(1, 2)  # noqa: E731
+        return (q, k, v), (view(q, 12), view(k, 2), view(v, 2))
+
+    with torch.autocast("cuda", dtype=torch.float16, enabled=layout == "step"):
+        (q1, k1, v1), (qv, kv, vv) = leaves()
+        qr, kr = rope(qv, kv, cos, sin)
+        o1 = packed_causal_attention(qr, kr, vv, bounds)
+        torch.autograd.backward(o1, do)
+        (q2, k2, v2), (qv, kv, vv) = leaves()
+        o2 = packed_causal_attention(qv, kv, vv, bounds, cos=cos, sin=sin)
+        torch.autograd.backward(o2, do)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2), "out"
+    for a, b, name in ((q1, q2, "dq"), (k1, k2, "dk"), (v1, v2, "dv")):
+        assert a.grad.dtype == b.grad.dtype, name
+        assert torch.equal(a.grad, b.grad), (name, float((a.grad.float() - b.grad.float()).abs().max()))

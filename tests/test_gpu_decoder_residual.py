@@ -161,3 +161,41 @@ def test_patched_layer_equals_unfused_step(dev, monkeypatch):
     assert grads1.keys() == grads2.keys() and len(grads1) == 8
     for n in grads1:
         _same(grads1[n], grads2[n], n)
+
+
+def test_fused_rope_step_equals_separate_rope(dev, monkeypatch):
+    """The training step with the rotary embedding inside the native attention and with RoPE's
+    own launches (qkv.FUSE_ROPE off): the same loss and LoRA gradients, bit for bit; the fused
+    run took the fused attention in both layers."""
+    banner("fused rope attention: 2-layer step, fused vs separate RoPE")
+    from claudemaxing_amd import attention as A
+    from claudemaxing_amd import qkv
+
+    # LoRA dropout on (the fused q/k/v block's layout), the same draws in both runs
+    model = qlora_step.build_model(dev, seed=0, num_hidden_layers=2)
+    g = torch.Generator(device=dev).manual_seed(1)
+    for n, p in model.named_parameters():
+        if "lora_B" in n:
+            p.data = torch.randn(p.shape, generator=g, device=dev) * 0.02
+    batch, _ = qlora_step.make_batch(dev, seed=3)
+    fused = []
+    real = A.packed_causal_attention
+
+    def counting(*args, **kwargs):
+        fused.append(kwargs.get("cos") is not None)
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(A, "packed_causal_attention", counting)
+    monkeypatch.setattr(qkv, "FUSE_ROPE", True)
+    torch.manual_seed(5)
+    loss1, grads1 = _loss_and_grads(model, batch)
+    assert fused == [True, True], fused
+    monkeypatch.setattr(qkv, "FUSE_ROPE", False)
+    fused.clear()
+    torch.manual_seed(5)
+    loss2, grads2 = _loss_and_grads(model, batch)
+    assert fused == [False, False], fused
+    torch.cuda.synchronize()
+    _same(loss1, loss2, "loss")
+    for n in grads1:
+        _same(grads1[n], grads2[n], n)
