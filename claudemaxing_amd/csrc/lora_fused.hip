@@ -492,17 +492,25 @@ extern "C" int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const flo
 // rows of outer(W[t], R[t]), W [T, D] fp16 (row stride ldw), R [T, 16] fp16, in fp32:
 //   lora_A's gradient  ga16^T xd16 : W = xd16 (D = K), R = ga16, out [16, K]  (rank-major)
 //   lora_B's gradient  g16^T a16   : W = g16  (D = N), R = a16,  out [N, 16]  (column-major)
-// The reference computes each as a GEMM over the tokens (solution/lora.py:96-107). A workgroup
-// of 256 lanes takes 512 columns of W and a slice of the tokens: the slice's R rows are staged
-// in the LDS (read back as broadcasts), each lane owns two columns and keeps their 2 x 16 sums,
-// loading its W pairs for 16 tokens at a time before using them. The partial sums of each slice
-// go to a workspace and a second kernel adds the slices in slice order (deterministic).
+// The reference computes each as a GEMM over the tokens (solution/lora.py:96-107). Here one
+// workgroup takes 32 columns of one job over all the tokens: a product out[16 ranks x 16 columns]
+// is v_mfma_f32_16x16x32_f16 steps of 32 tokens with the ranks as the left operand (R^T) and the
+// columns as the right one (W), the tokens being the contraction, so that no lane needs another
+// lane's data. Lane l supplies rank l % 16 and the column pair col0 + 2 (l % 16) .. +1 (the even
+// column to the first tile, the odd one to the second) over the 8 tokens 8 (l / 16) .. +7 of a
+// step: 2- and 4-byte loads whose 16 lanes of a group read 32 or 64 contiguous bytes of one token
+// row (a load instruction's cost is per lane, not per byte, at these widths). The 8
+// wavefronts take the steps in turn (step s on wavefront s % 8), each loading several steps
+// before it multiplies them, and their 16 x 16 sums are added through the LDS in a fixed order:
+// one launch, no workspace, and the same inputs give the same bits. The products of two fp16
+// values are exact in fp32, so the sums differ from a GEMM's only in their order.
 namespace {
 
 constexpr int kWgJobs = 4;
-constexpr int kWgCols = 2 * 256;   // columns of W per workgroup
-constexpr int kWgBatch = 32;       // tokens loaded per batch
-constexpr int kWgMaxSlice = 128;   // tokens per slice at most (LDS: 128 x 32 B)
+constexpr int kWgCols = 32;    // columns of W per workgroup: two 16-column MFMA tiles
+constexpr int kWgWaves = 8;    // wavefronts per workgroup, splitting the tokens
+constexpr int kWgBatch = 2;    // 32-token steps a wavefront loads before it multiplies them
+                               // (2 to 5 measured: 2 and 3 fastest at 1276 and 5000 tokens)
 
 struct WgJob {
   const _Float16* w;
@@ -516,104 +524,88 @@ struct WgJobs {
   WgJob j[kWgJobs];
 };
 
-__global__ __launch_bounds__(256) void lora_wgrad_partial(WgJobs jobs, int T, int t_slice,
-                                                          float* __restrict__ ws,
-                                                          int64_t ws_slice, int64_t ws_job) {
-  // fused multiply-adds here: these are sums of fp32 products like the GEMM they replace (the
-  // rounding points the adapter's values follow are elsewhere in this file)
-#pragma clang fp contract(fast)
-  __shared__ float4 s_r[kWgMaxSlice][kR / 4];  // the slice's R rows, widened once
-  const WgJob jb = jobs.j[blockIdx.z];
+__global__ __launch_bounds__(kWgWaves * cm::kWave) void lora_wgrad_kernel(WgJobs jobs,
+                                                                           int64_t T) {
+  __shared__ acc4 s_part[kWgWaves][2][cm::kWave];
+  const WgJob jb = jobs.j[blockIdx.y];
   const int col0 = blockIdx.x * kWgCols;
   if (col0 >= jb.d) return;  // this job has fewer columns (uniform per workgroup)
-  const int t0 = blockIdx.y * t_slice, n_t = max(0, min(T - t0, t_slice));
-  for (int i = threadIdx.x; i < 4 * n_t; i += blockDim.x) {
-    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
-    const half4v h = *reinterpret_cast<const half4v*>(jb.r + static_cast<int64_t>(t0 + i / 4) * kR + 4 * (i % 4));
-    s_r[i / 4][i % 4] = make_float4(static_cast<float>(h[0]), static_cast<float>(h[1]),
-                                    static_cast<float>(h[2]), static_cast<float>(h[3]));
-  }
-  const int d = col0 + 2 * threadIdx.x;
-  const bool ok = d < jb.d;  // d even, D a multiple of 8: both columns in range
-  const int dc = ok ? d : jb.d - 2;
-  float acc[2][kR];
+  const int lane = threadIdx.x % cm::kWave, wave = wave_index();
+  const int c16 = lane % 16, grp = lane / 16;
+  // the lane's column pair, clamped into the row (D is a multiple of 8, so a pair is whole;
+  // columns past D are not stored)
+  const int dc = min(col0 + 2 * c16, jb.d - 2);
+  const int64_t steps = (T + 31) / 32;
+  acc4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  for (int64_t s0 = wave; s0 < steps; s0 += kWgWaves * kWgBatch) {
+    _Float16 rv[kWgBatch][8];
+    uint32_t wv[kWgBatch][8];
+    // every load first (rows past T clamped to T - 1 and their values zeroed after the loads)
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+    for (int b = 0; b < kWgBatch; ++b) {
 #pragma unroll
-    for (int r = 0; r < kR; ++r) acc[c][r] = 0.0f;
-  __syncthreads();
-  for (int tb = 0; tb < n_t; tb += kWgBatch) {
-    uint32_t wv[kWgBatch];
-#pragma unroll
-    for (int i = 0; i < kWgBatch; ++i) {
-      const int t = min(tb + i, n_t - 1);  // clamped: the extra tokens are not added
-      wv[i] = *reinterpret_cast<const uint32_t*>(jb.w + static_cast<int64_t>(t0 + t) * jb.ldw + dc);
-    }
-#pragma unroll
-    for (int i = 0; i < kWgBatch; ++i) {
-      if (tb + i >= n_t) break;
-      const float w0 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(wv[i])));
-      const float w1 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(wv[i] >> 16)));
-#pragma unroll
-      for (int q = 0; q < kR / 4; ++q) {
-        const float4 rv = s_r[tb + i][q];
-        const float rr[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[0][4 * q + e] += w0 * rr[e];
-          acc[1][4 * q + e] += w1 * rr[e];
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int64_t t = min((s0 + kWgWaves * b) * 32 + 8 * grp + e, T - 1);
+        rv[b][e] = jb.r[t * kR + c16];
+        wv[b][e] = *reinterpret_cast<const uint32_t*>(jb.w + t * jb.ldw + dc);
       }
     }
+#pragma unroll
+    for (int b = 0; b < kWgBatch; ++b) {
+      const int64_t s = s0 + kWgWaves * b;
+      if (s >= steps) break;
+      half8 ra, wa, wb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool in = s * 32 + 8 * grp + e < T;
+        const _Float16 lo = __builtin_bit_cast(_Float16, static_cast<uint16_t>(wv[b][e]));
+        const _Float16 hi = __builtin_bit_cast(_Float16, static_cast<uint16_t>(wv[b][e] >> 16));
+        ra[e] = in ? rv[b][e] : static_cast<_Float16>(0.0f);
+        wa[e] = in ? lo : static_cast<_Float16>(0.0f);
+        wb[e] = in ? hi : static_cast<_Float16>(0.0f);
+      }
+      acc0 = mfma_k32(ra, wa, acc0);
+      acc1 = mfma_k32(ra, wb, acc1);
+    }
   }
-  if (!ok) return;
-  // partial of slice blockIdx.y, rank-major [16][D]
-  float* p = ws + blockIdx.z * ws_job + blockIdx.y * ws_slice;
+  s_part[wave][0][lane] = acc0;
+  s_part[wave][1][lane] = acc1;
+  __syncthreads();
+  if (wave >= 2) return;
+  // wavefront v adds tile v over the 8 wavefronts; lane l holds ranks 4 (l / 16) .. +3 of
+  // column col0 + 2 (l % 16) + v
+  const int d = col0 + 2 * c16 + wave;
+  acc4 sum;
 #pragma unroll
-  for (int r = 0; r < kR; ++r)
-    *reinterpret_cast<float2*>(p + static_cast<int64_t>(r) * jb.d + d) = make_float2(acc[0][r], acc[1][r]);
-}
-
-// out element (r, d) of job blockIdx.y = the slices' partials added in slice order.
-__global__ __launch_bounds__(256) void lora_wgrad_sum(WgJobs jobs, int n_slices,
-                                                      const float* __restrict__ ws,
-                                                      int64_t ws_slice, int64_t ws_job) {
-  const WgJob jb = jobs.j[blockIdx.y];
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= static_cast<int64_t>(kR) * jb.d) return;
-  const float* p = ws + blockIdx.y * ws_job + i;
-  float s = 0.0f;  // no tokens: a zero gradient
-  // 8 slices loaded before they are added (in slice order): one wait per 8, not per slice
-  for (int k0 = 0; k0 < n_slices; k0 += 8) {
-    float v[8];
+  for (int i = 0; i < 4; ++i) {
+    float v[kWgWaves];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = k0 + k < n_slices ? p[(k0 + k) * ws_slice] : 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k0 + k < n_slices) s += v[k];
+    for (int w = 0; w < kWgWaves; ++w) v[w] = s_part[w][wave][lane][i];
+    sum[i] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
   }
-  const int r = static_cast<int>(i / jb.d), dd = static_cast<int>(i % jb.d);
-  jb.out[jb.d_major ? static_cast<int64_t>(dd) * kR + r : i] = s;
-}
-
-int wgrad_slices(int64_t T) {
-  // about 2 workgroups per CU over the jobs' column blocks, slices of at most 128 tokens
-  int s = 32;
-  while ((T + s - 1) / s > kWgMaxSlice) s *= 2;
-  return s;
+  if (d >= jb.d) return;
+  if (jb.d_major) {
+    *reinterpret_cast<float4*>(jb.out + static_cast<int64_t>(d) * kR + 4 * grp) =
+        make_float4(sum[0], sum[1], sum[2], sum[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) jb.out[static_cast<int64_t>(4 * grp + i) * jb.d + d] = sum[i];
+  }
 }
 
 }  // namespace
 
 extern "C" int64_t cm_lora_weight_grads_workspace_bytes(int64_t T, int max_d, int n_jobs) {
   if (T < 0 || max_d <= 0 || n_jobs < 1 || n_jobs > kWgJobs) return -1;
-  return static_cast<int64_t>(wgrad_slices(T)) * n_jobs * kR * max_d * 4;
+  return 0;  // one launch, its sums in the LDS
 }
 
 extern "C" int cm_lora_weight_grads(const void* const* w, const int64_t* ldw, const int* d,
                                     const void* const* r, float* const* out,
                                     const int* d_major, int n_jobs, int64_t T, int rank,
                                     void* workspace, int64_t ws_bytes, void* stream) {
+  (void)workspace;
+  (void)ws_bytes;
   CM_CHECK_ARG(rank == kR && n_jobs >= 1 && n_jobs <= kWgJobs && T >= 0);
   CM_CHECK_ARG(w && ldw && d && r && out && d_major);
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
@@ -624,25 +616,13 @@ extern "C" int cm_lora_weight_grads(const void* const* w, const int64_t* ldw, co
     CM_CHECK_ARG((T == 0 || (w[q] && r[q])) && out[q] && d[q] > 0 && d[q] % 8 == 0 &&
                  ldw[q] >= d[q] && ldw[q] % 2 == 0);
     CM_CHECK_ARG((reinterpret_cast<uintptr_t>(w[q]) & 3) == 0 && aligned(r[q], 16) &&
-                 aligned(out[q], 4));
+                 aligned(out[q], d_major[q] ? 16 : 4));
     jobs.j[q] = WgJob{static_cast<const _Float16*>(w[q]), ldw[q],
                       static_cast<const _Float16*>(r[q]), out[q], d[q], d_major[q] ? 1 : 0};
     max_d = std::max(max_d, d[q]);
   }
-  const int S = wgrad_slices(T);
-  const int64_t ws_slice = static_cast<int64_t>(kR) * max_d, ws_job = S * ws_slice;
-  CM_CHECK_ARG(workspace && aligned(workspace, 16) && ws_bytes >= n_jobs * ws_job * 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* ws = static_cast<float*>(workspace);
-  const int t_slice = static_cast<int>((T + S - 1) / S);
-  if (T == 0) {
-    hipLaunchKernelGGL(lora_wgrad_sum, dim3(static_cast<unsigned>((kR * max_d + 255) / 256), n_jobs),
-                       dim3(256), 0, s, jobs, 0, ws, ws_slice, ws_job);
-    return cm::launch_status();
-  }
-  hipLaunchKernelGGL(lora_wgrad_partial, dim3((max_d + kWgCols - 1) / kWgCols, S, n_jobs),
-                     dim3(256), 0, s, jobs, static_cast<int>(T), t_slice, ws, ws_slice, ws_job);
-  hipLaunchKernelGGL(lora_wgrad_sum, dim3(static_cast<unsigned>((kR * max_d + 255) / 256), n_jobs),
-                     dim3(256), 0, s, jobs, S, ws, ws_slice, ws_job);
+  hipLaunchKernelGGL(lora_wgrad_kernel, dim3((max_d + kWgCols - 1) / kWgCols, n_jobs),
+                     dim3(kWgWaves * cm::kWave), 0, s, jobs, T);
   return cm::launch_status();
 }

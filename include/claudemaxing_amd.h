@@ -59,11 +59,11 @@ int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nested, const 
 /* The adapters' weight gradients, up to 4 at once: job q computes sum over the T token rows of
  * outer(w_q[t], r_q[t]) in fp32, w_q [T, d_q] fp16 (row stride ldw_q, even; d_q a multiple of 8;
  * 4-byte aligned), r_q [T, rank] fp16 contiguous (16-byte aligned), into out_q: [rank, d_q] when
- * d_major_q = 0 (lora_A's gradient ga16^T xd16: w = xd16, r = ga16), [d_q, rank] when 1
- * (lora_B's gradient g16^T a16: w = g16, r = a16). Replaces the token-sum GEMMs of
- * LoRABranch.backward (solution/lora.py:96-107). Partial sums per token slice go to
- * `workspace` (cm_lora_weight_grads_workspace_bytes(T, max d_q, n_jobs) bytes, 16-byte aligned)
- * and are added in slice order: deterministic. rank must be 16. */
+ * d_major_q = 0 (lora_A's gradient ga16^T xd16: w = xd16, r = ga16; out 4-byte aligned),
+ * [d_q, rank] when 1 (lora_B's gradient g16^T a16: w = g16, r = a16; out 16-byte aligned).
+ * Replaces the token-sum GEMMs of LoRABranch.backward (solution/lora.py:96-107). One launch;
+ * the sums are formed in a fixed order (the same inputs give the same bits). The workspace
+ * query returns 0 and `workspace` is not used (it may be null). rank must be 16. */
 int64_t cm_lora_weight_grads_workspace_bytes(int64_t T, int max_d, int n_jobs);
 int cm_lora_weight_grads(const void* const* w, const int64_t* ldw, const int* d,
                          const void* const* r, float* const* out, const int* d_major, int n_jobs,

@@ -197,18 +197,17 @@ def test_nf4_linear_argument_checks(lib):
     assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, None, o, w, big, None) == INVALID
     assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, w + 8, o, w, big, None) == INVALID
     # batched adapter weight gradients: 1..4 jobs, rank 16, widths multiples of 8, even strides,
-    # a large enough workspace
+    # aligned outputs; one launch without a workspace
     P, L, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     wg, wgws = lib.cm_lora_weight_grads, lib.cm_lora_weight_grads_workspace_bytes
-    assert wgws(1276, 1536, 4) == 32 * 4 * 16 * 1536 * 4 and wgws(1276, 1536, 5) == -1
-    jobs = lambda d, ldw: ((P * 1)(0x10000), (L * 1)(ldw), (I * 1)(d), (P * 1)(0x20000),
-                           (P * 1)(0x30000), (I * 1)(0))
-    ok_ws = wgws(64, 1536, 1)
-    assert wg(*jobs(1536, 1536), 0, 64, 16, 0x40000, ok_ws, None) == INVALID  # no jobs
-    assert wg(*jobs(1536, 1536), 1, 64, 8, 0x40000, ok_ws, None) == INVALID  # rank 8
-    assert wg(*jobs(1532, 1536), 1, 64, 16, 0x40000, ok_ws, None) == INVALID  # width % 8
-    assert wg(*jobs(1536, 1535), 1, 64, 16, 0x40000, ok_ws, None) == INVALID  # stride < width
-    assert wg(*jobs(1536, 1536), 1, 64, 16, 0x40000, ok_ws - 4, None) == INVALID  # workspace
+    assert wgws(1276, 1536, 4) == 0 and wgws(1276, 1536, 5) == -1 and wgws(-1, 1536, 1) == -1
+    jobs = lambda d, ldw, out=0x30000, major=0: ((P * 1)(0x10000), (L * 1)(ldw), (I * 1)(d),
+                                                 (P * 1)(0x20000), (P * 1)(out), (I * 1)(major))
+    assert wg(*jobs(1536, 1536), 0, 64, 16, None, 0, None) == INVALID  # no jobs
+    assert wg(*jobs(1536, 1536), 1, 64, 8, None, 0, None) == INVALID  # rank 8
+    assert wg(*jobs(1532, 1536), 1, 64, 16, None, 0, None) == INVALID  # width % 8
+    assert wg(*jobs(1536, 1535), 1, 64, 16, None, 0, None) == INVALID  # stride < width
+    assert wg(*jobs(1536, 1536, 0x30008, 1), 1, 64, 16, None, 0, None) == INVALID  # [d, 16] out
     # scale map: blocksize must divide the columns; NULL output
     assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536, 4096)), 0x50000, None) == INVALID
     assert lib.cm_nf4_scale_map(Arr(_nf4_weight(256, 1536)), None, None) == INVALID
