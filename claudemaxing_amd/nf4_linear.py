@@ -133,10 +133,12 @@ def _weights(pairs):
 # dequant kernel and multiply with torch's GEMM. The fused kernel expands every weight element
 # once per token tile (256 tokens), at ~4.6 VALU operations per element; the dequant kernel
 # expands each element once, and the GEMM then runs at the library's rate. Measured on MI355X
-# at 1276 tokens (fused vs dequant + GEMM): k/v projections 21 vs 30 us forward, 16 vs 30 us
-# backward; q/o 26 vs 30 us forward, 30 vs 30 us backward; gate+up 122 vs 101 us; down 78 vs
-# 71 us forward, 90 vs 48 us backward; the MLP input gradient 191 vs 186 us.
-FUSED_MAX_FLOPS = 8.0e9
+# at 1276 tokens, fused vs dequant + GEMM: k/v projections 21 vs 30 us forward, 16 vs 30 us
+# backward (back-to-back calls, launch gaps included); gate+up 122 vs 101 us; down 78 vs 71 us
+# forward, 90 vs 48 us backward; the MLP input gradient 191 vs 186 us. The o projection (6
+# GFLOP) in the graphed training step's kernel trace: 25.2 vs 23.0 us forward (fp32 output,
+# the split-K partial sum included), 32.0 vs 24.5 us backward.
+FUSED_MAX_FLOPS = 4.0e9
 
 
 def fused_pays(m, n, k):

@@ -83,10 +83,19 @@ def test_fused_adapter_matches(dev, rows, out_f):
     assert fused[0].dtype == torch.float32 and fused[1].dtype == torch.float32
     for name, a, b, c in zip(("out", "dx", "dA", "dB"), fused, unfused, ref):
         _check(name, a, b, c)
-    # most outputs agree bit for bit with the unfused path
+    # most outputs agree bit for bit with the unfused path where both run the base product on
+    # the fused NF4 GEMM (an fp16 result); above fused_pays' bound the unfused NF4Linear writes
+    # its fp32 output straight from the GEMM (no fp16 rounding), so there the two agree to fp16
+    # precision of the output's scale
+    from claudemaxing_amd.nf4_linear import fused_pays
+
     same = float((fused[0] == unfused[0]).float().mean())
     print(f"  identical outputs: {100 * same:.1f}%")
-    assert same > 0.9
+    if fused_pays(rows, out_f, 1536):
+        assert same > 0.9
+    else:
+        diff = float((fused[0] - unfused[0]).abs().max())
+        assert diff <= 2.0 ** -10 * float(unfused[0].abs().max()), diff
 
 
 @pytest.mark.gpu
