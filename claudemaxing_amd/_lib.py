@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -62,6 +62,7 @@ SIGNATURES = {
     "cm_lora_weight_grads_workspace_bytes": (_L, [_L, _I, _I]),
     "cm_lora_weight_grads": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _I, _P, _L, _P]),
     "cm_gemm_f32": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _L, _P]),
+    "cm_gemm_f32_kb": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _L, _P]),
     "cm_gemm_f32_add": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P, _P, _P, _L,
                              _P]),
     "cm_rmsnorm_fwd": (_I, [_P, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P, _I, _L, _I, _F, _P]),

@@ -10,11 +10,17 @@
 // global -> LDS loads, v_mfma_f32_32x32x16_f16) over its slice and writes its fp32 partial tile
 // to a workspace slice, and a second kernel adds the slices in slice order (deterministic: the
 // same inputs give the same bits). The workspace is S x M x N fp32.
+//
+// B may also be given k-major (cm_gemm_f32_kb: B[n][k] at b[k * ldb + n], a weight as stored
+// for the input gradient dX = G W): its LDS tiles are then read with transposing fragment reads
+// that hand each lane the same (n, k) elements as the row-major path, so the two give the same
+// bits for the same values.
 #include "gemm_lds.h"
 
 namespace {
 
 using cm::gemm::floatx16;
+using cm::gemm::KMajor;
 using cm::gemm::RowMajor;
 
 constexpr int kBM = 256, kBN = 192, kWM = 4, kWN = 2, kBK = 64, kStages = 2;
@@ -54,10 +60,12 @@ struct EpiSlice {
 
 struct Pairs {
   RowMajor a[2], b[2];
+  KMajor bk[2];     // B of each pair when the kernel takes it k-major
   int slices0;      // slices of pair 0; the rest belong to pair 1
   int k_slice[2];   // columns per slice of each pair (a multiple of 64)
 };
 
+template <bool KB>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(Pairs p, int remap, float* ws,
                                                                int M, int N) {
   __shared__ uint4 lds[kStages * (kBM + kBN) * (kBK / 8)];
@@ -68,12 +76,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(Pairs p, int rema
   // an empty slice still writes its (zero) partial tile, which the sum then reads
   const int k_end = max(k_begin, min(p.a[q].k_len, k_begin + p.k_slice[q]));
   EpiSlice epi{ws + static_cast<int64_t>(s) * M * N, M, N};
-  if (q == 0) {
-    cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[0], p.b[0], k_begin, k_end, tm, tn,
-                                                         epi, lds);
+  if constexpr (KB) {
+    if (q == 0) {
+      cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[0], p.bk[0], k_begin, k_end, tm,
+                                                           tn, epi, lds);
+    } else {
+      cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[1], p.bk[1], k_begin, k_end, tm,
+                                                           tn, epi, lds);
+    }
   } else {
-    cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[1], p.b[1], k_begin, k_end, tm, tn,
-                                                         epi, lds);
+    if (q == 0) {
+      cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[0], p.b[0], k_begin, k_end, tm,
+                                                           tn, epi, lds);
+    } else {
+      cm::gemm::gemm_lds<kBM, kBN, kWM, kWN, kBK, kStages>(p.a[1], p.b[1], k_begin, k_end, tm,
+                                                           tn, epi, lds);
+    }
   }
 }
 
@@ -152,12 +170,17 @@ namespace {
 int gemm_f32_impl(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
                   const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M,
                   int N, const float* residual, float* out, void* workspace, int64_t ws_bytes,
-                  void* stream) {
+                  void* stream, bool b_kmajor = false) {
   CM_CHECK_ARG(shape_ok(M, N, K0, K1));
   if (M == 0 || N == 0) return 0;
   CM_CHECK_ARG(a0 && b0 && out && workspace && (K1 == 0 || (a1 && b1)));
-  CM_CHECK_ARG(lda0 >= K0 && ldb0 >= K0 && lda0 % 8 == 0 && ldb0 % 8 == 0);
-  CM_CHECK_ARG(K1 == 0 || (lda1 >= K1 && ldb1 >= K1 && lda1 % 8 == 0 && ldb1 % 8 == 0));
+  // B's rows: K of them of N values when k-major (N a multiple of 8: whole 16-byte chunks), else
+  // N rows of K
+  const int64_t b_row = b_kmajor ? N : 0;
+  CM_CHECK_ARG(!b_kmajor || N % 8 == 0);
+  CM_CHECK_ARG(lda0 >= K0 && lda0 % 8 == 0 && ldb0 % 8 == 0 && ldb0 >= (b_kmajor ? b_row : K0));
+  CM_CHECK_ARG(K1 == 0 || (lda1 >= K1 && lda1 % 8 == 0 && ldb1 % 8 == 0 &&
+                           ldb1 >= (b_kmajor ? b_row : K1)));
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   CM_CHECK_ARG(al16(a0) && al16(b0) && al16(out) && al16(workspace) &&
                (K1 == 0 || (al16(a1) && al16(b1))) && (!residual || al16(residual)));
@@ -169,6 +192,8 @@ int gemm_f32_impl(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, in
   p.b[0] = RowMajor{static_cast<const _Float16*>(b0), ldb0, N, K0};
   p.a[1] = K1 ? RowMajor{static_cast<const _Float16*>(a1), lda1, M, K1} : p.a[0];
   p.b[1] = K1 ? RowMajor{static_cast<const _Float16*>(b1), ldb1, N, K1} : p.b[0];
+  p.bk[0] = KMajor{static_cast<const _Float16*>(b0), ldb0, N, K0};
+  p.bk[1] = K1 ? KMajor{static_cast<const _Float16*>(b1), ldb1, N, K1} : p.bk[0];
   p.slices0 = pl.slices[0];
   p.k_slice[0] = pl.k_slice[0];
   p.k_slice[1] = pl.k_slice[1];
@@ -176,8 +201,13 @@ int gemm_f32_impl(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, in
   const int remap = (tiles * pl.total()) % 8 == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(gemm_f32_kernel, dim3(tiles, pl.total()), dim3(kThreads), 0, s, p, remap, ws,
-                     M, N);
+  if (b_kmajor) {
+    hipLaunchKernelGGL(gemm_f32_kernel<true>, dim3(tiles, pl.total()), dim3(kThreads), 0, s, p,
+                       remap, ws, M, N);
+  } else {
+    hipLaunchKernelGGL(gemm_f32_kernel<false>, dim3(tiles, pl.total()), dim3(kThreads), 0, s, p,
+                       remap, ws, M, N);
+  }
   const int64_t n4 = static_cast<int64_t>(M) * N / 4;
   hipLaunchKernelGGL(gemm_f32_sum, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, s,
                      reinterpret_cast<const float4*>(ws), pl.total(), n4,
@@ -202,4 +232,12 @@ extern "C" int cm_gemm_f32_add(const void* a0, int64_t lda0, const void* b0, int
   CM_CHECK_ARG(M == 0 || N == 0 || residual != nullptr);
   return gemm_f32_impl(a0, lda0, b0, ldb0, K0, a1, lda1, b1, ldb1, K1, M, N, residual, out,
                        workspace, ws_bytes, stream);
+}
+
+extern "C" int cm_gemm_f32_kb(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                              const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1,
+                              int M, int N, float* out, void* workspace, int64_t ws_bytes,
+                              void* stream) {
+  return gemm_f32_impl(a0, lda0, b0, ldb0, K0, a1, lda1, b1, ldb1, K1, M, N, nullptr, out,
+                       workspace, ws_bytes, stream, true);
 }

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 5
+#define CM_ABI_VERSION 6
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -92,6 +92,14 @@ int cm_gemm_f32_add(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, 
                     const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M,
                     int N, const float* residual, float* out, void* workspace, int64_t ws_bytes,
                     void* stream);
+/* cm_gemm_f32 with each B_q given k-major: element (n, k) of B_q at b_q[k * ldb_q + n] (ldb_q >=
+ * N, a multiple of 8; N a multiple of 8), i.e. a weight W_q [K_q, N] as stored, so that
+ * out = sum_q A_q W_q (the MLP input gradient dgate Wg + dup Wu on the weights expanded by
+ * cm_nf4_dequant, without a transposed copy). The same bits as cm_gemm_f32 on the transposed
+ * operands. Same workspace query. No counterpart in the reference (a layout of the operand). */
+int cm_gemm_f32_kb(const void* a0, int64_t lda0, const void* b0, int64_t ldb0, int K0,
+                   const void* a1, int64_t lda1, const void* b1, int64_t ldb1, int K1, int M,
+                   int N, float* out, void* workspace, int64_t ws_bytes, void* stream);
 
 /* The same expansion written transposed, fp16 only: out[c][r] = W[r][c] for the weight W
  * [rows, cols] (rows a multiple of 64, cols of 128; packed 4-byte, out 16-byte aligned), the values

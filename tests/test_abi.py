@@ -196,6 +196,11 @@ def test_nf4_linear_argument_checks(lib):
     ga = lib.cm_gemm_f32_add  # the residual is required and 16-byte aligned
     assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, None, o, w, big, None) == INVALID
     assert ga(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 64, w + 8, o, w, big, None) == INVALID
+    gk = lib.cm_gemm_f32_kb  # B [K, N]: its row stride is at least N, N a multiple of 8
+    assert gk(a, 64, b, 56, 64, None, 0, None, 0, 0, 64, 64, o, w, big, None) == INVALID
+    bigk = gws(64, 60, 64, 0)
+    assert gk(a, 64, b, 64, 64, None, 0, None, 0, 0, 64, 60, o, w, bigk, None) == INVALID
+    assert gk(a, 64, b, 64, 64, None, 0, None, 0, 0, 0, 64, o, w, 0, None) == 0
     # batched adapter weight gradients: 1..4 jobs, rank 16, widths multiples of 8, even strides,
     # aligned outputs; one launch without a workspace
     P, L, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int

@@ -85,3 +85,39 @@ def test_residual_added_in_the_sum_launch(m, k0, k1, dev):
     assert torch.equal(got, want)
     with pytest.raises(ValueError):
         gemm_f32(*pairs, residual=res.t().contiguous().t())  # not contiguous
+
+
+@pytest.mark.parametrize("m,n,k0,k1", [(1276, 1536, 8960, 8960), (300, 200, 1032, 264),
+                                       (37, 896, 4864, 0), (8, 8, 8, 0), (513, 1544, 72, 136)])
+def test_kmajor_b_equals_rowmajor_on_the_transpose(m, n, k0, k1, dev):
+    """cm_gemm_f32_kb (B given [K, N], a weight as stored) gives the bits of cm_gemm_f32 on the
+    transposed operands (the same elements reach the same lanes in the same k order), and
+    matches fp64; edge tiles in n and k, one or two pairs."""
+    banner(f"gemm_f32 k-major B m={m} n={n} k0={k0} k1={k1}")
+    a0, bt0 = _pair(m, n, k0, dev, 7)
+    b0 = bt0.t().contiguous()  # [K0, N]
+    pairs_kb, pairs_rm = [(a0, b0)], [(a0, bt0)]
+    ref = a0.double() @ b0.double()
+    if k1:
+        a1, bt1 = _pair(m, n, k1, dev, 8)
+        b1 = bt1.t().contiguous()
+        pairs_kb.append((a1, b1))
+        pairs_rm.append((a1, bt1))
+        ref = ref + a1.double() @ b1.double()
+    assert gemm_f32_supported(m, n, *pairs_kb, b_kmajor=True)
+    out = gemm_f32(*pairs_kb, b_kmajor=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, gemm_f32(*pairs_rm))
+    _check(out, ref, "k-major B")
+
+
+def test_kmajor_b_row_stride(dev):
+    """A k-major B whose rows are a column block of a wider matrix (ldb > N)."""
+    a, bt = _pair(96, 64, 2048, dev, 9)
+    wide = torch.zeros(2048, 64 + 32, device=dev, dtype=torch.float16)
+    wide[:, :64] = bt.t()
+    b = wide[:, :64]
+    assert b.stride(0) == 96 and gemm_f32_supported(96, 64, (a, b), b_kmajor=True)
+    out = gemm_f32((a, b), b_kmajor=True)
+    assert torch.equal(out, gemm_f32((a, bt)))
+    assert not gemm_f32_supported(96, 60, (a, b[:, :60]), b_kmajor=True)  # N % 8
