@@ -556,10 +556,10 @@ def k_nf4_linear(dev, names):
             torch.addmm(torch.mm(gd, wg), gd, wu)
 
         def split_b(pairs=pairs, gd=gd):
-            # the training step's path: each weight expanded transposed, then one split-K launch
-            # over both products with an fp32 result
-            wgt, wut = (nf4.dequantize_nf4_t(p, st) for p, st in pairs)
-            gemm.gemm_f32((gd, wgt), (gd, wut))
+            # the training step's path: each weight expanded as stored, then one split-K launch
+            # over both products with an fp32 result, reading the weights k-major
+            wg, wu = (nf4.dequantize_nf4(p, st, torch.float16) for p, st in pairs)
+            gemm.gemm_f32((gd, wg), (gd, wu), b_kmajor=True)
 
         fwd_ref.append((ref_f, hold))
         bwd_ref.append((ref_b, hold))
@@ -573,9 +573,9 @@ def k_nf4_linear(dev, names):
         out.append(Kernel("nf4_linear_bwd", f"dgate Wg + dup Wu, {m} tokens", "mfma", flops, bwd))
         out.append(Kernel("nf4_linear_bwd_unfused", "the same: dequant x 2 + mm + addmm", "mfma",
                           flops, bwd_ref, step=False))
-        out.append(Kernel("nf4_linear_bwd_split", "the same: transposed dequant x 2 + split-K "
-                          "cm_gemm_f32 (fp32 dx; the training step's path)", "mfma", flops,
-                          bwd_split, step=False))
+        out.append(Kernel("nf4_linear_bwd_split", "the same: dequant x 2 + split-K "
+                          "cm_gemm_f32_kb (fp32 dx, the weights read k-major; the training "
+                          "step's path)", "mfma", flops, bwd_split, step=False))
     return out
 
 
