@@ -486,21 +486,48 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
 // row end need no mask: their q and dO rows are zero, so they add exactly zero.
 constexpr int kQTile = 32 * (kD / 8);   // Q / dO tile: 32 queries x 16 chunks
 constexpr int kQTTile = kD * (32 / 8);  // Q^T / dO^T tile: 128 d x 4 chunks
+constexpr int kDkdvVec = 2 * kQTile + 2 * kQTTile;  // lse (8 chunks) and Delta (8) follow
+constexpr int kDkdvStage = kDkdvVec + 16;
 
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
-    const _Float16* __restrict__ q16, const _Float16* __restrict__ qt16,
-    const _Float16* __restrict__ do16, const _Float16* __restrict__ dot16,
-    const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
-    const float* __restrict__ lse2, const float* __restrict__ delta,
-    const Rows* __restrict__ rows_p, int n_tokens, int n_pad, int hpg, float c_log2, float scale,
-    float* __restrict__ dk_part, float* __restrict__ dv_part) {
-  constexpr int kVec = 2 * kQTile + 2 * kQTTile;  // lse (8 chunks) and Delta (8) follow the tiles
-  constexpr int kStage = kVec + 16;
-  __shared__ uint4 lds[2][2][kStage];
-  const Rows& rows = *rows_p;
-  const int h = blockIdx.x, g = h / hpg;
-  const int b = blockIdx.y;  // a row's first key blocks (the most queries) dispatched first
-  if (!block_live(rows, b, n_tokens, n_pad)) return;
+// The operands of the backward's dK/dV and dQ blocks (one launch runs both).
+struct BwdArgs {
+  const _Float16* q16;
+  const _Float16* qt16;
+  const _Float16* do16;
+  const _Float16* dot16;
+  const _Float16* k16;
+  const _Float16* v16;
+  const _Float16* kt16;
+  const float* lse2;
+  const float* delta;
+  const Rows* rows;
+  int n_tokens, n_pad, hpg, H;
+  float c_log2, scale;
+  float* dk_part;
+  float* dv_part;
+  void* dq;         // fp32 or fp16, [H][N][D] or [N][H][D] with tok_major
+  int tok_major;
+  float* dq_rot;    // fused RoPE: dQ of the rotated q, [H][n_pad][D] fp32, or null
+};
+
+// raw: the workgroup's LDS, 4 stages of kDkdvStage
+__device__ __forceinline__ void bwd_dkdv_block(const BwdArgs& a, int h, int b, uint4* raw) {
+  constexpr int kVec = kDkdvVec;
+  constexpr int kStage = kDkdvStage;
+  auto lds = reinterpret_cast<uint4 (*)[2][kStage]>(raw);  // [pair][stage]
+  const _Float16* __restrict__ q16 = a.q16;
+  const _Float16* __restrict__ qt16 = a.qt16;
+  const _Float16* __restrict__ do16 = a.do16;
+  const _Float16* __restrict__ dot16 = a.dot16;
+  const _Float16* __restrict__ k16 = a.k16;
+  const _Float16* __restrict__ v16 = a.v16;
+  const float* __restrict__ lse2 = a.lse2;
+  const float* __restrict__ delta = a.delta;
+  const int n_pad = a.n_pad;
+  const float c_log2 = a.c_log2, scale = a.scale;
+  const Rows& rows = *a.rows;
+  const int g = h / a.hpg;
+  if (!block_live(rows, b, a.n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int kb = b - rows.pstart[r] / kBlk;
   const int len = rows.start[r + 1] - rows.start[r];
@@ -607,8 +634,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
   }
   cm::gemm::lds_barrier();
   if (pair == 1) return;
-  float* dkr = dk_part + (hq + p0 + key) * kD;
-  float* dvr = dv_part + (hq + p0 + key) * kD;
+  float* dkr = a.dk_part + (hq + p0 + key) * kD;
+  float* dvr = a.dv_part + (hq + p0 + key) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -634,19 +661,25 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
 constexpr int kKVTile = 32 * (kD / 8);  // K / V tile: 32 keys x 16 chunks
 constexpr int kKTTile = kD * (32 / 8);  // K^T tile: 128 d x 4 chunks
 
+constexpr int kDqStage = 2 * kKVTile + kKTTile;
+
 template <typename OT>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
-    const _Float16* __restrict__ q16, const _Float16* __restrict__ do16,
-    const _Float16* __restrict__ k16, const _Float16* __restrict__ v16,
-    const _Float16* __restrict__ kt16, const float* __restrict__ lse2,
-    const float* __restrict__ delta, const Rows* __restrict__ rows_p, int n_tokens, int n_pad,
-    int hpg, float c_log2, float scale, OT* __restrict__ dq, int tok_major,
-    float* __restrict__ dq_rot) {
-  constexpr int kStage = 2 * kKVTile + kKTTile;
-  __shared__ uint4 lds[2][2][kStage];
-  const Rows& rows = *rows_p;
-  const int h = blockIdx.x, g = h / hpg;
-  const int b = heavy_first_query_block();
+__device__ __forceinline__ void bwd_dq_block(const BwdArgs& a, int h, int b, uint4* raw) {
+  constexpr int kStage = kDqStage;
+  auto lds = reinterpret_cast<uint4 (*)[2][kStage]>(raw);  // [pair][stage]
+  const _Float16* __restrict__ q16 = a.q16;
+  const _Float16* __restrict__ do16 = a.do16;
+  const _Float16* __restrict__ k16 = a.k16;
+  const _Float16* __restrict__ v16 = a.v16;
+  const _Float16* __restrict__ kt16 = a.kt16;
+  const float* __restrict__ lse2 = a.lse2;
+  const float* __restrict__ delta = a.delta;
+  const int n_tokens = a.n_tokens, n_pad = a.n_pad, tok_major = a.tok_major;
+  const float c_log2 = a.c_log2, scale = a.scale;
+  float* __restrict__ dq_rot = a.dq_rot;
+  OT* __restrict__ dq = static_cast<OT*>(a.dq);
+  const Rows& rows = *a.rows;
+  const int g = h / a.hpg;
   if (!block_live(rows, b, n_tokens, n_pad)) return;
   const int r = row_of_block(rows, b);
   const int qb = b - rows.pstart[r] / kBlk;
@@ -737,8 +770,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
             (acc[dt][e] + xf[(dt * 16 + e) * cm::kWave]) * scale;
     return;
   }
-  OT* row = dq + (tok_major ? tok * gridDim.x + h  // gridDim.x = H
-                            : static_cast<int64_t>(h) * n_tokens + tok) * kD;
+  OT* row = dq + (tok_major ? tok * a.H + h : static_cast<int64_t>(h) * n_tokens + tok) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -749,6 +781,27 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
 
 // dK, dV = sum of the partials of the query heads of each group, [G][N][D] (or [N][G][D]) in the
 // output dtype.
+// ---------------------------------------------------------------------------------------------
+// The backward's dK/dV and dQ blocks in one launch: blockIdx.x < H is the dK/dV block
+// (blockIdx.y, head blockIdx.x), the rest the dQ block (gridDim.y - 1 - blockIdx.y, head
+// blockIdx.x - H). The two sets are independent (different outputs, the same relayout inputs),
+// and each has a few heavy blocks (a long row's first key blocks, its last query blocks) among
+// many light ones: dispatched together, heaviest first in both, the light blocks of one fill the
+// CUs the other's heavy blocks leave idle. The LDS holds the larger of the two stage rings.
+constexpr int kBwdLds = 4 * (kDkdvStage > kDqStage ? kDkdvStage : kDqStage);
+
+template <typename OT>
+__global__ __launch_bounds__(kThreads) void attn_bwd_kernel(BwdArgs a) {
+  __shared__ uint4 raw[kBwdLds];
+  const int x = blockIdx.x;
+  if (x < a.H) {
+    bwd_dkdv_block(a, x, blockIdx.y, raw);  // a row's first key blocks (the most queries) first
+  } else {
+    bwd_dq_block<OT>(a, x - a.H, static_cast<int>(gridDim.y) - 1 - blockIdx.y, raw);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Thread (position, 4 values of d) of key/value head blockIdx.y. With a fused RoPE, dK is the
 // gradient of the rotated k taken back through the transposed rotation (the partner values,
 // d +- 64, are 16 lanes away: a position's 32 threads are consecutive lanes and return together),
@@ -863,11 +916,12 @@ size_t fwd_ws_bytes(int64_t n_pad, int H, int G) {
          align256(static_cast<size_t>(H) * n_pad * kD * 2);
 }
 
+// q16, do16, qt16, dot16; k16, v16, kt16; Delta; dK / dV partials and the fused RoPE's dQ
 size_t bwd_ws_bytes(int64_t n_pad, int H, int G) {
   const size_t hq = align256(static_cast<size_t>(H) * n_pad * kD * 2);
   const size_t gk = align256(static_cast<size_t>(G) * n_pad * kD * 2);
   const size_t part = align256(static_cast<size_t>(H) * n_pad * kD * 4);
-  return 4 * hq + 3 * gk + align256(static_cast<size_t>(H) * n_pad * 4) + 2 * part;
+  return 4 * hq + 3 * gk + align256(static_cast<size_t>(H) * n_pad * 4) + 3 * part;
 }
 
 }  // namespace
@@ -994,7 +1048,8 @@ int bwd_impl(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void*
              const void* rows_image, int64_t n_tokens, int64_t n_pad, int H, int G, int head_dim,
              float scale, void* dq, int dq_dtype, void* dk, int dk_dtype, void* dv, int dv_dtype,
              int grads_token_major, void* workspace, int64_t workspace_bytes, void* stream) {
-  CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 65535);
+  // the backward's grid holds 2 H workgroups along x
+  CM_CHECK_ARG(head_dim == kD && H > 0 && G > 0 && H % G == 0 && H <= 32767);
   CM_CHECK_ARG((q_dtype == CM_F32 || q_dtype == CM_F16) && (k_dtype == CM_F32 || k_dtype == CM_F16) &&
                (v_dtype == CM_F32 || v_dtype == CM_F16));
   CM_CHECK_ARG((dq_dtype == CM_F32 || dq_dtype == CM_F16) &&
@@ -1016,17 +1071,17 @@ int bwd_impl(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void*
   const size_t nq = static_cast<size_t>(H) * n_pad * kD, nk = static_cast<size_t>(G) * n_pad * kD;
   _Float16* q16 = ws.take<_Float16>(nq);
   _Float16* do16 = ws.take<_Float16>(nq);
-  // qt16 and dot16 are read by the dK/dV kernel only; with a fused RoPE the dQ kernel, which runs
-  // after it, writes its fp32 [H][n_pad][D] dq_rot over the two (adjacent: nq fp32 values)
   _Float16* qt16 = ws.take<_Float16>(nq);
   _Float16* dot16 = ws.take<_Float16>(nq);
-  float* dq_rot = rope.cos != nullptr ? reinterpret_cast<float*>(qt16) : nullptr;
   _Float16* k16 = ws.take<_Float16>(nk);
   _Float16* v16 = ws.take<_Float16>(nk);
   _Float16* kt16 = ws.take<_Float16>(nk);
   float* delta = ws.take<float>(static_cast<size_t>(H) * n_pad);
   float* dk_part = ws.take<float>(nq);
   float* dv_part = ws.take<float>(nq);
+  // with a fused RoPE, dQ of the rotated q ([H][n_pad][D] fp32) for the head-sum launch to rotate
+  float* dq_rot_ws = ws.take<float>(nq);
+  float* dq_rot = rope.cos != nullptr ? dq_rot_ws : nullptr;
   const int np = static_cast<int>(n_pad), nt = static_cast<int>(n_tokens);
   const int n_blocks = np / kBlk;
   const Rows* rows = static_cast<const Rows*>(rows_image);
@@ -1047,20 +1102,13 @@ int bwd_impl(const void* q, int q_dtype, int64_t sq_h, int64_t sq_t, const void*
   hipLaunchKernelGGL(attn_relayout_kernel, dim3(n_blocks, 2 * H + 2 * G), dim3(256), 0, s, jobs,
                      rows, nt, np);
   if (int st = cm::launch_status()) return st;
-  const float c_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(H, n_blocks), dim3(kThreads), 0, s, q16, qt16,
-                     do16, dot16, k16, v16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
-                     dk_part, dv_part);
-  if (int st = cm::launch_status()) return st;
   const int tm = grads_token_major ? 1 : 0;
+  const BwdArgs ba{q16,  qt16, do16, dot16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, H,
+                   scale * 1.4426950408889634f, scale, dk_part, dv_part, dq, tm, dq_rot};
   if (dq_dtype == CM_F32) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, dim3(H, n_blocks), dim3(kThreads), 0, s, q16,
-                       do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
-                       static_cast<float*>(dq), tm, dq_rot);
+    hipLaunchKernelGGL(attn_bwd_kernel<float>, dim3(2 * H, n_blocks), dim3(kThreads), 0, s, ba);
   } else {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<_Float16>, dim3(H, n_blocks), dim3(kThreads), 0, s,
-                       q16, do16, k16, v16, kt16, lse2, delta, rows, nt, np, H / G, c_log2, scale,
-                       static_cast<_Float16*>(dq), tm, dq_rot);
+    hipLaunchKernelGGL(attn_bwd_kernel<_Float16>, dim3(2 * H, n_blocks), dim3(kThreads), 0, s, ba);
   }
   if (int st = cm::launch_status()) return st;
   const DqRope dqr{dq_rot, dq, dq_dtype == CM_F32 ? 1 : 0, H};
