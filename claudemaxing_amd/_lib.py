@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -76,6 +76,8 @@ SIGNATURES = {
                      _L, _L, _I, _I, _I, _I, _P]),
     "cm_swiglu_fwd": (_I, [_P, _I, _P, _I, _P, _I, _L, _I, _P]),
     "cm_swiglu_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _L, _I, _I, _I, _P]),
+    "cm_swiglu_fwd_rows": (_I, [_P, _I, _P, _I, _L, _P, _I, _L, _L, _L, _I, _P]),
+    "cm_swiglu_bwd_rows": (_I, [_P, _I, _L, _P, _I, _P, _I, _L, _P, _P, _L, _L, _I, _I, _I, _P]),
     "cm_lora_pack": (_I, [_P, _I, _P, _P, _P, _L, _F, _P]),
     "cm_lora_unpack": (_I, [_P, _P, _P, _P, _P, _I, _L, _F, _P]),
     "cm_xent_rows": (_I, [_P, _I, _L, _P, _P, _P, _P, _L, _L, _I, _F, _P]),

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 6
+#define CM_ABI_VERSION 7
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -205,6 +205,22 @@ int cm_swiglu_fwd(const void* gate, int g_dtype, const void* up, int u_dtype, vo
 int cm_swiglu_bwd(const void* dy, int dy_dtype, const void* gate, int g_dtype, const void* up,
                   int u_dtype, void* dgate, void* dup, int64_t n, int want_dgate, int want_dup,
                   int round_silu, void* stream);
+
+/* The two SwiGLU kernels above over rows: gate and up are [rows, cols] with rows ld_gu elements
+ * apart (the two halves of one [rows, 2F] gate/up product, up = gate + F), out and dy rows
+ * ld_out / ld_dy apart. The same values, element for element, as cm_swiglu_fwd / cm_swiglu_bwd
+ * on contiguous copies. Replace the same reference kernels (solution/swiglu_recompute.py:36-48,
+ * 51-79) where the MLP multiplies both projections in one product
+ * (MLPInputRecompute.forward / backward, swiglu_recompute.py:155-215). cols and every ld a
+ * multiple of 8, ld >= cols, all pointers 16-byte aligned; dgate / dup may equal gate / up.
+ */
+int cm_swiglu_fwd_rows(const void* gate, int g_dtype, const void* up, int u_dtype,
+                       int64_t ld_gu, void* out, int out_dtype, int64_t ld_out, int64_t rows,
+                       int64_t cols, int round_silu, void* stream);
+int cm_swiglu_bwd_rows(const void* dy, int dy_dtype, int64_t ld_dy, const void* gate,
+                       int g_dtype, const void* up, int u_dtype, int64_t ld_gu, void* dgate,
+                       void* dup, int64_t rows, int64_t cols, int want_dgate, int want_dup,
+                       int round_silu, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
 /* LoRA dropout mask pack. Replaces solution/lora.py:30-42 (lora_dropout_pack_kernel) as

@@ -68,7 +68,7 @@ def routed(x, gate_proj, up_proj, grad, monkeypatch, down_compute=None):
     """MLPInputRecompute's output and input gradient, and the name of the backward route it
     took."""
     taken = []
-    for name in ("_dx_fused", "_dx_kmajor", "_dx_transposed", "_dx_expanded", "_dx_autograd"):
+    for name in ("_dx_fused", "_dx_merged", "_dx_transposed", "_dx_expanded", "_dx_autograd"):
         fn = getattr(SR, name)
         monkeypatch.setattr(SR, name, lambda *a, _f=fn, _n=name: (taken.append(_n), _f(*a))[1])
     xr = x.detach().clone().requires_grad_(True)
@@ -97,10 +97,10 @@ def check(name, got, stock_v, ref, tol):
 ROUTES = [
     ("_dx_fused", 96, H, torch.float16, torch.float32),        # 2.6 GFLOP per product: fused
     ("_dx_fused", 96, H, torch.float16, torch.float16),
-    ("_dx_kmajor", 384, H, torch.float16, torch.float32),      # 10.6 GFLOP, fp32 dx: split-K
-    ("_dx_kmajor", 1276, H, torch.float16, torch.float32),     # the training step's batch
+    ("_dx_merged", 384, H, torch.float16, torch.float32),      # 10.6 GFLOP, fp32 dx: split-K
+    ("_dx_merged", 1276, H, torch.float16, torch.float32),     # the training step's batch
     ("_dx_transposed", 384, H, torch.float16, torch.float16),  # fp16 dx: expanded, transposed
-    ("_dx_kmajor", 384, 1600, torch.float16, torch.float32),   # width not a multiple of 128
+    ("_dx_merged", 384, 1600, torch.float16, torch.float32),   # width not a multiple of 128
     ("_dx_expanded", 384, 1600, torch.float16, torch.float16),  # ... and an fp16 dx
     ("_dx_expanded", 160, H, torch.bfloat16, torch.float32),   # bf16 compute
     ("_dx_expanded", 160, H, torch.bfloat16, torch.bfloat16),
@@ -139,7 +139,7 @@ def test_fp16_output_for_a_4bit_down_projection(dev, monkeypatch):
     x = torch.randn(384, H, generator=g).to(dev)
     grad = torch.randn(384, F, generator=g).to(dev)
     out, dx, taken = routed(x, gp, upp, grad, monkeypatch, down_compute=torch.float16)
-    assert taken == ["_dx_kmajor"] and out.dtype == torch.float16
+    assert taken == ["_dx_merged"] and out.dtype == torch.float16
     assert dx.dtype == torch.float32
     s_out, s_dx = stock(x, gp, upp, grad)
     r_out, r_dx = fp32_reference(x, oracle_weight(gp), oracle_weight(upp), grad)

@@ -117,3 +117,35 @@ def test_extreme_gate_values(dev):
     assert torch.equal(torch.isnan(out.cpu()), torch.isnan(ref))
     fin = torch.isfinite(ref)
     assert_close(out.cpu()[fin], ref[fin], 1e-4, "extremes")
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+@pytest.mark.parametrize("rows,f", [(1276, 8960), (3, 1000), (1, 8)])
+def test_row_kernels_read_the_halves_of_a_merged_product(dtype, rows, f, dev):
+    """cm_swiglu_fwd_rows / cm_swiglu_bwd_rows on y = [gate | up] ([rows, 2f], the MLP's merged
+    gate/up product): bit-identical to the flat kernels on contiguous copies of the halves, the
+    backward in place over y, and within the oracle's tolerance."""
+    from claudemaxing_amd import swiglu_recompute as SR
+
+    banner(f"swiglu rows={rows} f={f} {dtype}")
+    gen = torch.Generator().manual_seed(7)
+    y = (torch.randn(rows, 2 * f, generator=gen) * 3).to(dtype).to(dev)
+    grad = torch.randn(rows, f, generator=gen).to(dtype).to(dev)
+    gate, up = y[:, :f].contiguous(), y[:, f:].contiguous()
+    for round_silu in (True, False):
+        out = torch.empty(rows, f, dtype=dtype, device=dev)
+        SR._swiglu_fwd_rows(y, f, out, round_silu)
+        flat = torch.empty_like(out)
+        SR._swiglu_fwd(gate, up, flat, round_silu)
+        assert torch.equal(out, flat)
+        yb = y.clone()
+        SR._swiglu_bwd_rows(grad, yb, f, round_silu)
+        dg, du = torch.empty_like(gate), torch.empty_like(up)
+        SR._swiglu_bwd(grad, gate, up, dg, du, round_silu)
+        assert torch.equal(yb[:, :f], dg) and torch.equal(yb[:, f:], du)
+    r_out, r_dg, r_du = O.forward_backward(gate.cpu(), up.cpu(), grad.cpu())
+    tol = tolerance(dtype, dtype)
+    assert_close(out, r_out, tol, "out")
+    assert_close(yb[:, :f], r_dg, tol, "dgate")
+    assert_close(yb[:, f:], r_du, tol, "dup")
+
