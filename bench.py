@@ -527,7 +527,7 @@ def k_nf4_linear(dev, names):
     flops = 2 * 2 * m * f * h
     in_bytes = sum(p.numel() for p, _ in qs) + x.numel() * 2
     out = []
-    fwd, fwd_ref, bwd, bwd_ref, bwd_split = [], [], [], [], []
+    fwd, fwd_ref, fwd_merged, bwd, bwd_ref, bwd_split = [], [], [], [], [], []
     for _ in range(copies_for(in_bytes + 2 * g.numel() * 2)):
         pairs = [(p.to(dev), st.to(dev)) for p, st in qs]
         xd, gd = x.to(dev), g.to(dev)
@@ -538,8 +538,10 @@ def k_nf4_linear(dev, names):
         ldo = (ctypes.c_int64 * 2)(f, f)
         g_arr = (ctypes.c_void_p * 2)(gd.data_ptr(), gd.data_ptr())
         ldg = (ctypes.c_int64 * 2)(f, f)
+        w2 = torch.empty(2 * f, h, dtype=torch.float16, device=dev)  # [Wg; Wu]
+        gcat = torch.cat([gd, gd], 1)  # [dgate | dup], the merged product's gradient
         assert xd.shape == (m, h) and all(y.shape == (m, f) for y in ys) and dx.shape == (m, h)
-        hold = (pairs, xd, gd, ys, dx, w_arr, keep, out_arr, ldo, g_arr, ldg)
+        hold = (pairs, xd, gd, ys, dx, w_arr, keep, out_arr, ldo, g_arr, ldg, w2, gcat)
         fwd.append((bound("cm_nf4_linear_fwd", xd.data_ptr(), h, m, w_arr, 2, None, out_arr, ldo,
                           _lib.F16, None, 0, _stream(dev)), hold))
         ws_bytes = _lib.load().cm_nf4_linear_workspace_bytes(m, w_arr, 2, 1)
@@ -555,13 +557,23 @@ def k_nf4_linear(dev, names):
             wg, wu = (nf4.dequantize_nf4(p, st, torch.float16) for p, st in pairs)
             torch.addmm(torch.mm(gd, wg), gd, wu)
 
-        def split_b(pairs=pairs, gd=gd):
-            # the training step's path: each weight expanded as stored, then one split-K launch
-            # over both products with an fp32 result, reading the weights k-major
-            wg, wu = (nf4.dequantize_nf4(p, st, torch.float16) for p, st in pairs)
-            gemm.gemm_f32((gd, wg), (gd, wu), b_kmajor=True)
+        def expand_pair(pairs=pairs, w2=w2):
+            for (p, st), half in zip(pairs, (w2[:f], w2[f:])):
+                nf4.dequantize_nf4(p, st, torch.float16, out=half)
+
+        def merged_f(xd=xd, w2=w2, expand_pair=expand_pair):
+            # the training step's path: both weights expanded into one [2F, K] weight, one GEMM
+            expand_pair()
+            torch.nn.functional.linear(xd, w2)
+
+        def split_b(gcat=gcat, w2=w2, expand_pair=expand_pair):
+            # the training step's path: the same [2F, K] weight, then one split-K launch over the
+            # concatenated contraction with an fp32 result, reading the weight k-major
+            expand_pair()
+            gemm.gemm_f32((gcat, w2), b_kmajor=True)
 
         fwd_ref.append((ref_f, hold))
+        fwd_merged.append((merged_f, hold))
         bwd_ref.append((ref_b, hold))
         bwd_split.append((split_b, hold))
     if "nf4_linear_fwd" in names:
@@ -569,13 +581,17 @@ def k_nf4_linear(dev, names):
                           flops, fwd))
         out.append(Kernel("nf4_linear_fwd_unfused", "the same: dequant + torch fp16 GEMM x 2",
                           "mfma", flops, fwd_ref, step=False))
+        out.append(Kernel("nf4_linear_fwd_merged", "the same: dequant x 2 into one [2F,K] weight "
+                          "+ one torch fp16 GEMM (the training step's path)", "mfma", flops,
+                          fwd_merged, step=False))
     if "nf4_linear_bwd" in names:
         out.append(Kernel("nf4_linear_bwd", f"dgate Wg + dup Wu, {m} tokens", "mfma", flops, bwd))
         out.append(Kernel("nf4_linear_bwd_unfused", "the same: dequant x 2 + mm + addmm", "mfma",
                           flops, bwd_ref, step=False))
-        out.append(Kernel("nf4_linear_bwd_split", "the same: dequant x 2 + split-K "
-                          "cm_gemm_f32_kb (fp32 dx, the weights read k-major; the training "
-                          "step's path)", "mfma", flops, bwd_split, step=False))
+        out.append(Kernel("nf4_linear_bwd_split", "the same: dequant x 2 into one [2F,K] weight "
+                          "+ split-K cm_gemm_f32_kb over the 2F contraction (fp32 dx, the weight "
+                          "read k-major; the training step's path)", "mfma", flops, bwd_split,
+                          step=False))
     return out
 
 

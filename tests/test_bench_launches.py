@@ -134,8 +134,8 @@ def test_every_bench_launch_stays_inside_its_tensors(recorded):
     # the device copy and the launch floors pass no tensors to check
     names = set(bench.ALL) - {"lmhead_ce", "hbm_copy_ref"} - bench.FLOORS
     kernels = bench.build_kernels(dev, sorted(names))
-    # "_unfused" and "_split" lines time torch-level comparison paths beside a C-ABI entry
-    side = ("_unfused", "_split")
+    # "_unfused", "_split" and "_merged" lines time torch-level paths beside a C-ABI entry
+    side = ("_unfused", "_split", "_merged")
     assert {k.name for k in kernels if not k.name.endswith(side)} == names
     checked = 0
     for kern in kernels:
