@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -110,6 +110,7 @@ SIGNATURES = {
     "cm_probe_mfma_f16_flops": (_L, [_I, _I]),
     "cm_probe_launch": (_I, [_I, _I, _P]),
     "cm_nf4_scale_map": (_I, [_PW, _P, _P]),
+    "cm_nf4_dequant_group": (_I, [_PW, _I, _PP, _I, _P]),
 }
 
 _lock = threading.Lock()

@@ -94,12 +94,15 @@ struct Pack8<float> {
 // workgroup of the launch is resident at once (the barrier waits on the earliest loads), slower
 // by ~3% for a streaming launch of many waves of workgroups, which issues the words first.
 // Both orders compute the same values.
+// The workgroup body, for workgroup `wg` of one weight's launch (the single-weight kernel and the
+// grouped one both run it).
 template <typename OutT, bool NESTED, bool SCALES_FIRST>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
+__device__ __forceinline__ void dequant_vec_wg(
     const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
     const float* __restrict__ code, const float* __restrict__ code2,
     const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
-    OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
+    OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2,
+    uint32_t wg) {
   static_assert(kThreads >= 256, "one code2 entry per lane");
   static_assert(kThreads * kUnits / 4 <= kThreads, "one absmax block of the range per lane");
   static_assert(kThreads == 256, "one code pair per lane");
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
   __shared__ float s_code2[NESTED ? 256 : 1];
   __shared__ uint2 s_blk[kThreads];  // block blk0 + t: {absmax byte, absmax2 bits} or {-, absmax}
   const int t = threadIdx.x;
-  const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnits);
+  const int64_t u0 = static_cast<int64_t>(wg) * (kThreads * kUnits);
   const uint32_t blk0 = static_cast<uint32_t>(u0 >> unit_shift);
   // blocks in the workgroup's range (1 when the range lies inside one block)
   const int nb = unit_shift < 30 && ((kThreads * kUnits) >> unit_shift) > 0
@@ -170,6 +173,57 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
     for (int j = 0; j < kUnits; ++j)
       if (u0 + t + j * kThreads < n_units) unit(j);
   }
+}
+
+template <typename OutT, bool NESTED, bool SCALES_FIRST>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
+    const uint32_t* __restrict__ packed, const void* __restrict__ absmax,
+    const float* __restrict__ code, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, const float* __restrict__ offset_ptr,
+    OutT* __restrict__ out, int64_t n_units, int unit_shift, int bs2_shift, uint32_t bs2) {
+  dequant_vec_wg<OutT, NESTED, SCALES_FIRST>(packed, absmax, code, code2, absmax2, offset_ptr,
+                                             out, n_units, unit_shift, bs2_shift, bs2,
+                                             blockIdx.x);
+}
+
+// Several weights expanded by one launch: weight i takes workgroups [first[i], first[i + 1]) and
+// each workgroup runs the single-weight body on its weight, so every output element is the one
+// the single-weight kernel writes. A workgroup finds its weight with static indices only (the
+// descriptors stay in kernel-argument registers).
+constexpr int kGroupMax = 8;
+struct DqJob {
+  const uint32_t* packed;
+  const void* absmax;
+  const float* code;
+  const float* code2;
+  const float* absmax2;
+  const float* offset;
+  void* out;
+  int64_t n_units;
+  int unit_shift, bs2_shift;
+  uint32_t bs2;
+};
+struct DqGroup {
+  DqJob job[kGroupMax];
+  uint32_t first[kGroupMax];
+  int n;
+};
+
+template <typename OutT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_group(DqGroup g) {
+  const uint32_t b = blockIdx.x;
+  DqJob job = g.job[0];
+  uint32_t first = 0;
+#pragma unroll
+  for (int i = 1; i < kGroupMax; ++i) {
+    if (i < g.n && b >= g.first[i]) {
+      job = g.job[i];
+      first = g.first[i];
+    }
+  }
+  dequant_vec_wg<OutT, NESTED, false>(job.packed, job.absmax, job.code, job.code2, job.absmax2,
+                                      job.offset, static_cast<OutT*>(job.out), job.n_units,
+                                      job.unit_shift, job.bs2_shift, job.bs2, b - first);
 }
 
 // Scalar path: one packed byte per lane, any alignment; bytes [first, n_bytes).
@@ -382,4 +436,94 @@ extern "C" int cm_nf4_dequant(const uint8_t* packed, const void* absmax, int nes
     default: return static_cast<int>(hipErrorInvalidValue);
   }
 #undef CM_NF4_CASE
+}
+
+namespace {
+
+// Whether cm_nf4_dequant_group can take the weights in one launch: the vector path for every
+// weight (4-byte aligned packed bytes in whole 4-byte units, 16-byte aligned outputs), one
+// nestedness, power-of-two block sizes.
+bool groupable(const cm_nf4_weight* w, int n_w, void* const* out) {
+  for (int i = 0; i < n_w; ++i) {
+    const int64_t n_bytes = w[i].rows * w[i].cols / 2;
+    if (w[i].nested != w[0].nested || n_bytes % 4 || !cm::aligned(w[i].packed, 4) ||
+        !cm::aligned(out[i], 16))
+      return false;
+  }
+  return true;
+}
+
+template <typename OutT, bool NESTED>
+int launch_group(const cm_nf4_weight* w, int n_w, void* const* out, hipStream_t s) {
+  DqGroup g{};
+  int64_t blocks = 0;
+  const int64_t per_block = int64_t{kThreads} * kUnits;
+  for (int i = 0; i < n_w; ++i) {
+    const int64_t n_units = w[i].rows * w[i].cols / 8;
+    g.first[i] = static_cast<uint32_t>(blocks);
+    g.job[i] = DqJob{reinterpret_cast<const uint32_t*>(w[i].packed), w[i].absmax, w[i].code,
+                     NESTED ? w[i].code2 : nullptr, NESTED ? w[i].absmax2 : nullptr,
+                     NESTED ? w[i].offset : nullptr, out[i], n_units,
+                     log2_exact(w[i].blocksize) - 3,
+                     NESTED ? log2_exact(w[i].blocksize2) : 0,
+                     NESTED ? static_cast<uint32_t>(w[i].blocksize2) : 1u};
+    blocks += (n_units + per_block - 1) / per_block;
+  }
+  g.n = n_w;
+  if (blocks == 0) return 0;
+  hipLaunchKernelGGL((nf4_dequant_group<OutT, NESTED>), dim3(static_cast<uint32_t>(blocks)),
+                     dim3(kThreads), 0, s, g);
+  return cm::launch_status();
+}
+
+}  // namespace
+
+extern "C" int cm_nf4_dequant_group(const cm_nf4_weight* w, int n_w, void* const* out,
+                                    int out_dtype, void* stream) {
+  CM_CHECK_ARG(n_w >= 0 && n_w <= kGroupMax);
+  if (n_w == 0) return 0;
+  CM_CHECK_ARG(w && out);
+  int64_t blocks = 0;
+  for (int i = 0; i < n_w; ++i) {
+    const cm_nf4_weight& d = w[i];
+    CM_CHECK_ARG(d.rows >= 0 && d.cols >= 0 && (d.rows * d.cols) % 2 == 0);
+    if (d.rows * d.cols == 0) continue;
+    CM_CHECK_ARG(d.packed && d.absmax && d.code && out[i]);
+    CM_CHECK_ARG(d.blocksize >= 32 && log2_exact(d.blocksize) >= 0);
+    CM_CHECK_ARG(d.rows * d.cols / d.blocksize < (int64_t{1} << 31));
+    if (d.nested) CM_CHECK_ARG(d.code2 && d.absmax2 && d.offset && d.blocksize2 >= 1);
+    blocks += (d.rows * d.cols / 8 + kThreads * kUnits - 1) / (kThreads * kUnits);
+  }
+  CM_CHECK_ARG(blocks < (int64_t{1} << 31));
+  CM_CHECK_ARG(out_dtype == CM_F16 || out_dtype == CM_F32 || out_dtype == CM_BF16);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // empty weights are left out of the launch
+  cm_nf4_weight ws[kGroupMax];
+  void* outs[kGroupMax];
+  int n = 0;
+  for (int i = 0; i < n_w; ++i) {
+    if (w[i].rows * w[i].cols == 0) continue;
+    ws[n] = w[i];
+    outs[n++] = out[i];
+  }
+  if (n == 0) return 0;
+  if (!groupable(ws, n, outs)) {  // one launch per weight, the same kernels and values
+    for (int i = 0; i < n; ++i) {
+      const cm_nf4_weight& d = ws[i];
+      const int st = cm_nf4_dequant(d.packed, d.absmax, d.nested, d.code, d.code2, d.absmax2,
+                                    d.offset, outs[i], out_dtype, d.rows * d.cols / 2,
+                                    d.blocksize, d.nested ? d.blocksize2 : 1, stream);
+      if (st) return st;
+    }
+    return 0;
+  }
+#define CM_NF4_GROUP(T)                                                  \
+  return ws[0].nested ? launch_group<T, true>(ws, n, outs, s)            \
+                      : launch_group<T, false>(ws, n, outs, s)
+  switch (out_dtype) {
+    case CM_F16: CM_NF4_GROUP(_Float16);
+    case CM_F32: CM_NF4_GROUP(float);
+    default: CM_NF4_GROUP(cm::bf16_t);
+  }
+#undef CM_NF4_GROUP
 }

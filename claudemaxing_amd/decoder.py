@@ -28,6 +28,7 @@ modules) and take the kernels, on an fp32 residual stream; any other call runs t
 
 import torch
 
+from . import expand
 from ._patching import install, tagged
 from .rmsnorm import _kernel_covers, add_norm, norm_pass
 
@@ -71,6 +72,7 @@ def patch_qwen2_decoder_residual():
                              use_cache=use_cache, position_embeddings=position_embeddings,
                              **kwargs)
             n1, n2 = self.input_layernorm, self.post_attention_layernorm
+            expand.expand_layer(self, hidden_states)  # the layer's NF4 expansions, one launch
             y, residual = norm_pass(hidden_states, n1.weight, n1.variance_epsilon)
             attn, _ = self.self_attn(hidden_states=y, attention_mask=attention_mask,
                                      position_ids=position_ids, past_key_values=past_key_values,
@@ -82,9 +84,9 @@ def patch_qwen2_decoder_residual():
             else:
                 h = residual + attn
                 y = n2(h)
-            if _mlp_takes_residual(self.mlp):
-                return self.mlp(y, residual=h)
-            return h + self.mlp(y)
+            out = self.mlp(y, residual=h) if _mlp_takes_residual(self.mlp) else h + self.mlp(y)
+            expand.drop(hidden_states.device)
+            return out
 
         return forward
 

@@ -15,7 +15,7 @@ import weakref
 
 import torch
 
-from . import _lib
+from . import _lib, expand
 from .gemm import gemm_f32, gemm_f32_supported, split_k_pays
 from .nf4 import _BLOCKSIZES, QuantState, _nf4_code, _offset_tensor, dequantize_nf4, quantize_nf4
 from .rmsnorm import fp16_copy_of, fp16_grad_copy_of
@@ -127,6 +127,47 @@ def _weights(pairs):
         cache.clear()
     cache[keys] = got
     return got
+
+
+def _plain_weights(pairs):
+    """(cm_nf4_weight array of the pairs without the fused GEMMs' scale maps, tensors it points
+    into, the QuantStates as weak references): what the expansion kernels read, kept on the first
+    pair's QuantState per weight version (as _weights keeps its arrays)."""
+    keys = tuple(_weight_key(p, s) for p, s in pairs)
+    cache = getattr(pairs[0][1], "_cm_plain_arrays", None)
+    if cache is None:
+        cache = pairs[0][1]._cm_plain_arrays = {}
+    got = cache.get(keys)
+    if got is not None and all(r() is s for r, (_, s) in zip(got[2], pairs)):
+        return got
+    built = [_descriptor(p, s, scale_map=False) for p, s in pairs]
+    got = ((_lib.NF4Weight * len(built))(*[d for d, _ in built]), [k for _, k in built],
+           tuple(weakref.ref(s) for _, s in pairs))
+    if len(cache) > 16:
+        cache.clear()
+    cache[keys] = got
+    return got
+
+
+def dequantize_group(pairs, outs, checked=False):
+    """Expand the NF4 weights `pairs` [(packed, QuantState)] into `outs` (contiguous tensors of
+    one dtype on the weights' device, each of its weight's size) with one launch
+    (cm_nf4_dequant_group): the values are dequantize_nf4's. `checked`: the caller made the
+    outputs so (the checks below are skipped)."""
+    if not pairs:
+        return
+    if len(pairs) != len(outs) or len(pairs) > 8:
+        raise ValueError("dequantize_group: one output per weight, at most 8 weights")
+    dtype = outs[0].dtype
+    for (packed, state), out in zip(pairs, () if checked else outs):
+        if (out.dtype != dtype or not out.is_contiguous() or out.device != packed.device
+                or out.numel() != int(state.shape[0]) * int(state.shape[1])):
+            raise ValueError("dequantize_group: each output must be a contiguous tensor of its "
+                             "weight's size, all of one dtype, on the weights' device")
+    w = _plain_weights(pairs)[0]
+    out_arr = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _lib.call("cm_nf4_dequant_group", w, len(pairs), out_arr, _lib.dtype_code(dtype),
+              _lib.stream(outs[0].device))
 
 
 # Products below this many FLOPs take the fused kernel; larger ones expand the weight with the
@@ -249,7 +290,9 @@ class MatMulNF4(torch.autograd.Function):
                      and fused_pays(xc.numel() // max(xc.shape[-1], 1), *state.shape))
         if ctx.fused:
             return nf4_linear_fwd(xc, [(packed, state)], [bias], out_dtype)[0]
-        w = dequantize_nf4(packed, state, compute)
+        w = expand.take(packed, compute)  # expanded with the rest of its decoder layer
+        if w is None:
+            w = dequantize_nf4(packed, state, compute)
         if out_dtype == torch.float32 and compute != torch.float32 and xc.is_cuda:
             # the GEMM writes fp32 itself (fp32 sums, no fp16 rounding and no cast launch)
             x2 = xc.reshape(-1, xc.shape[-1])
@@ -280,7 +323,11 @@ class MatMulNF4(torch.autograd.Function):
         if ctx.fused and ctx.x_dtype in (torch.float16, torch.float32):
             dx = nf4_linear_bwd([g], [(ctx.packed, ctx.state)], ctx.x_dtype)
             return dx, None, None, None, None, None, d_res
-        w = dequantize_nf4(ctx.packed, ctx.state, g.dtype)
+        w = expand.take(ctx.packed, g.dtype)
+        if w is None:  # the first expansion of a layer's backward expands the layer's group
+            w = expand.backward_group(ctx.packed, g.dtype)
+        if w is None:
+            w = dequantize_nf4(ctx.packed, ctx.state, g.dtype)
         return torch.matmul(g, w).to(ctx.x_dtype), None, None, None, None, None, d_res
 
 

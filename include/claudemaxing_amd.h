@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 7
+#define CM_ABI_VERSION 8
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -524,6 +524,18 @@ int cm_nf4_linear_bwd(const void* const* g, const int64_t* ldg, int64_t m,
 /* Workspace bytes of cm_nf4_linear_fwd (backward = 0) or cm_nf4_linear_bwd (backward = 1) for
  * these sizes (0: the call does not split its contraction), -1 for invalid weights. */
 int64_t cm_nf4_linear_workspace_bytes(int64_t m, const cm_nf4_weight* w, int n_w, int backward);
+
+/* Several NF4 weights expanded by one launch: out[i] receives weight w[i] as cm_nf4_dequant
+ * writes it (the same values, element for element), [rows, cols] in out_dtype (fp32, fp16 or
+ * bf16). Replaces the reference's per-weight nf4_dequant_kernel launches
+ * (solution/nf4.py:26-46, launched per weight by dequantize_nf4, nf4.py:64-82) where a decoder
+ * layer expands its o, gate, up and down weights together. At most 8 weights; one launch when
+ * every weight takes the vector path (4-byte aligned packed bytes in whole 4-byte units,
+ * 16-byte aligned outputs) and all share one nestedness, else one cm_nf4_dequant per weight.
+ * The fused GEMMs' scale_map is not read.
+ */
+int cm_nf4_dequant_group(const cm_nf4_weight* w, int n_w, void* const* out, int out_dtype,
+                         void* stream);
 
 /* ---- On-box peak probes (measurement only; no counterpart in the reference) ----------------
  * The roofline denominators as this board attains them, which bench.py reports beside the

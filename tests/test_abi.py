@@ -77,6 +77,9 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_swiglu_bwd_rows(0x1000, 1, 8, 0x2000, 1, 0x3000, 1, 32, 0x2000, 0x3000, 4, 16,
                                   1, 1, 1, None) == INVALID  # dy rows narrower than cols
     assert lib.cm_swiglu_fwd_rows(None, 1, None, 1, 32, None, 1, 16, 0, 16, 1, None) == 0
+    # grouped NF4 expansion: at most 8 weights; none is a no-op
+    assert lib.cm_nf4_dequant_group(None, 9, None, 1, None) == INVALID
+    assert lib.cm_nf4_dequant_group(None, 0, None, 1, None) == 0
     assert lib.cm_rmsnorm_fwd(None, 1, 4, None, 0, None, 1, None, None, None, None, 1, 2, 8,
                               1e-6, None) == INVALID  # row stride < n_cols
     assert lib.cm_xent_rows(None, 1, 4, None, None, None, None, 1, 8, 0, 1.0, None) == INVALID

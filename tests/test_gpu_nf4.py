@@ -208,3 +208,60 @@ def test_state_dict_checkpoint_dequantizes_bit_exact(nested, dev, tmp_path):
     y = lin(x.to(dev)).float().cpu()
     r = x.float() @ torch.from_numpy(ref).reshape(1536, 1536).float().t()
     assert (y - r).abs().max().item() <= 2e-3 * max(1.0, r.abs().max().item())
+
+
+def test_group_expansion_equals_single_expansions(dev):
+    """cm_nf4_dequant_group: several weights (nested and plain, blocksizes 64 / 128 / 256,
+    one empty) in one launch, into separate tensors and into the two halves of one buffer:
+    bit-identical to dequantize_nf4 per weight, in every output dtype."""
+    from claudemaxing_amd.nf4_linear import dequantize_group
+
+    banner("nf4 group expansion")
+    gen = torch.Generator().manual_seed(11)
+    specs = [((1536, 1536), 64, True), ((896, 512), 128, True), ((640, 256), 256, True),
+             ((0, 64), 64, True)]
+    pairs = []
+    for shape, bs, nested in specs:
+        w = torch.randn(*shape, generator=gen) * 0.05
+        p, st = quantize_nf4(w, bs, nested)
+        pairs.append((p.to(dev), st.to(dev)))
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        outs = [torch.full(tuple(st.shape), 7.0, dtype=dtype, device=dev) for _, st in pairs]
+        dequantize_group(pairs, outs)
+        for (p, st), o in zip(pairs, outs):
+            assert_bits_equal(o, dequantize_nf4(p, st, dtype), f"group {tuple(st.shape)} {dtype}")
+    # two weights of one shape into the halves of one [2F, K] buffer (the MLP's merged weight)
+    two = [quantize_nf4(torch.randn(512, 384, generator=gen) * 0.05, 64, True) for _ in range(2)]
+    two = [(p.to(dev), st.to(dev)) for p, st in two]
+    buf = torch.empty(1024, 384, dtype=torch.float16, device=dev)
+    dequantize_group(two, [buf[:512], buf[512:]])
+    assert_bits_equal(buf, torch.cat([dequantize_nf4(p, st, torch.float16) for p, st in two]),
+                      "merged halves")
+    # plain (not double-quantized) weights group too; a mixed group falls back to one launch per
+    # weight with the same values
+    plain = [quantize_nf4(torch.randn(256, 256, generator=gen) * 0.05, 64, False)
+             for _ in range(2)]
+    plain = [(p.to(dev), st.to(dev)) for p, st in plain]
+    for group in (plain, [plain[0], pairs[0]]):
+        outs = [torch.empty(tuple(st.shape), dtype=torch.float16, device=dev) for _, st in group]
+        dequantize_group(group, outs)
+        for (p, st), o in zip(group, outs):
+            assert_bits_equal(o, dequantize_nf4(p, st, torch.float16), "plain / mixed group")
+    torch.cuda.synchronize()
+
+
+def test_group_expansion_misaligned_output_falls_back(dev):
+    """An output that is not 16-byte aligned takes one launch per weight (the single-weight
+    byte path for that one): the same values."""
+    from claudemaxing_amd.nf4_linear import dequantize_group
+
+    banner("nf4 group expansion, misaligned output")
+    gen = torch.Generator().manual_seed(12)
+    pairs = [quantize_nf4(torch.randn(128, 256, generator=gen) * 0.05, 64, True)
+             for _ in range(2)]
+    pairs = [(p.to(dev), st.to(dev)) for p, st in pairs]
+    big = torch.empty(128 * 256 + 1, dtype=torch.float16, device=dev)
+    outs = [big[1:].view(128, 256), torch.empty(128, 256, dtype=torch.float16, device=dev)]
+    dequantize_group(pairs, outs)
+    for (p, st), o in zip(pairs, outs):
+        assert_bits_equal(o, dequantize_nf4(p, st, torch.float16), "misaligned group")
