@@ -260,33 +260,61 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
   const int len = rows.start[r + 1] - rows.start[r];
   const int local0 = (b - rows.pstart[r] / kBlk) * kBlk;
   const int pos0 = b * kBlk;
-  for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
+  // A thread takes chunks c = threadIdx.x + 256 i (token c / 16, 8 values of d at 8 (c % 16)).
+  // All of its loads are issued before any store (the jobs' pointers carry no aliasing
+  // information, so loads written after a store would wait for it): one memory round trip per
+  // block instead of one per chunk. The arithmetic, and so every bit, is the per-chunk one.
+  constexpr int kIt = kBlk * (kD / 8) / 256;
+  static_assert(kIt * 256 == kBlk * (kD / 8), "whole chunks per thread");
+  const bool rot = job.rope.cos != nullptr;
+  float xv[kIt][8], cv[kIt][8], sv[kIt][8];
+  half8 ov[kIt];
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int c = threadIdx.x + 256 * it;
     const int t = c / (kD / 8), ch = c % (kD / 8);
     const int local = local0 + t;
     const bool ok = local < len;
     const int64_t tok = rows.start[r] + local;
-    half8 x;
-    if (job.rope.cos == nullptr) {
-      x = ok ? load8(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8) : zero8();
+    if (ok) {
+      load8f(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8, xv[it]);
     } else {
-      // the partner of chunk ch (d +- 64) is chunk ch ^ 8, held by the lane 8 away (a token's
-      // 16 chunks are 16 consecutive lanes, every lane of the loop active)
-      float xv[8], pv[8];
-      if (ok) {
-        load8f(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8, xv);
-      } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pv[i] = __shfl_xor(xv[i], 8, cm::kWave);
+      for (int i = 0; i < 8; ++i) xv[it][i] = 0.0f;
+    }
+    if (rot) {
       const int64_t ct = ok ? tok : rows.start[r];  // pads: any row of the batch's tables
       const float* cr = job.rope.cos + ct * job.rope.cs_t + ch * 8;
       const float* sr = job.rope.sin + ct * job.rope.cs_t + ch * 8;
 #pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        cv[it][i] = cr[i];
+        sv[it][i] = sr[i];
+      }
+    }
+    if (job.delta)
+      ov[it] = ok ? *reinterpret_cast<const half8*>(job.o + tok * job.so_t + h * kD + ch * 8)
+                  : zero8();
+  }
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int c = threadIdx.x + 256 * it;
+    const int t = c / (kD / 8), ch = c % (kD / 8);
+    const bool ok = local0 + t < len;
+    half8 x;
+    if (!rot) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(xv[it][i]);
+    } else {
+      // the partner of chunk ch (d +- 64) is chunk ch ^ 8, held by the lane 8 away (a token's
+      // 16 chunks are 16 consecutive lanes, every lane of the loop active)
+      float pv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[i] = __shfl_xor(xv[it][i], 8, cm::kWave);
+#pragma unroll
       for (int i = 0; i < 8; ++i)
-        x[i] = static_cast<_Float16>(ch < 8 ? rot_minus(xv[i], pv[i], cr[i], sr[i])
-                                            : rot_plus(xv[i], pv[i], cr[i], sr[i]));
+        x[i] = static_cast<_Float16>(ch < 8 ? rot_minus(xv[it][i], pv[i], cv[it][i], sv[it][i])
+                                            : rot_plus(xv[it][i], pv[i], cv[it][i], sv[it][i]));
     }
     if (job.nat)
       *reinterpret_cast<half8*>(job.nat + (static_cast<int64_t>(h) * n_pad + pos0 + t) * kD +
@@ -301,9 +329,8 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
     if (job.delta) {
       float d = 0.0f;
       if (ok) {
-        const half8 o = *reinterpret_cast<const half8*>(job.o + tok * job.so_t + h * kD + ch * 8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d += static_cast<float>(x[i]) * static_cast<float>(o[i]);
+        for (int i = 0; i < 8; ++i) d += static_cast<float>(x[i]) * static_cast<float>(ov[it][i]);
       }
       // the 16 chunks of a token are 16 consecutive lanes
 #pragma unroll
