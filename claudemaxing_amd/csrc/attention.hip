@@ -81,6 +81,48 @@ __device__ __forceinline__ bool block_live(const Rows& rows, int b, int n_tokens
          rows.pstart[r] % kBlk == 0 && rows.start[r + 1] <= n_tokens;
 }
 
+// Where padded block b lies: its row r, the row's first real token, real length and first padded
+// position; live = false for a block with no work (block_live).
+struct Where {
+  bool live;
+  int r, start, len, pstart;
+};
+
+// block_live and row_of_block in one round of loads: lane i of the wavefront loads start[i] and
+// pstart[i] (one coalesced load each) beside the scalar load of the row count, the block's row
+// is the number of rows 1 .. n - 1 that start at or before it (a ballot: pstart is
+// non-decreasing, so they are a prefix), and the entries the block needs are read from the lanes
+// that hold them. The walk over pstart loaded one entry after the other, a dependent load per row
+// at the start of every workgroup. Batches of 64 rows or more take the walk. Called with every
+// lane of the wavefront active and b uniform.
+__device__ __forceinline__ Where locate(const Rows& rows, int b, int n_tokens, int n_pad) {
+  const int n = rows.n;
+  const int lane = threadIdx.x % cm::kWave;
+  const int stv = rows.start[lane], psv = rows.pstart[lane];  // lane <= 63 < kMaxRows + 1
+  Where w{false, 0, 0, 0, 0};
+  if (n < 1 || n >= cm::kWave) {
+    if (!block_live(rows, b, n_tokens, n_pad)) return w;
+    w.r = row_of_block(rows, b);
+    w.start = rows.start[w.r];
+    w.len = rows.start[w.r + 1] - w.start;
+    w.pstart = rows.pstart[w.r];
+    w.live = true;
+    return w;
+  }
+  const int pend = __builtin_amdgcn_readlane(psv, n);
+  if (__builtin_amdgcn_readlane(stv, n) != n_tokens || pend > n_pad || b * kBlk >= pend)
+    return w;
+  const int r = __popcll(__ballot(lane >= 1 && lane < n && psv / kBlk <= b));
+  const int s0 = __builtin_amdgcn_readlane(stv, r), s1 = __builtin_amdgcn_readlane(stv, r + 1);
+  const int p0 = __builtin_amdgcn_readlane(psv, r), p1 = __builtin_amdgcn_readlane(psv, r + 1);
+  w.len = s1 - s0;
+  w.live = w.len >= 0 && s0 >= 0 && w.len <= p1 - p0 && p0 % kBlk == 0 && s1 <= n_tokens;
+  w.r = r;
+  w.start = s0;
+  w.pstart = p0;
+  return w;
+}
+
 // Grids of the forward and backward kernels: (heads, padded blocks), heads the fast dimension,
 // so that the blocks of one position are dispatched together. A query block's work grows with
 // its index in its row (it sees every key block before it), so the query kernels take the
@@ -242,7 +284,8 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
                                                             int n_tokens, int n_pad) {
   __shared__ _Float16 tile[kD * kBlk];  // transposed staging [d][slot]
   const Rows& rows = *rows_p;
-  if (!block_live(rows, blockIdx.x, n_tokens, n_pad)) return;
+  const Where where = locate(rows, blockIdx.x, n_tokens, n_pad);
+  if (!where.live) return;
   const int y = blockIdx.y;
   // the job of this blockIdx.y, selected with static indices only
   Job job = jobs.job[0];
@@ -256,9 +299,8 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
   }
   const int h = y - first;
   const int b = blockIdx.x;
-  const int r = row_of_block(rows, b);
-  const int len = rows.start[r + 1] - rows.start[r];
-  const int local0 = (b - rows.pstart[r] / kBlk) * kBlk;
+  const int len = where.len;
+  const int local0 = (b - where.pstart / kBlk) * kBlk;
   const int pos0 = b * kBlk;
   // A thread takes chunks c = threadIdx.x + 256 i (token c / 16, 8 values of d at 8 (c % 16)).
   // All of its loads are issued before any store (the jobs' pointers carry no aliasing
@@ -275,7 +317,7 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
     const int t = c / (kD / 8), ch = c % (kD / 8);
     const int local = local0 + t;
     const bool ok = local < len;
-    const int64_t tok = rows.start[r] + local;
+    const int64_t tok = where.start + local;
     if (ok) {
       load8f(job.src, job.dtype, h * job.sh + tok * job.st + ch * 8, xv[it]);
     } else {
@@ -283,7 +325,7 @@ __global__ __launch_bounds__(256) void attn_relayout_kernel(Jobs jobs, const Row
       for (int i = 0; i < 8; ++i) xv[it][i] = 0.0f;
     }
     if (rot) {
-      const int64_t ct = ok ? tok : rows.start[r];  // pads: any row of the batch's tables
+      const int64_t ct = ok ? tok : where.start;  // pads: any row of the batch's tables
       const float* cr = job.rope.cos + ct * job.rope.cs_t + ch * 8;
       const float* sr = job.rope.sin + ct * job.rope.cs_t + ch * 8;
 #pragma unroll
@@ -370,11 +412,11 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   const Rows& rows = *rows_p;
   const int h = blockIdx.x, g = h / hpg;
   const int b = heavy_first_query_block();
-  if (!block_live(rows, b, n_tokens, n_pad)) return;
-  const int r = row_of_block(rows, b);
-  const int qb = b - rows.pstart[r] / kBlk;
-  const int len = rows.start[r + 1] - rows.start[r];
-  const int p0 = rows.pstart[r];
+  const Where where = locate(rows, b, n_tokens, n_pad);
+  if (!where.live) return;
+  const int qb = b - where.pstart / kBlk;
+  const int len = where.len;
+  const int p0 = where.pstart;
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
   const int pair = wave >> 1, wq = wave & 1;
@@ -394,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   half8 qf[kD / 16];
   {
     // q as given (token rows), or its rotated fp16 copy in the padded positions (fused RoPE)
-    const int64_t at = q_padded ? p0 + (q_ok ? ql : 0) : rows.start[r] + (q_ok ? ql : 0);
+    const int64_t at = q_padded ? p0 + (q_ok ? ql : 0) : where.start + (q_ok ? ql : 0);
     const int64_t off = h * sq_h + at * sq_t;
 #pragma unroll
     for (int ds = 0; ds < kD / 16; ++ds)
@@ -490,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   if (hh == 0) lse2[static_cast<int64_t>(h) * n_pad + p0 + ql] = mt + __log2f(l);
   if (!q_ok) return;
   const float inv = 1.0f / l;
-  _Float16* orow = out + (static_cast<int64_t>(rows.start[r] + ql) * H + h) * kD;
+  _Float16* orow = out + (static_cast<int64_t>(where.start + ql) * H + h) * kD;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -554,11 +596,11 @@ __device__ __forceinline__ void bwd_dkdv_block(const BwdArgs& a, int h, int b, u
   const float c_log2 = a.c_log2, scale = a.scale;
   const Rows& rows = *a.rows;
   const int g = h / a.hpg;
-  if (!block_live(rows, b, a.n_tokens, n_pad)) return;
-  const int r = row_of_block(rows, b);
-  const int kb = b - rows.pstart[r] / kBlk;
-  const int len = rows.start[r + 1] - rows.start[r];
-  const int p0 = rows.pstart[r];
+  const Where where = locate(rows, b, a.n_tokens, n_pad);
+  if (!where.live) return;
+  const int kb = b - where.pstart / kBlk;
+  const int len = where.len;
+  const int p0 = where.pstart;
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
   const int pair = wave >> 1, wq = wave & 1;
@@ -707,11 +749,11 @@ __device__ __forceinline__ void bwd_dq_block(const BwdArgs& a, int h, int b, uin
   OT* __restrict__ dq = static_cast<OT*>(a.dq);
   const Rows& rows = *a.rows;
   const int g = h / a.hpg;
-  if (!block_live(rows, b, n_tokens, n_pad)) return;
-  const int r = row_of_block(rows, b);
-  const int qb = b - rows.pstart[r] / kBlk;
-  const int len = rows.start[r + 1] - rows.start[r];
-  const int p0 = rows.pstart[r];
+  const Where where = locate(rows, b, n_tokens, n_pad);
+  if (!where.live) return;
+  const int qb = b - where.pstart / kBlk;
+  const int len = where.len;
+  const int p0 = where.pstart;
   const int lane = threadIdx.x % cm::kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / cm::kWave);
   const int pair = wave >> 1, wq = wave & 1;
@@ -784,7 +826,7 @@ __device__ __forceinline__ void bwd_dq_block(const BwdArgs& a, int h, int b, uin
   cm::gemm::lds_barrier();
   if (pair == 1 || ql >= len) return;
   // dq is [H][N][D], or [N][H][D] with tok_major
-  const int64_t tok = rows.start[r] + ql;
+  const int64_t tok = where.start + ql;
   if (dq_rot != nullptr) {
     // fused RoPE: the gradient of the rotated q, [H][n_pad][D] fp32, which the reduce launch
     // takes back through the transposed rotation (reading the cos / sin rows coalesced there)
@@ -867,11 +909,12 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(
   const Rows& rows = *rows_p;
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int pos = i / (kD / 4), d = (i % (kD / 4)) * 4;
-  if (pos >= n_pad || !block_live(rows, pos / kBlk, n_tokens, n_pad)) return;
-  const int r = row_of_block(rows, pos / kBlk);
-  const int local = pos - rows.pstart[r];
-  if (local >= rows.start[r + 1] - rows.start[r]) return;
-  const int64_t tok = rows.start[r] + local;
+  // a workgroup's 8 positions share one 64-position block (blockIdx.x * 8 .. + 7)
+  const Where where = locate(rows, __builtin_amdgcn_readfirstlane(pos / kBlk), n_tokens, n_pad);
+  if (pos >= n_pad || !where.live) return;
+  const int local = pos - where.pstart;
+  if (local >= where.len) return;
+  const int64_t tok = where.start + local;
   const int G = static_cast<int>(gridDim.y) - (dqr.rot != nullptr ? dqr.H : 0);
   if (static_cast<int>(blockIdx.y) >= G) {  // query head blockIdx.y - G of a fused RoPE
     const int h = blockIdx.y - G;
