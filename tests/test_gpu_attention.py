@@ -97,6 +97,10 @@ LENGTHS = [
     [63, 64, 65, 128, 129],
     [2048],
     [int(x) for x in torch.randint(1, 40, (100,), generator=torch.Generator().manual_seed(3))],
+    # the kernels locate a block's row with one lane per row below 64 rows, by walking the table
+    # from 64 on: both sides of that edge
+    [int(x) for x in torch.randint(1, 20, (63,), generator=torch.Generator().manual_seed(4))],
+    [int(x) for x in torch.randint(1, 20, (64,), generator=torch.Generator().manual_seed(5))],
 ]
 
 
