@@ -2,10 +2,12 @@
 tests_local/test_swiglu_recompute.py:194-268: the patched MLP against the original, output and
 every gradient; frozen projections keep only the MLP input for the backward).
 
-MLPInputRecompute's backward recomputes gate/up and the input gradient by one of four routes
-(claudemaxing_amd/swiglu_recompute.py): the NF4-fused GEMM (small products), the transposed
-NF4 expansion (fp16, large products), the natural NF4 expansion (other dtypes or widths), and
-autograd re-running the projections (any other layer). Each route is forced by its natural
+MLPInputRecompute's backward recomputes gate/up and the input gradient by one of five routes
+(claudemaxing_amd/swiglu_recompute.py): the NF4-fused GEMM (small products), the merged [2F, K]
+weight (large products with an fp32 input gradient: one product each way, the row-strided
+SwiGLU kernels on its halves, a k-major split-K input gradient), the transposed NF4 expansion
+(fp16 input gradient), the natural NF4 expansion (other dtypes or widths), and autograd
+re-running the projections (any other layer). Each route is forced by its natural
 condition, checked to be the one taken, and its output and input gradient are compared with
 
   * an fp32 evaluation of the same layers (the NF4 weights expanded by the CPU oracle, fp32
