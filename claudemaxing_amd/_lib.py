@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libclaudemaxing_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -100,6 +100,9 @@ SIGNATURES = {
     "cm_attn_rows_image": (_L, [_P, _I, _P]),
     "cm_lora_fused_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _F, _F, _P]),
     "cm_lora_fused_bwd1": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
+    "cm_lora_fused_fwd_multi": (_I, [_P, _L, _I, _I, _F, _F, _I, _PP, _PP, _PP, _PP, _PP, _PP,
+                                     _PP, _P, _P]),
+    "cm_lora_fused_bwd1_multi": (_I, [_L, _I, _F, _I, _PP, _PP, _PP, _PP, _PP, _P, _P]),
     "cm_lora_fused_bwd2": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _F, _P]),
     "cm_attn_workspace_bytes": (_L, [_L, _I, _I, _I, _I]),
     "cm_nf4_linear_fwd": (_I, [_P, _L, _L, _PW, _I, _PP, _PP, _PL, _I, _P, _L, _P]),

@@ -100,12 +100,37 @@ __device__ __forceinline__ int wave_index() {
 // fp16(B)[tile] . a^T, tile j on wavefront j % 8; lane l gets row l % 16 and the 4 consecutive
 // outputs 16 j + 4 (l / 16) .. +3 (base read 8 bytes, out written 16 bytes at a time).
 // SK and SN bound the steps and tiles per wavefront.
+// One adapter's operands; a launch takes up to kMaxJobs adapters on the same input x (the q and v
+// adapters of an attention block), adapter blockIdx.y, so that their independent row tiles run
+// side by side instead of one launch after the other.
+constexpr int kMaxJobs = 4;
+struct FwdJob {
+  const uint8_t* keep;
+  const float* A;
+  const float* B;
+  const _Float16* base;
+  float* out;
+  uint8_t* bits;
+  _Float16* a16;
+  int N;
+};
+struct FwdJobs {
+  FwdJob j[kMaxJobs];
+};
+
 template <int SK, int SN>
 __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ keep, const float* __restrict__ A,
-    const float* __restrict__ B, const _Float16* __restrict__ base, float* __restrict__ out,
-    uint8_t* __restrict__ bits, _Float16* __restrict__ a16, int T, int K, int N, int rows,
-    float scale_p, float scaling) {
+    const float* __restrict__ x, FwdJobs jobs, int T, int K, int rows, float scale_p,
+    float scaling) {
+  const FwdJob jb = jobs.j[blockIdx.y];
+  const uint8_t* __restrict__ keep = jb.keep;
+  const float* __restrict__ A = jb.A;
+  const float* __restrict__ B = jb.B;
+  const _Float16* __restrict__ base = jb.base;
+  float* __restrict__ out = jb.out;
+  uint8_t* __restrict__ bits = jb.bits;
+  _Float16* __restrict__ a16 = jb.a16;
+  const int N = jb.N;
   __shared__ acc4 red[kWaves][cm::kWave];
   const int lane = threadIdx.x % cm::kWave, wave = wave_index();
   const int r16 = lane % 16, grp = lane / 16;
@@ -213,11 +238,28 @@ __global__ __launch_bounds__(kThreads) void lora_fused_fwd_kernel(
 // lane l brings row l % 16's gradient at outputs 32 s + 4 g .. +3 and 32 s + 16 + 4 g .. +3
 // (writing gbase and g there) and fp16(B)[those 8 outputs][rank l % 16]. SN bounds the steps per
 // wavefront.
+struct Bwd1Job {
+  const float* grad;
+  const float* B;
+  _Float16* gbase;
+  _Float16* g16;
+  _Float16* ga16;
+  int N;
+};
+struct Bwd1Jobs {
+  Bwd1Job j[kMaxJobs];
+};
+
 template <int SN>
-__global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(
-    const float* __restrict__ grad, const float* __restrict__ B, _Float16* __restrict__ gbase,
-    _Float16* __restrict__ g16, _Float16* __restrict__ ga16, int T, int N, int rows,
-    float scaling) {
+__global__ __launch_bounds__(kThreads) void lora_fused_bwd1_kernel(Bwd1Jobs jobs, int T,
+                                                                   int rows, float scaling) {
+  const Bwd1Job jb = jobs.j[blockIdx.y];
+  const float* __restrict__ grad = jb.grad;
+  const float* __restrict__ B = jb.B;
+  _Float16* __restrict__ gbase = jb.gbase;
+  _Float16* __restrict__ g16 = jb.g16;
+  _Float16* __restrict__ ga16 = jb.ga16;
+  const int N = jb.N;
   __shared__ acc4 red[kWaves][cm::kWave];
   const int lane = threadIdx.x % cm::kWave, wave = wave_index();
   const int r16 = lane % 16, grp = lane / 16;
@@ -421,6 +463,51 @@ dim3 tile_grid(int64_t T, int rows) { return dim3(static_cast<unsigned>((T + row
     default: { constexpr int J = 16; __VA_ARGS__; break; } \
   }
 
+namespace {
+
+// The checks of one adapter of cm_lora_fused_fwd / _fwd_multi.
+bool fwd_job_ok(const float* x, const uint8_t* keep, const float* weight_a, const float* weight_b,
+                const void* base16, const float* out, const uint8_t* bits, const void* a16,
+                int K, int N) {
+  return N > 0 && N % 8 == 0 && N <= kMaxN && x && keep && weight_a && weight_b && base16 &&
+         out && bits && a16 && aligned(x, 16) && aligned(keep, 8) && aligned(weight_a, 16) &&
+         aligned(weight_b, 16) && aligned(base16, 8) && aligned(out, 16) && aligned(a16, 8) &&
+         K % 8 == 0;
+}
+
+int launch_fwd(const float* x, const FwdJobs& jobs, int n_jobs, int max_n, int64_t T, int K,
+               float scale_p, float scaling, hipStream_t s) {
+  const int rows = tile_rows(T);
+  dim3 grid = tile_grid(T, rows);
+  grid.y = n_jobs;
+  CM_LORA_SK_SWITCH(steps_bound(K), SK, CM_LORA_SN_SWITCH(tiles_bound(max_n), SN, {
+    hipLaunchKernelGGL((lora_fused_fwd_kernel<SK, SN>), grid, dim3(kThreads), 0, s, x, jobs,
+                       static_cast<int>(T), K, rows, scale_p, scaling);
+  }));
+  return cm::launch_status();
+}
+
+bool bwd1_job_ok(const float* grad, const float* weight_b, const void* gbase16, const void* g16,
+                 const void* ga16, int N) {
+  return N > 0 && N % 8 == 0 && N <= kMaxN && grad && weight_b && gbase16 && g16 && ga16 &&
+         aligned(grad, 16) && aligned(weight_b, 4) && aligned(gbase16, 8) && aligned(g16, 8) &&
+         aligned(ga16, 2);
+}
+
+int launch_bwd1(const Bwd1Jobs& jobs, int n_jobs, int max_n, int64_t T, float scaling,
+                hipStream_t s) {
+  const int rows = tile_rows(T);
+  dim3 grid = tile_grid(T, rows);
+  grid.y = n_jobs;
+  CM_LORA_SK_SWITCH(steps_bound(max_n), SN, {
+    hipLaunchKernelGGL(lora_fused_bwd1_kernel<SN>, grid, dim3(kThreads), 0, s, jobs,
+                       static_cast<int>(T), rows, scaling);
+  });
+  return cm::launch_status();
+}
+
+}  // namespace
+
 extern "C" int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a,
                                  const float* weight_b, const void* base16, float* out,
                                  uint8_t* bits, void* a16, int64_t T, int K, int N, int rank,
@@ -429,18 +516,36 @@ extern "C" int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const floa
   CM_CHECK_ARG(K % 8 == 0 && N % 8 == 0 && K <= kMaxK && N <= kMaxN);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
-  CM_CHECK_ARG(x && keep && weight_a && weight_b && base16 && out && bits && a16);
-  CM_CHECK_ARG(aligned(x, 16) && aligned(keep, 8) && aligned(weight_a, 16) &&
-               aligned(weight_b, 16) && aligned(base16, 8) && aligned(out, 16) && aligned(a16, 8));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int rows = tile_rows(T);
-  CM_LORA_SK_SWITCH(steps_bound(K), SK, CM_LORA_SN_SWITCH(tiles_bound(N), SN, {
-    hipLaunchKernelGGL((lora_fused_fwd_kernel<SK, SN>), tile_grid(T, rows), dim3(kThreads), 0, s,
-                       x, keep, weight_a, weight_b, static_cast<const _Float16*>(base16), out,
-                       bits, static_cast<_Float16*>(a16), static_cast<int>(T), K, N, rows, scale_p,
-                       scaling);
-  }));
-  return cm::launch_status();
+  CM_CHECK_ARG(fwd_job_ok(x, keep, weight_a, weight_b, base16, out, bits, a16, K, N));
+  FwdJobs jobs{};
+  jobs.j[0] = FwdJob{keep, weight_a, weight_b, static_cast<const _Float16*>(base16), out, bits,
+                     static_cast<_Float16*>(a16), N};
+  return launch_fwd(x, jobs, 1, N, T, K, scale_p, scaling, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cm_lora_fused_fwd_multi(const float* x, int64_t T, int K, int rank, float scale_p,
+                                       float scaling, int n_jobs, const uint8_t* const* keep,
+                                       const float* const* weight_a,
+                                       const float* const* weight_b, const void* const* base16,
+                                       float* const* out, uint8_t* const* bits,
+                                       void* const* a16, const int* N, void* stream) {
+  CM_CHECK_ARG(rank == kR && T >= 0 && K > 0 && K % 8 == 0 && K <= kMaxK);
+  CM_CHECK_ARG(n_jobs >= 1 && n_jobs <= kMaxJobs);
+  CM_CHECK_ARG(keep && weight_a && weight_b && base16 && out && bits && a16 && N);
+  if (T == 0) return 0;
+  CM_CHECK_ARG(T <= 0x7fffffff / 2);
+  FwdJobs jobs{};
+  int max_n = 0;
+  for (int i = 0; i < n_jobs; ++i) {
+    CM_CHECK_ARG(fwd_job_ok(x, keep[i], weight_a[i], weight_b[i], base16[i], out[i], bits[i],
+                            a16[i], K, N[i]));
+    jobs.j[i] = FwdJob{keep[i], weight_a[i], weight_b[i],
+                       static_cast<const _Float16*>(base16[i]), out[i], bits[i],
+                       static_cast<_Float16*>(a16[i]), N[i]};
+    max_n = std::max(max_n, N[i]);
+  }
+  return launch_fwd(x, jobs, n_jobs, max_n, T, K, scale_p, scaling,
+                    static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16,
@@ -449,17 +554,30 @@ extern "C" int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void
   CM_CHECK_ARG(rank == kR && T >= 0 && N > 0 && N % 8 == 0 && N <= kMaxN);
   if (T == 0) return 0;
   CM_CHECK_ARG(T <= 0x7fffffff / 2);
-  CM_CHECK_ARG(grad && weight_b && gbase16 && g16 && ga16);
-  CM_CHECK_ARG(aligned(grad, 16) && aligned(weight_b, 4) && aligned(gbase16, 8) &&
-               aligned(g16, 8) && aligned(ga16, 2));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int rows = tile_rows(T);
-  CM_LORA_SK_SWITCH(steps_bound(N), SN, {
-    hipLaunchKernelGGL(lora_fused_bwd1_kernel<SN>, tile_grid(T, rows), dim3(kThreads), 0, s, grad,
-                       weight_b, static_cast<_Float16*>(gbase16), static_cast<_Float16*>(g16),
-                       static_cast<_Float16*>(ga16), static_cast<int>(T), N, rows, scaling);
-  });
-  return cm::launch_status();
+  CM_CHECK_ARG(bwd1_job_ok(grad, weight_b, gbase16, g16, ga16, N));
+  Bwd1Jobs jobs{};
+  jobs.j[0] = Bwd1Job{grad, weight_b, static_cast<_Float16*>(gbase16),
+                      static_cast<_Float16*>(g16), static_cast<_Float16*>(ga16), N};
+  return launch_bwd1(jobs, 1, N, T, scaling, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cm_lora_fused_bwd1_multi(int64_t T, int rank, float scaling, int n_jobs,
+                                        const float* const* grad, const float* const* weight_b,
+                                        void* const* gbase16, void* const* g16,
+                                        void* const* ga16, const int* N, void* stream) {
+  CM_CHECK_ARG(rank == kR && T >= 0 && n_jobs >= 1 && n_jobs <= kMaxJobs);
+  CM_CHECK_ARG(grad && weight_b && gbase16 && g16 && ga16 && N);
+  if (T == 0) return 0;
+  CM_CHECK_ARG(T <= 0x7fffffff / 2);
+  Bwd1Jobs jobs{};
+  int max_n = 0;
+  for (int i = 0; i < n_jobs; ++i) {
+    CM_CHECK_ARG(bwd1_job_ok(grad[i], weight_b[i], gbase16[i], g16[i], ga16[i], N[i]));
+    jobs.j[i] = Bwd1Job{grad[i], weight_b[i], static_cast<_Float16*>(gbase16[i]),
+                        static_cast<_Float16*>(g16[i]), static_cast<_Float16*>(ga16[i]), N[i]};
+    max_n = std::max(max_n, N[i]);
+  }
+  return launch_bwd1(jobs, n_jobs, max_n, T, scaling, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cm_lora_fused_bwd2(const void* dxb16, const void* ga16, const float* weight_a,

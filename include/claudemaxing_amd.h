@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define CM_ABI_VERSION 8
+#define CM_ABI_VERSION 9
 
 /* Element types of tensor arguments. */
 typedef enum {
@@ -442,6 +442,22 @@ int cm_lora_fused_fwd(const float* x, const uint8_t* keep, const float* weight_a
  */
 int cm_lora_fused_bwd1(const float* grad, const float* weight_b, void* gbase16, void* g16,
                        void* ga16, int64_t T, int N, int rank, float scaling, void* stream);
+
+/* The two calls above for up to 4 adapters on the same input x (and of one rank, dropout
+ * scale and scaling) in one launch each: adapter i's operands are element i of the arrays, its
+ * output width N[i]. The same values as one call per adapter; the adapters' row tiles run side
+ * by side. Replaces the per-adapter launches of solution/lora.py:78-186 for the q and v adapters
+ * of an attention block (LoRABranch there runs once per adapter layer).
+ */
+int cm_lora_fused_fwd_multi(const float* x, int64_t T, int K, int rank, float scale_p,
+                            float scaling, int n_jobs, const uint8_t* const* keep,
+                            const float* const* weight_a, const float* const* weight_b,
+                            const void* const* base16, float* const* out, uint8_t* const* bits,
+                            void* const* a16, const int* N, void* stream);
+int cm_lora_fused_bwd1_multi(int64_t T, int rank, float scaling, int n_jobs,
+                             const float* const* grad, const float* const* weight_b,
+                             void* const* gbase16, void* const* g16, void* const* ga16,
+                             const int* N, void* stream);
 
 /* Backward, part 2, after the caller's base input gradient dxb16 = gbase16 @ W (fp16 [T, K]):
  *   gxd = fp16(sum_r ga16[t][r] * fp16(weight_a[r][k]))

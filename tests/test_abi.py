@@ -77,6 +77,11 @@ def test_argument_checks_run_on_the_host(lib):
     assert lib.cm_swiglu_bwd_rows(0x1000, 1, 8, 0x2000, 1, 0x3000, 1, 32, 0x2000, 0x3000, 4, 16,
                                   1, 1, 1, None) == INVALID  # dy rows narrower than cols
     assert lib.cm_swiglu_fwd_rows(None, 1, None, 1, 32, None, 1, 16, 0, 16, 1, None) == 0
+    # several LoRA adapters per launch: 1 to 4 of them
+    assert lib.cm_lora_fused_fwd_multi(None, 4, 1536, 16, 1.05, 2.0, 5, None, None, None, None,
+                                       None, None, None, None, None) == INVALID
+    assert lib.cm_lora_fused_bwd1_multi(4, 16, 2.0, 0, None, None, None, None, None, None,
+                                        None) == INVALID
     # grouped NF4 expansion: at most 8 weights; none is a no-op
     assert lib.cm_nf4_dequant_group(None, 9, None, 1, None) == INVALID
     assert lib.cm_nf4_dequant_group(None, 0, None, 1, None) == 0

@@ -162,3 +162,70 @@ def test_weight_grads_batch_no_tokens(dev):
     xd = torch.empty(0, 1536, device=dev, dtype=torch.float16)
     out = _weight_grads([(ga, xd)])
     assert out is not None and torch.count_nonzero(out[0]) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [1276, 37])
+def test_multi_adapter_launches_equal_single_ones(dev, t):
+    """cm_lora_fused_fwd_multi / cm_lora_fused_bwd1_multi over the q and v adapters of a block
+    (widths 1536 and 256, their own masks): every output bit-identical to one call per
+    adapter."""
+    import ctypes
+
+    from claudemaxing_amd import _lib
+
+    banner(f"lora fused multi-adapter launches t={t}")
+    k = 1536
+    g = torch.Generator(device=dev).manual_seed(t)
+    x = torch.randn(t, k, generator=g, device=dev)
+    st = _lib.stream(dev)
+    P = ctypes.c_void_p
+    ads = []
+    for n in (1536, 256):
+        ads.append(dict(
+            n=n, keep=torch.rand(t, k, generator=g, device=dev) > 0.05,
+            a=torch.randn(16, k, generator=g, device=dev) * 0.05,
+            b=torch.randn(n, 16, generator=g, device=dev) * 0.05,
+            base=torch.randn(t, n, generator=g, device=dev).half(),
+            grad=torch.randn(t, n, generator=g, device=dev)))
+
+    def outs_fwd():
+        return [dict(out=torch.empty(t, d["n"], device=dev),
+                     bits=torch.empty(t * k // 8, dtype=torch.uint8, device=dev),
+                     a16=torch.empty(t, 16, dtype=torch.float16, device=dev)) for d in ads]
+
+    single, multi = outs_fwd(), outs_fwd()
+    for d, o in zip(ads, single):
+        _lib.call("cm_lora_fused_fwd", x.data_ptr(), d["keep"].data_ptr(), d["a"].data_ptr(),
+                  d["b"].data_ptr(), d["base"].data_ptr(), o["out"].data_ptr(),
+                  o["bits"].data_ptr(), o["a16"].data_ptr(), t, k, d["n"], 16, 1 / 0.95, 2.0, st)
+
+    def arr(vals):
+        return (P * len(vals))(*vals)
+
+    _lib.call("cm_lora_fused_fwd_multi", x.data_ptr(), t, k, 16, 1 / 0.95, 2.0, 2,
+              arr([d["keep"].data_ptr() for d in ads]), arr([d["a"].data_ptr() for d in ads]),
+              arr([d["b"].data_ptr() for d in ads]), arr([d["base"].data_ptr() for d in ads]),
+              arr([o["out"].data_ptr() for o in multi]), arr([o["bits"].data_ptr() for o in multi]),
+              arr([o["a16"].data_ptr() for o in multi]), (ctypes.c_int * 2)(1536, 256), st)
+    for o1, o2 in zip(single, multi):
+        for key in o1:
+            assert torch.equal(o1[key], o2[key]), key
+
+    def outs_bwd():
+        return [dict(gbase=torch.empty(t, d["n"], dtype=torch.float16, device=dev),
+                     g16=torch.empty(t, d["n"], dtype=torch.float16, device=dev),
+                     ga16=torch.empty(t, 16, dtype=torch.float16, device=dev)) for d in ads]
+
+    single, multi = outs_bwd(), outs_bwd()
+    for d, o in zip(ads, single):
+        _lib.call("cm_lora_fused_bwd1", d["grad"].data_ptr(), d["b"].data_ptr(),
+                  o["gbase"].data_ptr(), o["g16"].data_ptr(), o["ga16"].data_ptr(), t, d["n"],
+                  16, 2.0, st)
+    _lib.call("cm_lora_fused_bwd1_multi", t, 16, 2.0, 2, arr([d["grad"].data_ptr() for d in ads]),
+              arr([d["b"].data_ptr() for d in ads]), arr([o["gbase"].data_ptr() for o in multi]),
+              arr([o["g16"].data_ptr() for o in multi]), arr([o["ga16"].data_ptr() for o in multi]),
+              (ctypes.c_int * 2)(1536, 256), st)
+    for o1, o2 in zip(single, multi):
+        for key in o1:
+            assert torch.equal(o1[key], o2[key]), key
