@@ -149,3 +149,29 @@ def test_row_kernels_read_the_halves_of_a_merged_product(dtype, rows, f, dev):
     assert_close(yb[:, :f], r_dg, tol, "dgate")
     assert_close(yb[:, f:], r_du, tol, "dup")
 
+
+
+@pytest.mark.parametrize("dtype", [F16, F32])
+def test_row_kernels_honour_a_padded_row_stride(dtype, dev):
+    """Rows of the merged product further apart than 2f (a padded buffer): the kernels read and
+    write the halves at the row stride, and the padding columns are left alone."""
+    from claudemaxing_amd import swiglu_recompute as SR
+
+    banner(f"swiglu rows with a padded stride {dtype}")
+    rows, f, pad = 300, 1000, 24
+    gen = torch.Generator().manual_seed(8)
+    full = (torch.randn(rows, 2 * f + pad, generator=gen) * 3).to(dtype).to(dev)
+    y = full[:, :2 * f]
+    grad = torch.randn(rows, f, generator=gen).to(dtype).to(dev)
+    gate, up = y[:, :f].contiguous(), y[:, f:].contiguous()
+    out = torch.empty(rows, f, dtype=dtype, device=dev)
+    SR._swiglu_fwd_rows(y, f, out, True)
+    flat = torch.empty_like(out)
+    SR._swiglu_fwd(gate, up, flat, True)
+    assert torch.equal(out, flat)
+    before = full[:, 2 * f:].clone()
+    SR._swiglu_bwd_rows(grad, y, f, True)
+    dg, du = torch.empty_like(gate), torch.empty_like(up)
+    SR._swiglu_bwd(grad, gate, up, dg, du, True)
+    assert torch.equal(y[:, :f], dg) and torch.equal(y[:, f:], du)
+    assert torch.equal(full[:, 2 * f:], before)
